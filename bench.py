@@ -1,0 +1,240 @@
+"""Benchmark of libflint's GEMM hot path on one MI355X.
+
+Default workload: BASELINE.json configs[1], the fused forward epilogues of a
+GPT-2 124M layer at 8,192 tokens -- MLP up 8192x3072x768 + bias + tanh-GELU,
+MLP down 8192x768x3072 + bias + residual, attention projection 8192x768x768
++ bias + residual -- FP16 operands, FP32 accumulation, through the C ABI.
+A step is one pass of the three GEMMs over one batch. `value` is whole-job
+TFLOPS (2mnk per GEMM over the step's wall time, inputs resident in HBM,
+buffer sets rotated past the 256 MB Infinity Cache).
+
+Also reported, in the same JSON line:
+  roofline      the dominant kernel's achieved TFLOP/s (algorithmic 2mnk over
+                its mean HIP-event duration on the launch stream) against
+                MI355X's dense FP16 MFMA peak (2,516.6 TFLOP/s);
+  cpu_baseline  PyTorch CPU FP32 of the same three ops on the host cores.
+
+--suite PATH also times every GEMM shape and reduction of the hot path and
+writes them to PATH as JSON (one object per kernel).
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "tests"))
+
+PEAK_FP16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk, dense
+PEAK_HBM_GBS = 8000.0
+METRIC = "GEMM TFLOPS & % of FP16 MFMA peak at GPT-2 124M shapes (8192 tok)"
+INFINITY_CACHE = 256 << 20
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--suite", type=str, default=None)
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+def fused_workload(torch, dev, seed=0):
+    """One buffer set of configs[1]."""
+    from inputs import normal, uniform
+
+    M, C = 8192, 768
+    s = {}
+    s["x_up"] = uniform((M, C), seed + 1).to(dev)
+    s["w_up"] = normal((4 * C, C), seed + 2, 0.02, torch.float16).to(dev)
+    s["b_up"] = normal((4 * C,), seed + 3, 0.02).to(dev)
+    s["y_up"] = torch.empty((M, 4 * C), dtype=torch.float16, device=dev)
+    s["pre_up"] = torch.empty((M, 4 * C), dtype=torch.float16, device=dev)
+    s["x_dn"] = uniform((M, 4 * C), seed + 4).to(dev)
+    s["w_dn"] = normal((C, 4 * C), seed + 5, 0.02, torch.float16).to(dev)
+    s["b_dn"] = normal((C,), seed + 6, 0.02).to(dev)
+    s["r_dn"] = normal((M, C), seed + 7).to(dev)
+    s["y_dn"] = torch.empty((M, C), dtype=torch.float32, device=dev)
+    s["x_pr"] = uniform((M, C), seed + 8).to(dev)
+    s["w_pr"] = normal((C, C), seed + 9, 0.02, torch.float16).to(dev)
+    s["b_pr"] = normal((C,), seed + 10, 0.02).to(dev)
+    s["r_pr"] = normal((M, C), seed + 11).to(dev)
+    s["y_pr"] = torch.empty((M, C), dtype=torch.float32, device=dev)
+    return s
+
+
+KERNELS = [
+    # name, m, n, k
+    ("gemm_nt_bias_gelu 8192x3072x768", 8192, 3072, 768),
+    ("gemm_nt_bias_residual 8192x768x3072", 8192, 768, 3072),
+    ("gemm_nt_bias_residual 8192x768x768", 8192, 768, 768),
+]
+
+
+def launch(f, s, i):
+    M, C = 8192, 768
+    if i == 0:
+        f.gemm_nt_bias_gelu(s["y_up"], s["pre_up"], s["x_up"], s["w_up"], s["b_up"], M, 4 * C, C)
+    elif i == 1:
+        f.gemm_nt_bias_residual(s["y_dn"], s["x_dn"], s["w_dn"], s["b_dn"], s["r_dn"], M, C,
+                                4 * C)
+    else:
+        f.gemm_nt_bias_residual(s["y_pr"], s["x_pr"], s["w_pr"], s["b_pr"], s["r_pr"], M, C, C)
+
+
+def set_bytes(s):
+    return sum(t.numel() * t.element_size() for t in s.values())
+
+
+def check(torch, s):
+    """Parity of the last step's outputs against PyTorch FP32 CPU on sampled rows."""
+    from inputs import rel_err
+
+    rows = torch.arange(0, 8192, 61)
+    cpu = {k: v[rows].cpu() if v.dim() == 2 and v.shape[0] == 8192 else v.cpu()
+           for k, v in s.items()}
+    up = cpu["x_up"].float() @ cpu["w_up"].float().T + cpu["b_up"]
+    gelu = torch.nn.functional.gelu(up.double(), approximate="tanh")
+    dn = cpu["r_dn"] + (cpu["x_dn"].float() @ cpu["w_dn"].float().T + cpu["b_dn"])
+    pr = cpu["r_pr"] + (cpu["x_pr"].float() @ cpu["w_pr"].float().T + cpu["b_pr"])
+    return max(rel_err(cpu["y_up"], gelu), rel_err(cpu["pre_up"], up), rel_err(cpu["y_dn"], dn),
+               rel_err(cpu["y_pr"], pr))
+
+
+def cpu_baseline(torch):
+    """PyTorch CPU FP32 of the same three ops on 1,024 of the 8,192 rows,
+    median of 3 after a warm-up, scaled to TFLOPS."""
+    from inputs import normal, uniform
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    M, C = 1024, 768
+    x_up = uniform((M, C), 1).float()
+    w_up = normal((4 * C, C), 2, 0.02).float()
+    b_up = normal((4 * C,), 3, 0.02)
+    x_dn = uniform((M, 4 * C), 4).float()
+    w_dn = normal((C, 4 * C), 5, 0.02).float()
+    b_dn = normal((C,), 6, 0.02)
+    r = normal((M, C), 7)
+    x_pr = uniform((M, C), 8).float()
+    w_pr = normal((C, C), 9, 0.02).float()
+
+    def step():
+        y = torch.nn.functional.gelu(torch.addmm(b_up, x_up, w_up.T), approximate="tanh")
+        z = r + torch.addmm(b_dn, x_dn, w_dn.T)
+        v = r + torch.addmm(b_dn, x_pr, w_pr.T)
+        return y, z, v
+
+    step()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    flops = sum(2 * M * n * k for _, _, n, k in KERNELS)
+    return {"value": round(flops / statistics.median(times) / 1e12, 4), "unit": "TFLOPS",
+            "cores": threads, "kind": "port",
+            "sample": "torch CPU fp32 addmm (+GELU / +residual) of the 3 configs[1] GEMMs on "
+                      "1,024 of 8,192 rows, median of 3"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); the multi-GPU path is "
+              "design-only for this build.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from flint_amd.flint_lib import Flint
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dev = torch.device("cuda:0")
+    f = Flint()
+    # Enough sets that the rotation exceeds the Infinity Cache.
+    sets = [fused_workload(torch, dev, 0)]
+    per_set = set_bytes(sets[0])
+    while len(sets) * per_set <= 2 * INFINITY_CACHE:
+        sets.append(fused_workload(torch, dev, 100 * len(sets)))
+    stream = torch.cuda.current_stream()
+
+    for i in range(args.warmup):
+        for k in range(3):
+            launch(f, sets[i % len(sets)], k)
+    torch.cuda.synchronize()
+
+    events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        s = sets[i % len(sets)]
+        for k in range(3):
+            a, b = events[i][k]
+            a.record(stream)
+            launch(f, s, k)
+            b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    flops = [2 * m * n * k for _, m, n, k in KERNELS]
+    step_flops = sum(flops)
+    ms = [statistics.mean(events[i][k][0].elapsed_time(events[i][k][1])
+                          for i in range(args.steps)) for k in range(3)]
+    kernels = {}
+    for (name, m, n, k), fl, t in zip(KERNELS, flops, ms):
+        tf = fl / (t * 1e-3) / 1e12
+        kernels[name] = {"ms": round(t, 5), "tflops": round(tf, 2),
+                         "frac_mfma": round(tf / PEAK_FP16_TFLOPS, 4)}
+    dom = max(range(3), key=lambda k: ms[k])
+    achieved = flops[dom] / (ms[dom] * 1e-3) / 1e12
+    ms_step = wall / args.steps * 1e3
+    value = step_flops / (wall / args.steps) / 1e12
+    err = check(torch, sets[(args.steps - 1) % len(sets)])
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded U[-1,1] activations, N(0,0.02) weights/bias, N(0,1) residual)",
+        "config": {"workload": "configs[1]: fused forward epilogues of a GPT-2 124M layer at "
+                               "8192 tokens (MLP up +bias+GELU, MLP down +bias+residual, attn "
+                               "proj +bias+residual)",
+                   "tokens": 8192, "width": 768, "parallelism": "none (1 GPU)"},
+        "frac_of_peak": round(value / PEAK_FP16_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                     "traffic": None, "kernel": KERNELS[dom][0]},
+        "kernels": kernels,
+        "parity_max_rel_err": err,
+        "rotation_sets": len(sets),
+        "rotation_bytes": len(sets) * per_set,
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(torch)
+    if args.suite:
+        from flint_amd import bench_suite
+
+        bench_suite.run(f, torch, dev, Path(args.suite))
+    print(json.dumps(out), flush=True)
+    if err > 2e-3:
+        print(f"parity failure: max rel err {err}", file=sys.stderr)
+        sys.exit(1)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,628 @@
+// The GEMM family on gfx950 matrix cores: FP16 operands, FP32 accumulation in
+// v_mfma_f32_32x32x16_f16, one rounding per output.
+//
+// Layouts (ref src/kernels/gemm.cu:1-12 for the semantics):
+//   NT  y(m x n) = x(m x k) w(n x k)^T     forward linear layer
+//   NN  y(m x n) = x(m x k) w(k x n)       input gradient
+//   TN  y(m x n) = x(k x m)^T w(k x n)     weight gradient, FP32 out, split-K
+//
+// Design (MI355X-first, not a translation of the reference's warp tiling):
+//  * A workgroup of 256 threads (4 wave64s) owns a BM x BN macro-tile and walks
+//    k in steps of 64. Both operands are staged in LDS as k-contiguous rows
+//    ([row][64] halves, 128 B per row), so the MFMA fragment of a lane is one
+//    ds_read_b128. 16-byte chunks are XOR-swizzled by (row ^ row>>3) & 7, which
+//    keeps any 8 (32-bank) or 16 (64-bank) consecutive lanes of a fragment read
+//    on distinct banks.
+//  * Operands whose rows run along k in HBM (NT's x and w, NN's x) are copied as
+//    16-byte chunks. Operands stored k-major (NN's w, both TN operands) are read
+//    as 8x8 blocks of halves (8 rows of 16 bytes), transposed in registers and
+//    written as 8 LDS rows, so the main loop is the same for every layout.
+//  * Two LDS stages: the next k-step's global loads are in flight while the
+//    current stage feeds the MFMAs; one barrier per k-step.
+//  * The MFMA's A operand is the w tile and its B operand the x tile, so a
+//    lane's 16 accumulators are 4 runs of 4 consecutive output columns of one
+//    output row: the epilogue does 8-byte (FP16) or 16-byte (FP32) vector
+//    stores and 16-byte bias / residual loads.
+//  * Tiles are numbered so that each of the 8 XCDs (which take workgroups
+//    round-robin) owns a contiguous, grouped block of tiles and reuses its
+//    operand rows from its own L2.
+//  * Epilogues (bias, bias+GELU writing pre and y, bias+residual into FP32,
+//    dGELU, scale) run on the FP32 accumulators before the single rounding.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "common/common.h"
+#include "kernels/kernels.h"
+
+namespace flint {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+constexpr int kBK = 64;               // k per main-loop step
+constexpr int kChunksK = kBK / 8;     // 16-byte chunks per LDS row
+
+enum class Layout { kNT, kNN, kTN };
+// What the kernel's store stage does. kTn writes FP32 (plain, accumulate or a
+// split's partial); kTnHalf is the batched TN's FP16 output.
+enum class Store { kNone, kBias, kBiasGelu, kBiasResidual, kDGelu, kScale, kTn, kTnHalf };
+
+__device__ __forceinline__ int swizzle(int row, int chunk) {
+    return chunk ^ ((row ^ (row >> 3)) & 7);
+}
+
+// GPT-2's tanh GELU. 0.5 s (1 + tanh u) equals s / (1 + exp(-2u)), which has
+// no cancellation for negative s; u = sqrt(2/pi) (s + 0.044715 s^3).
+__device__ __forceinline__ float gelu(float s) {
+    const float two_u = 1.5957691216057308f * s * __builtin_fmaf(0.044715f, s * s, 1.0f);
+    return s / (1.0f + expf(-two_u));
+}
+
+// d/ds [s sigma(2u)] = sigma + s sigma (1 - sigma) 2u', 2u' = 2 sqrt(2/pi)
+// (1 + 3 * 0.044715 s^2). 1 - sigma is taken as e sigma for s >= 0 (keeps
+// precision as sigma -> 1) and directly for s < 0 (e may overflow there).
+// Infinite s returns GELU's limits; NaN propagates.
+__device__ __forceinline__ float gelu_grad(float s) {
+    const float e = expf(-1.5957691216057308f * s * __builtin_fmaf(0.044715f, s * s, 1.0f));
+    const float sigma = 1.0f / (1.0f + e);
+    const float one_minus = s < 0.0f ? 1.0f - sigma : e * sigma;
+    const float q = s * one_minus * __builtin_fmaf(0.21406444860866706f, s * s, 1.5957691216057308f);
+    const float g = __builtin_fmaf(sigma, q, sigma);
+    return __builtin_isinf(s) ? (s > 0.0f ? 1.0f : 0.0f) : g;
+}
+
+struct TileArgs {
+    int tiles_m, tiles_n;     // macro-tiles per batch / split
+    int tiles_per_slice;      // tiles_m * tiles_n
+    int slices;               // batches, or k splits for TN
+    int group_m;              // grouped ordering width (in m tiles)
+    int split_len;            // TN: k per split (multiple of kBK)
+};
+
+// Maps the linear workgroup id to (slice, tile_m, tile_n). Workgroup b runs on
+// XCD b % 8; the remap gives XCD x the contiguous range of logical ids
+// [x * total/8, (x+1) * total/8) when total is a multiple of 8. Within a slice,
+// tiles go in groups of group_m rows of tiles, column by column.
+__device__ __forceinline__ bool map_tile(const TileArgs& t, int* slice, int* tm, int* tn) {
+    const unsigned total = unsigned(t.tiles_per_slice) * unsigned(t.slices);
+    unsigned bid = blockIdx.x + blockIdx.y * gridDim.x;
+    if (bid >= total) return false;
+    if ((total & 7u) == 0) bid = (bid & 7u) * (total >> 3) + (bid >> 3);
+    *slice = int(bid / unsigned(t.tiles_per_slice));
+    const int id = int(bid % unsigned(t.tiles_per_slice));
+    const int per_group = t.group_m * t.tiles_n;
+    const int group = id / per_group;
+    const int first_m = group * t.group_m;
+    const int rows = min(t.tiles_m - first_m, t.group_m);
+    const int in_group = id - group * per_group;
+    *tm = first_m + in_group % rows;
+    *tn = in_group / rows;
+    return true;
+}
+
+// Copies a ROWS x 64 tile of a k-contiguous matrix (row r at base + r*ld) into
+// LDS rows, 16-byte chunks.
+template <int ROWS, bool CHECK>
+struct DirectTile {
+    static constexpr int kChunks = ROWS * kChunksK;
+    static constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
+    f16x8 r[kPer];
+
+    __device__ __forceinline__ void load(const _Float16* __restrict__ base, size_t ld,
+                                         int rows_valid, int k_valid, int tid) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = tid + i * kThreads;
+            if (kChunks % kThreads != 0 && c >= kChunks) continue;
+            const int row = c / kChunksK;
+            const int kc = c % kChunksK;
+            const _Float16* p = base + size_t(row) * ld + kc * 8;
+            if (CHECK) {
+                r[i] = (row < rows_valid && kc * 8 < k_valid) ? *reinterpret_cast<const f16x8*>(p)
+                                                             : f16x8{};
+            } else {
+                r[i] = *reinterpret_cast<const f16x8*>(p);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(_Float16* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = tid + i * kThreads;
+            if (kChunks % kThreads != 0 && c >= kChunks) continue;
+            const int row = c / kChunksK;
+            const int kc = c % kChunksK;
+            *reinterpret_cast<f16x8*>(lds + row * kBK + swizzle(row, kc) * 8) = r[i];
+        }
+    }
+};
+
+// Copies the transpose of a 64 x ROWS tile of a matrix stored with k as its row
+// index (element (k, c) at base + k*ld + c) into ROWS LDS rows of 64 k values:
+// 8x8 blocks of halves are read as 8 rows of 16 bytes and transposed in
+// registers.
+template <int ROWS, bool CHECK>
+struct TransposedTile {
+    static constexpr int kColBlocks = ROWS / 8;
+    static constexpr int kBlocks = kColBlocks * kChunksK;
+    static constexpr int kPer = (kBlocks + kThreads - 1) / kThreads;
+    f16x8 r[kPer][8];
+
+    __device__ __forceinline__ void load(const _Float16* __restrict__ base, size_t ld,
+                                         int cols_valid, int k_valid, int tid) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int b = tid + i * kThreads;
+            if (kBlocks % kThreads != 0 && b >= kBlocks) continue;
+            const int cb = b % kColBlocks;
+            const int kb = b / kColBlocks;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int kr = kb * 8 + e;
+                const _Float16* p = base + size_t(kr) * ld + cb * 8;
+                if (CHECK) {
+                    r[i][e] = (kr < k_valid && cb * 8 < cols_valid)
+                                  ? *reinterpret_cast<const f16x8*>(p)
+                                  : f16x8{};
+                } else {
+                    r[i][e] = *reinterpret_cast<const f16x8*>(p);
+                }
+            }
+        }
+    }
+    __device__ __forceinline__ void store(_Float16* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int b = tid + i * kThreads;
+            if (kBlocks % kThreads != 0 && b >= kBlocks) continue;
+            const int cb = b % kColBlocks;
+            const int kb = b / kColBlocks;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                f16x8 o;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = r[i][e][j];
+                const int row = cb * 8 + j;
+                *reinterpret_cast<f16x8*>(lds + row * kBK + swizzle(row, kb) * 8) = o;
+            }
+        }
+    }
+};
+
+struct Operands {
+    void* y;
+    const _Float16* x;
+    const _Float16* w;
+    const float* bias;     // bias (n FP32)
+    void* aux;             // pre (GELU out / dGELU in) or residual
+    float* partials;       // TN split partials, or null
+    float scale;
+    int accumulate;        // TN: y += instead of y =
+    int m, n, k;
+};
+
+template <int BM, int BN, int WAVES_M, Layout L, Store S, bool CHECK>
+__global__ void __launch_bounds__(kThreads)
+gemm_kernel(Operands op, TileArgs ta) {
+    constexpr int WAVES_N = 4 / WAVES_M;
+    constexpr int WTM = BM / WAVES_M;   // wave tile rows (m)
+    constexpr int WTN = BN / WAVES_N;   // wave tile cols (n)
+    constexpr int FM = WTM / 32;
+    constexpr int FN = WTN / 32;
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tiles are whole 32x32 MFMA blocks");
+
+    using TileA = typename std::conditional<L == Layout::kTN, TransposedTile<BM, CHECK>,
+                                            DirectTile<BM, CHECK>>::type;
+    using TileB = typename std::conditional<L == Layout::kNT, DirectTile<BN, CHECK>,
+                                            TransposedTile<BN, CHECK>>::type;
+
+    __shared__ __attribute__((aligned(16))) _Float16 lds_a[2][BM * kBK];
+    __shared__ __attribute__((aligned(16))) _Float16 lds_b[2][BN * kBK];
+
+    int slice, tm, tn;
+    if (!map_tile(ta, &slice, &tm, &tn)) return;
+
+    const int tid = threadIdx.x;
+    const int m = op.m, n = op.n;
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+
+    // Slice: a batch (offset every operand) or a TN split of k.
+    const _Float16* x = op.x;
+    const _Float16* w = op.w;
+    int k_begin = 0, k_end = op.k;
+    size_t y_batch = 0;
+    if (S == Store::kTn && op.partials != nullptr) {
+        k_begin = slice * ta.split_len;
+        k_end = min(op.k, k_begin + ta.split_len);
+    } else if (ta.slices > 1) {
+        x += size_t(slice) * m * op.k;
+        w += size_t(slice) * n * op.k;
+        y_batch = size_t(slice) * m * n;
+    }
+
+    // Each operand's tile origin and how many rows / k values are in range.
+    const _Float16* a_ptr;
+    const _Float16* b_ptr;
+    size_t a_ld, b_ld;
+    size_t a_step, b_step;
+    if (L == Layout::kTN) {      // x is k x m
+        a_ptr = x + size_t(k_begin) * m + m0; a_ld = m; a_step = size_t(kBK) * m;
+    } else {                     // x is m x k
+        a_ptr = x + size_t(m0) * op.k + k_begin; a_ld = op.k; a_step = kBK;
+    }
+    if (L == Layout::kNT) {      // w is n x k
+        b_ptr = w + size_t(n0) * op.k + k_begin; b_ld = op.k; b_step = kBK;
+    } else {                     // w is k x n
+        b_ptr = w + size_t(k_begin) * n + n0; b_ld = n; b_step = size_t(kBK) * n;
+    }
+    const int a_rows_valid = m - m0;
+    const int b_rows_valid = n - n0;
+
+    TileA ta_regs;
+    TileB tb_regs;
+    const int k_len = k_end - k_begin;
+    const int steps = (k_len + kBK - 1) / kBK;
+
+    ta_regs.load(a_ptr, a_ld, a_rows_valid, k_len, tid);
+    tb_regs.load(b_ptr, b_ld, b_rows_valid, k_len, tid);
+    ta_regs.store(lds_a[0], tid);
+    tb_regs.store(lds_b[0], tid);
+    __syncthreads();
+
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WAVES_N;
+    const int wn = wave % WAVES_N;
+    const int frag_row = lane & 31;
+    const int frag_chunk = lane >> 5;
+
+    f32x16 acc[FN][FM];
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
+
+    for (int s = 0; s < steps; ++s) {
+        const int cur = s & 1;
+        const bool more = s + 1 < steps;
+        if (more) {
+            const int k_left = k_len - (s + 1) * kBK;
+            ta_regs.load(a_ptr + (s + 1) * a_step, a_ld, a_rows_valid, k_left, tid);
+            tb_regs.load(b_ptr + (s + 1) * b_step, b_ld, b_rows_valid, k_left, tid);
+        }
+        const _Float16* la = lds_a[cur];
+        const _Float16* lb = lds_b[cur];
+#pragma unroll
+        for (int kk = 0; kk < kBK / 16; ++kk) {
+            const int chunk = kk * 2 + frag_chunk;
+            f16x8 xa[FM];
+            f16x8 wb[FN];
+#pragma unroll
+            for (int j = 0; j < FM; ++j) {
+                const int row = wm * WTM + j * 32 + frag_row;
+                xa[j] = *reinterpret_cast<const f16x8*>(la + row * kBK + swizzle(row, chunk) * 8);
+            }
+#pragma unroll
+            for (int i = 0; i < FN; ++i) {
+                const int row = wn * WTN + i * 32 + frag_row;
+                wb[i] = *reinterpret_cast<const f16x8*>(lb + row * kBK + swizzle(row, chunk) * 8);
+            }
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wb[i], xa[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            ta_regs.store(lds_a[cur ^ 1], tid);
+            tb_regs.store(lds_b[cur ^ 1], tid);
+        }
+        __syncthreads();
+    }
+
+    // Store stage. Lane holds output row m0 + wm*WTM + j*32 + (lane & 31) and,
+    // for each group g, 4 consecutive columns n0 + wn*WTN + i*32 + 8g + 4*(lane>>5).
+    const int col_lane = (lane >> 5) * 4;
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+        const int row = m0 + wm * WTM + j * 32 + frag_row;
+        if (CHECK && row >= m) continue;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int col = n0 + wn * WTN + i * 32 + g * 8 + col_lane;
+                float v[4] = {acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2],
+                              acc[i][j][g * 4 + 3]};
+                const size_t at = y_batch + size_t(row) * n + col;
+                const bool whole = !CHECK || (col + 3 < n && (n & 3) == 0);
+                if (CHECK && col >= n) continue;
+                if (S == Store::kTn) {
+                    float* out = op.partials ? op.partials + size_t(slice) * m * n
+                                             : static_cast<float*>(op.y);
+                    const bool add = op.partials == nullptr && op.accumulate;
+                    if (whole) {
+                        f32x4* p = reinterpret_cast<f32x4*>(out + at);
+                        f32x4 r = {v[0], v[1], v[2], v[3]};
+                        if (add) r = *p + r;
+                        *p = r;
+                    } else {
+                        for (int q = 0; q < 4; ++q)
+                            if (col + q < n) out[at + q] = add ? out[at + q] + v[q] : v[q];
+                    }
+                    continue;
+                }
+                if (S == Store::kBias || S == Store::kBiasGelu || S == Store::kBiasResidual) {
+                    if (whole) {
+                        const f32x4 b = *reinterpret_cast<const f32x4*>(op.bias + col);
+                        v[0] += b[0]; v[1] += b[1]; v[2] += b[2]; v[3] += b[3];
+                    } else {
+                        for (int q = 0; q < 4; ++q) v[q] += col + q < n ? op.bias[col + q] : 0.0f;
+                    }
+                }
+                if (S == Store::kBiasResidual) {
+                    float* out = static_cast<float*>(op.y);
+                    const float* res = static_cast<const float*>(op.aux);
+                    if (whole) {
+                        const f32x4 r = *reinterpret_cast<const f32x4*>(res + at);
+                        f32x4 o = {r[0] + v[0], r[1] + v[1], r[2] + v[2], r[3] + v[3]};
+                        *reinterpret_cast<f32x4*>(out + at) = o;
+                    } else {
+                        for (int q = 0; q < 4; ++q)
+                            if (col + q < n) out[at + q] = res[at + q] + v[q];
+                    }
+                    continue;
+                }
+                if (S == Store::kScale) {
+                    for (int q = 0; q < 4; ++q) v[q] *= op.scale;
+                }
+                if (S == Store::kDGelu) {
+                    const _Float16* pre = static_cast<const _Float16*>(op.aux);
+                    if (whole) {
+                        const f16x4 p = *reinterpret_cast<const f16x4*>(pre + at);
+                        for (int q = 0; q < 4; ++q) v[q] *= gelu_grad(float(p[q]));
+                    } else {
+                        for (int q = 0; q < 4; ++q)
+                            if (col + q < n) v[q] *= gelu_grad(float(pre[at + q]));
+                    }
+                }
+                _Float16* out = static_cast<_Float16*>(op.y);
+                if (S == Store::kBiasGelu) {
+                    _Float16* pre = static_cast<_Float16*>(op.aux);
+                    if (whole) {
+                        f16x4 p = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
+                        *reinterpret_cast<f16x4*>(pre + at) = p;
+                    } else {
+                        for (int q = 0; q < 4; ++q)
+                            if (col + q < n) pre[at + q] = _Float16(v[q]);
+                    }
+                    for (int q = 0; q < 4; ++q) v[q] = gelu(v[q]);
+                }
+                if (whole) {
+                    f16x4 o = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
+                    *reinterpret_cast<f16x4*>(out + at) = o;
+                } else {
+                    for (int q = 0; q < 4; ++q)
+                        if (col + q < n) out[at + q] = _Float16(v[q]);
+                }
+            }
+        }
+    }
+}
+
+// Adds a split TN's partials in split order: y = old + (p0 + p1 + ...), or
+// y = p0 + p1 + ... (ref src/kernels/gemm.cu:678-703 for the order).
+__global__ void __launch_bounds__(256)
+tn_reduce(float* __restrict__ y, const float* __restrict__ partials, size_t quads, int splits,
+          int accumulate) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(partials);
+    f32x4* out = reinterpret_cast<f32x4*>(y);
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < quads;
+         i += size_t(gridDim.x) * blockDim.x) {
+        f32x4 sum = p[i];
+        for (int s = 1; s < splits; ++s) sum += p[size_t(s) * quads + i];
+        if (accumulate) sum = out[i] + sum;
+        out[i] = sum;
+    }
+}
+
+struct Config {
+    int bm, bn, waves_m;
+};
+
+// The macro-tile for an m x n output with `slices` independent slices,
+// minimising (whole waves of tiles over the CUs) x (tile cost), where a tile's
+// cost is its MFMA work over the tile shape's measured relative efficiency.
+Config pick_config(size_t m, size_t n, size_t slices, int cus) {
+    struct Cand { int bm, bn, wm; double eff; };
+    static const Cand cands[] = {
+        {256, 192, 2, 1.00}, {256, 128, 2, 0.95}, {128, 192, 2, 0.90},
+        {128, 128, 2, 0.80}, {128, 64, 4, 0.55}, {64, 128, 1, 0.55},
+    };
+    Config best{128, 128, 2};
+    double best_cost = 1e300;
+    for (const Cand& c : cands) {
+        if (c.bn > 64 && n <= 64) continue;
+        const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn) *
+                             double(slices);
+        const double waves = std::ceil(tiles / cus);
+        const double cost = waves * double(c.bm) * double(c.bn) / c.eff;
+        if (cost < best_cost * 0.999) {
+            best_cost = cost;
+            best = Config{c.bm, c.bn, c.wm};
+        }
+    }
+    return best;
+}
+
+template <Layout L, Store S, bool CHECK>
+hipError_t dispatch(const Config& c, dim3 grid, const Operands& op, const TileArgs& ta,
+                    hipStream_t stream) {
+#define FLINT_GEMM_CASE(BM_, BN_, WM_)                                                   \
+    if (c.bm == BM_ && c.bn == BN_ && c.waves_m == WM_) {                                \
+        hipLaunchKernelGGL((gemm_kernel<BM_, BN_, WM_, L, S, CHECK>), grid, dim3(kThreads), 0, \
+                           stream, op, ta);                                              \
+        return hipGetLastError();                                                        \
+    }
+    FLINT_GEMM_CASE(256, 192, 2)
+    FLINT_GEMM_CASE(256, 128, 2)
+    FLINT_GEMM_CASE(128, 192, 2)
+    FLINT_GEMM_CASE(128, 128, 2)
+    FLINT_GEMM_CASE(128, 64, 4)
+    FLINT_GEMM_CASE(64, 128, 1)
+#undef FLINT_GEMM_CASE
+    return hipErrorInvalidValue;
+}
+
+template <Layout L, Store S>
+hipError_t run(Operands op, size_t slices, int split_len, hipStream_t stream) {
+    int cus = 256;
+    if (hipError_t e = device_cus(&cus); e != hipSuccess) return e;
+    const bool split = S == Store::kTn && op.partials != nullptr;
+    // A TN split's tile shape is the one gemm_tn_splits planned with.
+    const Config c = pick_config(op.m, op.n, S == Store::kTn ? 1 : slices, cus);
+    TileArgs ta;
+    ta.tiles_m = (op.m + c.bm - 1) / c.bm;
+    ta.tiles_n = (op.n + c.bn - 1) / c.bn;
+    ta.tiles_per_slice = ta.tiles_m * ta.tiles_n;
+    ta.slices = int(slices);
+    ta.group_m = 8;
+    ta.split_len = split_len;
+    const size_t total = size_t(ta.tiles_per_slice) * slices;
+    const unsigned gx = unsigned(std::min<size_t>(total, size_t{1} << 20));
+    const unsigned gy = unsigned((total + gx - 1) / gx);
+    const dim3 grid(gx, gy);
+    // The unchecked kernel needs whole tiles and whole k-steps in every slice.
+    const int k_piece = split ? split_len : op.k;
+    const bool exact = op.m % c.bm == 0 && op.n % c.bn == 0 && k_piece % kBK == 0 &&
+                       op.k % kBK == 0;
+    return exact ? dispatch<L, S, false>(c, grid, op, ta, stream)
+                 : dispatch<L, S, true>(c, grid, op, ta, stream);
+}
+
+Operands make_ops(void* y, const void* x, const void* w, size_t m, size_t n, size_t k) {
+    Operands op{};
+    op.y = y;
+    op.x = static_cast<const _Float16*>(x);
+    op.w = static_cast<const _Float16*>(w);
+    op.m = int(m);
+    op.n = int(n);
+    op.k = int(k);
+    op.scale = 1.0f;
+    return op;
+}
+
+// TN's split of k. The count is the smallest that keeps at least 3/4 of the
+// CUs busy over all waves of tiles (or the fullest, up to 16 splits), each split
+// at least 1,024 long and a multiple of the 64-step; the last split takes the
+// rest. (Policy follows ref src/kernels/gemm.cu:737-784, with CUs for slots.)
+constexpr int kMinSplitK = 1024;
+constexpr int kMaxSplits = 16;
+
+}  // namespace
+
+hipError_t gemm_tn_splits(size_t m, size_t n, size_t k, int* splits, int* split_len) {
+    int cus = 256;
+    if (hipError_t e = device_cus(&cus); e != hipSuccess) return e;
+    const Config c = pick_config(m, n, 1, cus);
+    const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn);
+    const int most = std::min<int>(kMaxSplits, std::max<int>(1, int(k / kMinSplitK)));
+    int want = 1;
+    double best = 0;
+    for (int s = 1; s <= most; ++s) {
+        const double blocks = tiles * s;
+        const double waves = std::ceil(blocks / cus);
+        const double fill = blocks / (waves * cus);
+        if (fill > best) {
+            best = fill;
+            want = s;
+        }
+        if (fill >= 0.75) {
+            want = s;
+            break;
+        }
+    }
+    const size_t per = (k + want - 1) / want;
+    const size_t len = (per + kBK - 1) / kBK * kBK;
+    *split_len = int(len);
+    *splits = int((k + len - 1) / len);
+    return hipSuccess;
+}
+
+hipError_t gemm_tn_workspace(size_t m, size_t n, size_t k, size_t* bytes) {
+    int splits = 1, len = 0;
+    if (hipError_t e = gemm_tn_splits(m, n, k, &splits, &len); e != hipSuccess) return e;
+    *bytes = splits > 1 ? size_t(splits) * m * n * sizeof(float) : 0;
+    return hipSuccess;
+}
+
+hipError_t launch_gemm_nt(void* y, const void* x, const void* w, const void* bias, void* aux,
+                          Epilogue e, size_t m, size_t n, size_t k, hipStream_t stream) {
+    Operands op = make_ops(y, x, w, m, n, k);
+    op.bias = static_cast<const float*>(bias);
+    op.aux = aux;
+    switch (e) {
+    case Epilogue::kNone: return run<Layout::kNT, Store::kNone>(op, 1, 0, stream);
+    case Epilogue::kBias: return run<Layout::kNT, Store::kBias>(op, 1, 0, stream);
+    case Epilogue::kBiasGelu: return run<Layout::kNT, Store::kBiasGelu>(op, 1, 0, stream);
+    case Epilogue::kBiasResidual: return run<Layout::kNT, Store::kBiasResidual>(op, 1, 0, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gemm_nn(void* y, const void* x, const void* w, const void* aux, Epilogue e,
+                          size_t m, size_t n, size_t k, hipStream_t stream) {
+    Operands op = make_ops(y, x, w, m, n, k);
+    op.aux = const_cast<void*>(aux);
+    switch (e) {
+    case Epilogue::kNone: return run<Layout::kNN, Store::kNone>(op, 1, 0, stream);
+    case Epilogue::kDGelu: return run<Layout::kNN, Store::kDGelu>(op, 1, 0, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_t n, size_t k,
+                          bool accumulate, void* workspace, hipStream_t stream) {
+    int splits = 1, len = 0;
+    if (hipError_t e = gemm_tn_splits(m, n, k, &splits, &len); e != hipSuccess) return e;
+    Operands op = make_ops(y, x, w, m, n, k);
+    op.accumulate = accumulate ? 1 : 0;
+    op.partials = splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    if (hipError_t e = run<Layout::kTN, Store::kTn>(op, size_t(splits), len, stream);
+        e != hipSuccess || splits == 1) {
+        return e;
+    }
+    const size_t quads = m * n / 4;
+    const unsigned blocks = unsigned(std::clamp<size_t>((quads + 255) / 256, 1, 8192));
+    hipLaunchKernelGGL(tn_reduce, dim3(blocks), dim3(256), 0, stream, static_cast<float*>(y),
+                       op.partials, quads, splits, op.accumulate);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_nt_batched(void* y, const void* x, const void* w, size_t batches,
+                                  size_t m, size_t n, size_t k, float scale, hipStream_t stream) {
+    Operands op = make_ops(y, x, w, m, n, k);
+    op.scale = scale;
+    return run<Layout::kNT, Store::kScale>(op, batches, 0, stream);
+}
+
+hipError_t launch_gemm_nn_batched(void* y, const void* x, const void* w, size_t batches,
+                                  size_t m, size_t n, size_t k, hipStream_t stream) {
+    Operands op = make_ops(y, x, w, m, n, k);
+    return run<Layout::kNN, Store::kNone>(op, batches, 0, stream);
+}
+
+hipError_t launch_gemm_tn_batched(void* y, const void* x, const void* w, size_t batches,
+                                  size_t m, size_t n, size_t k, hipStream_t stream) {
+    Operands op = make_ops(y, x, w, m, n, k);
+    return run<Layout::kTN, Store::kTnHalf>(op, batches, 0, stream);
+}
+
+}  // namespace flint

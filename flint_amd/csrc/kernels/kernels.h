@@ -1,0 +1,102 @@
+// Launchers for the gfx950 kernels. The C-ABI layer (csrc/api) validates the
+// arguments, then calls exactly one of these; each queues its kernels on the
+// stream and returns the launch error, if any.
+#pragma once
+
+#include <cstddef>
+
+#include <hip/hip_runtime.h>
+
+namespace flint {
+
+// Size limits of the ABI (ref src/kernels/gemm.cuh:13-18, src/api/gemm.cpp:21).
+constexpr size_t kGemmMaxMN = size_t{65535} * 128;
+constexpr size_t kGemmMaxK = size_t{1} << 16;
+constexpr size_t kGemmBatchedMaxM = 1024;
+constexpr size_t kGemmMaxBatches = 65535;
+
+// GEMM epilogues (what happens to the FP32 sums before the single rounding).
+enum class Epilogue { kNone, kBias, kBiasGelu, kBiasResidual, kDGelu, kScale };
+
+hipError_t launch_gemm_nt(void* y, const void* x, const void* w, const void* bias,
+                          void* aux, Epilogue e, size_t m, size_t n, size_t k,
+                          hipStream_t stream);
+hipError_t launch_gemm_nn(void* y, const void* x, const void* w, const void* aux, Epilogue e,
+                          size_t m, size_t n, size_t k, hipStream_t stream);
+// Number of k splits TN uses for m x n x k on this device (1 = none).
+hipError_t gemm_tn_splits(size_t m, size_t n, size_t k, int* splits, int* split_len);
+hipError_t gemm_tn_workspace(size_t m, size_t n, size_t k, size_t* bytes);
+hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_t n, size_t k,
+                          bool accumulate, void* workspace, hipStream_t stream);
+hipError_t launch_gemm_nt_batched(void* y, const void* x, const void* w, size_t batches,
+                                  size_t m, size_t n, size_t k, float scale, hipStream_t stream);
+hipError_t launch_gemm_nn_batched(void* y, const void* x, const void* w, size_t batches,
+                                  size_t m, size_t n, size_t k, hipStream_t stream);
+hipError_t launch_gemm_tn_batched(void* y, const void* x, const void* w, size_t batches,
+                                  size_t m, size_t n, size_t k, hipStream_t stream);
+
+// Row reductions.
+constexpr size_t kLayerNormMaxCols = size_t{1} << 24;
+constexpr size_t kLayerNormMaxRows = size_t{0x7fffffff} * 8;
+constexpr size_t kBiasGradientChunkRows = 256;
+constexpr size_t kBiasGradientMaxCols = size_t{65535} * 256;
+constexpr size_t kBiasGradientMaxRows = size_t{0x7fffffff} * kBiasGradientChunkRows;
+constexpr size_t kSoftmaxMaxLength = 1024;
+constexpr size_t kSoftmaxMaxBatches = 65535;
+constexpr size_t kCrossEntropyMaxCols = size_t{1} << 16;
+constexpr size_t kCrossEntropyMaxRows = size_t{0x7fffffff} * 8;
+
+// Workspace of the bias gradient: an FP32 sum and its error per column per
+// started chunk of 256 rows (ref src/kernels/bias_gradient.cuh:25-27).
+constexpr size_t bias_gradient_workspace(size_t rows, size_t cols) {
+    return (rows + kBiasGradientChunkRows - 1) / kBiasGradientChunkRows * cols * 8;
+}
+
+hipError_t launch_layernorm_forward(void* y, void* mean, void* rstd, const void* x,
+                                    const void* gamma, const void* beta, size_t rows, size_t cols,
+                                    float eps, hipStream_t stream);
+hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const void* dy,
+                                     const void* x, const void* mean, const void* rstd,
+                                     const void* gamma, size_t rows, size_t cols,
+                                     bool accumulate_dx, bool accumulate_params, void* workspace,
+                                     hipStream_t stream);
+hipError_t launch_bias_gradient(void* dbias, const void* dy, size_t rows, size_t cols,
+                                bool accumulate, void* workspace, hipStream_t stream);
+// Merges per-chunk (sum, error) partials left in workspace into out (cols FP32).
+hipError_t launch_bias_gradient_finish(void* out, const void* workspace, size_t rows,
+                                       size_t cols, bool accumulate, hipStream_t stream);
+hipError_t launch_causal_softmax_forward(void* p, const void* s, size_t rows, size_t length,
+                                         hipStream_t stream);
+hipError_t launch_causal_softmax_backward(void* ds, const void* p, const void* dp, size_t rows,
+                                          size_t length, float scale, hipStream_t stream);
+hipError_t launch_softmax_cross_entropy(void* dlogits, void* row_loss, const void* logits,
+                                        const void* targets, float scale, size_t rows,
+                                        size_t vocab, size_t cols, hipStream_t stream);
+
+// Data movement.
+constexpr size_t kEmbeddingMaxWidth = size_t{1} << 24;
+constexpr size_t kEmbeddingMaxVocab = size_t{1} << 16;
+constexpr size_t kEmbeddingMaxRows = size_t{0x7fffffff} * 8;
+constexpr size_t kEmbeddingBackwardMaxWidth = kBiasGradientMaxCols;
+constexpr size_t kEmbeddingBackwardMaxRows = 0xffffffffu;
+constexpr size_t kEmbeddingBackwardMaxPositionValues = kBiasGradientMaxCols;
+constexpr size_t kHeadsMaxRowWidth = size_t{1} << 24;
+constexpr size_t kHeadsMaxRows = size_t{0x7fffffff} * 8;
+
+hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t stream);
+// Zeroes bytes at dst (16-byte aligned) with a kernel, not a memset node.
+hipError_t launch_fill_zero(void* dst, size_t bytes, hipStream_t stream);
+hipError_t launch_fp32_to_fp16(void* y, const void* x, size_t count, hipStream_t stream);
+hipError_t launch_heads(void* y, const void* x, size_t batches, size_t length, size_t heads,
+                        size_t head_width, size_t row_width, size_t first, bool merge,
+                        hipStream_t stream);
+hipError_t launch_embedding_forward(void* x, const void* tokens, const void* wte,
+                                    const void* wpe, size_t rows, size_t length, size_t width,
+                                    hipStream_t stream);
+size_t embedding_backward_workspace(size_t sequences, size_t length, size_t vocab, size_t width);
+hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, const void* tokens,
+                                     size_t sequences, size_t length, size_t vocab, size_t width,
+                                     bool accumulate_wte, bool accumulate_wpe, void* workspace,
+                                     hipStream_t stream);
+
+}  // namespace flint

@@ -1,0 +1,118 @@
+// Device helpers shared by the row-reduction kernels: compensated sums, wave64
+// reductions, 16-byte chunk (un)packing and an accurate exp built on
+// v_exp_f32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+// No implicit fused multiply-adds anywhere after this point: HIP's __fmul_rn /
+// __fadd_rn are plain operators, and a contracted a.sum + u*v would make the
+// TwoSum error terms inexact and change the shape-only summation orders.
+#pragma clang fp contract(off)
+
+namespace flint {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+
+// A rounded sum and the running sum of the rounding errors left in it
+// (Knuth's TwoSum per addition; Ogita-Rump-Oishi Sum2).
+struct Comp {
+    float sum = 0.0f;
+    float error = 0.0f;
+};
+
+// Single IEEE operations, written here (under contract(off)) rather than via
+// HIP's __f*_rn, whose bodies carry the header's contraction setting.
+__device__ __forceinline__ float add_rn(float a, float b) { return a + b; }
+__device__ __forceinline__ float sub_rn(float a, float b) { return a - b; }
+__device__ __forceinline__ float mul_rn(float a, float b) { return a * b; }
+
+__device__ __forceinline__ void comp_add(Comp& a, float v) {
+    const float t = add_rn(a.sum, v);
+    const float v_part = sub_rn(t, a.sum);
+    a.error = add_rn(a.error, add_rn(sub_rn(a.sum, sub_rn(t, v_part)), sub_rn(v, v_part)));
+    a.sum = t;
+}
+
+// Merges (b_sum, b_error) into a: both errors first, then b's sum by TwoSum.
+// Symmetric in a and b bit for bit, since TwoSum's error is exact.
+__device__ __forceinline__ void comp_merge(Comp& a, float b_sum, float b_error) {
+    const float errors = add_rn(a.error, b_error);
+    a.error = 0.0f;
+    comp_add(a, b_sum);
+    a.error = add_rn(a.error, errors);
+}
+
+// Adds d*d with the product's own rounding error (exact via fma).
+__device__ __forceinline__ void comp_add_square(Comp& a, float d) {
+    const float p = mul_rn(d, d);
+    a.error = add_rn(a.error, __builtin_fmaf(d, d, -p));
+    comp_add(a, p);
+}
+
+// Adds u*v with the product's rounding error.
+__device__ __forceinline__ void comp_add_product(Comp& a, float u, float v) {
+    const float p = mul_rn(u, v);
+    a.error = add_rn(a.error, __builtin_fmaf(u, v, -p));
+    comp_add(a, p);
+}
+
+// Butterfly over `width` lanes (a power of two up to 64) starting at xor
+// offset width/2. Every lane of the group ends with the same bits.
+template <int WIDTH>
+__device__ __forceinline__ Comp comp_reduce(Comp a) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off /= 2) {
+        const float s = __shfl_xor(a.sum, off, 64);
+        const float e = __shfl_xor(a.error, off, 64);
+        comp_merge(a, s, e);
+    }
+    return a;
+}
+
+template <int WIDTH>
+__device__ __forceinline__ float sum_reduce(float v) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off /= 2) v = add_rn(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int WIDTH>
+__device__ __forceinline__ float max_reduce(float v) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off /= 2) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// exp(x) to about 2 FP32 ulps: x log2(e) is formed as hi + lo with the
+// product's rounding error recovered by fma (log2(e) itself split in two
+// floats), then 2^hi comes from v_exp_f32 and the 2^lo factor from its first
+// order term 1 + lo ln 2 (|lo| < 2^-20 makes the second order negligible).
+__device__ __forceinline__ float exp_accurate(float x) {
+    constexpr float kLog2eHi = 1.44269502162933349609375f;       // float(log2 e)
+    constexpr float kLog2eLo = 1.925963033500011079101604e-8f;   // log2 e - kLog2eHi
+    constexpr float kLn2 = 0.693147180559945309f;
+    const float hi = x * kLog2eHi;
+    const float lo = __builtin_fmaf(x, kLog2eHi, -hi) + x * kLog2eLo;
+    const float e = __builtin_amdgcn_exp2f(hi);
+    // x = -inf leaves lo NaN with e = 0 (and x = +inf, e = inf): e is then exact.
+    return __builtin_isfinite(lo) ? __builtin_fmaf(e, lo * kLn2, e) : e;
+}
+
+__device__ __forceinline__ void unpack8(const h8& h, float (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = float(h[i]);
+}
+
+__device__ __forceinline__ h8 pack8(const float (&v)[8]) {
+    h8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = _Float16(v[i]);
+    return h;
+}
+
+}  // namespace flint

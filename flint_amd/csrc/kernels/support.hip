@@ -1,0 +1,455 @@
+// Data-movement kernels around the hot path: byte copy, FP32 -> FP16, the
+// attention heads' split / merge, and the embedding's forward and backward
+// passes. All are HBM-bound; every one moves 16-byte vectors where the
+// alignment the ABI promises allows it.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "common/common.h"
+#include "kernels/kernels.h"
+#include "kernels/reduce_common.h"
+
+#pragma clang fp contract(off)
+
+namespace flint {
+namespace {
+
+constexpr unsigned kMaxGrid = 1u << 20;
+
+unsigned grid_for(size_t items, unsigned threads) {
+    return unsigned(std::clamp<size_t>((items + threads - 1) / threads, 1, kMaxGrid));
+}
+
+// ------------------------------------------------------------------- copy
+
+__global__ void __launch_bounds__(256)
+copy_vec(u4* __restrict__ dst, const u4* __restrict__ src, size_t vecs) {
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < vecs; i += size_t(gridDim.x) * 256)
+        dst[i] = src[i];
+}
+
+__global__ void __launch_bounds__(256)
+copy_bytes(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, size_t bytes) {
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < bytes;
+         i += size_t(gridDim.x) * 256)
+        dst[i] = src[i];
+}
+
+__global__ void __launch_bounds__(256)
+fill_zero_vec(u4* __restrict__ dst, size_t vecs) {
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < vecs; i += size_t(gridDim.x) * 256)
+        dst[i] = u4{0u, 0u, 0u, 0u};
+}
+
+__global__ void __launch_bounds__(256)
+fill_zero_bytes(uint8_t* __restrict__ dst, size_t bytes) {
+    for (size_t i = threadIdx.x; i < bytes; i += 256) dst[i] = 0;
+}
+
+// ------------------------------------------------------------ FP32 -> FP16
+
+__global__ void __launch_bounds__(256)
+fp32_to_fp16(_Float16* __restrict__ y, const float* __restrict__ x, size_t count) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const size_t quads = count / 4;
+    const size_t stride = size_t(gridDim.x) * 256;
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < quads; i += stride) {
+        const f4 v = reinterpret_cast<const f4*>(x)[i];
+        reinterpret_cast<h4*>(y)[i] = h4{_Float16(v[0]), _Float16(v[1]), _Float16(v[2]),
+                                         _Float16(v[3])};
+    }
+    // The last count % 4 values, one thread each.
+    if (blockIdx.x == 0 && threadIdx.x < count - quads * 4) {
+        const size_t i = quads * 4 + threadIdx.x;
+        y[i] = _Float16(x[i]);
+    }
+}
+
+// ------------------------------------------------------------ heads
+
+// One thread per 16-byte chunk of the heads layout [b][h][t][c].
+__global__ void __launch_bounds__(256)
+heads_move(h8* __restrict__ y, const h8* __restrict__ x, size_t rows, size_t length, int heads,
+           int head_chunks, int row_chunks, int first_chunk, int merge) {
+    const size_t total = rows * size_t(heads) * head_chunks;
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < total;
+         i += size_t(gridDim.x) * 256) {
+        const int c = int(i % head_chunks);
+        size_t rest = i / head_chunks;
+        const size_t t = rest % length;
+        rest /= length;
+        const int h = int(rest % heads);
+        const size_t b = rest / heads;
+        const size_t row_at = (b * length + t) * row_chunks + first_chunk + h * head_chunks + c;
+        if (merge) y[row_at] = x[i];
+        else y[i] = x[row_at];
+    }
+}
+
+// ------------------------------------------------------------ embedding fwd
+
+// One wave per row: x[r] = wte[tokens[r]] + wpe[r % length], one FP32 add each.
+__global__ void __launch_bounds__(256)
+embedding_forward(float* __restrict__ x, const uint16_t* __restrict__ tokens,
+                  const float* __restrict__ wte, const float* __restrict__ wpe, size_t rows,
+                  size_t length, size_t width) {
+    const size_t quads = width / 4;
+    for (size_t row = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6); row < rows;
+         row += size_t(gridDim.x) * 4) {
+        const size_t tok = tokens[row];
+        const f4* a = reinterpret_cast<const f4*>(wte + tok * width);
+        const f4* b = reinterpret_cast<const f4*>(wpe + (row % length) * width);
+        f4* o = reinterpret_cast<f4*>(x + row * width);
+        for (size_t q = threadIdx.x & 63; q < quads; q += 64) o[q] = a[q] + b[q];
+    }
+}
+
+// ------------------------------------------------------------ embedding bwd
+
+constexpr int kSortTile = 2048;   // rows per sort workgroup
+constexpr int kDigits = 256;      // 8-bit digits, two passes over 16-bit tokens
+
+// Per tile, per digit counts, stored digit-major (counts[d * tiles + tile]) so
+// one exclusive scan over the array gives every (tile, digit) its output base.
+__global__ void __launch_bounds__(256)
+sort_count(unsigned* __restrict__ counts, const uint16_t* __restrict__ tokens, size_t rows,
+           int shift, unsigned tiles) {
+    __shared__ unsigned hist[kDigits];
+    hist[threadIdx.x] = 0;
+    __syncthreads();
+    const size_t base = size_t(blockIdx.x) * kSortTile;
+    for (int i = threadIdx.x; i < kSortTile; i += 256) {
+        const size_t r = base + i;
+        if (r < rows) atomicAdd(&hist[(tokens[r] >> shift) & 255], 1u);
+    }
+    __syncthreads();
+    counts[size_t(threadIdx.x) * tiles + blockIdx.x] = hist[threadIdx.x];
+}
+
+// Exclusive scan of n values in place, one workgroup of 1024 threads, each
+// owning a contiguous segment.
+__global__ void __launch_bounds__(1024)
+scan_exclusive(unsigned* __restrict__ v, size_t n) {
+    __shared__ unsigned part[1024];
+    const size_t per = (n + 1023) / 1024;
+    const size_t lo = std::min(n, size_t(threadIdx.x) * per);
+    const size_t hi = std::min(n, lo + per);
+    unsigned s = 0;
+    for (size_t i = lo; i < hi; ++i) s += v[i];
+    part[threadIdx.x] = s;
+    __syncthreads();
+    for (int off = 1; off < 1024; off *= 2) {
+        const unsigned add = threadIdx.x >= unsigned(off) ? part[threadIdx.x - off] : 0u;
+        __syncthreads();
+        part[threadIdx.x] += add;
+        __syncthreads();
+    }
+    unsigned run = part[threadIdx.x] - s;
+    for (size_t i = lo; i < hi; ++i) {
+        const unsigned c = v[i];
+        v[i] = run;
+        run += c;
+    }
+}
+
+// Stable scatter of one 8-bit pass. Wave w of a tile owns rows
+// [tile*2048 + 512 w, +512) and walks them 64 at a time in order; a row's rank
+// among same-digit rows of its round comes from 8 ballots.
+__global__ void __launch_bounds__(256)
+sort_scatter(uint16_t* __restrict__ out_tokens, unsigned* __restrict__ out_rows,
+             const uint16_t* __restrict__ in_tokens, const unsigned* __restrict__ in_rows,
+             const unsigned* __restrict__ scanned, size_t rows, int shift, unsigned tiles) {
+    __shared__ unsigned wcount[4][kDigits];
+    __shared__ unsigned run[4][kDigits];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    for (int w = 0; w < 4; ++w) wcount[w][threadIdx.x] = 0;
+    __syncthreads();
+    const size_t wave_base = size_t(blockIdx.x) * kSortTile + size_t(wave) * 512;
+    for (int i = lane; i < 512; i += 64) {
+        const size_t r = wave_base + i;
+        if (r < rows) atomicAdd(&wcount[wave][(in_tokens[r] >> shift) & 255], 1u);
+    }
+    __syncthreads();
+    {
+        const int d = threadIdx.x;
+        unsigned b = scanned[size_t(d) * tiles + blockIdx.x];
+        for (int w = 0; w < 4; ++w) {
+            run[w][d] = b;
+            b += wcount[w][d];
+        }
+    }
+    __syncthreads();
+    for (int round = 0; round < 8; ++round) {
+        const size_t r = wave_base + size_t(round) * 64 + lane;
+        const bool valid = r < rows;
+        const uint16_t tok = valid ? in_tokens[r] : 0;
+        const unsigned row_id = valid ? (in_rows ? in_rows[r] : unsigned(r)) : 0u;
+        const int digit = (tok >> shift) & 255;
+        unsigned long long match = __ballot(valid);
+#pragma unroll
+        for (int bit = 0; bit < 8; ++bit) {
+            const bool set = (digit >> bit) & 1;
+            const unsigned long long b = __ballot(set);
+            match &= set ? b : ~b;
+        }
+        const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        const unsigned rank = unsigned(__popcll(match & below));
+        if (valid) {
+            const unsigned pos = run[wave][digit] + rank;
+            out_tokens[pos] = tok;
+            out_rows[pos] = row_id;
+        }
+        // The group's last lane advances the digit's running base.
+        const bool last = valid && (match >> lane) == 1ull;
+        __builtin_amdgcn_wave_barrier();
+        if (last) run[wave][digit] += unsigned(__popcll(match));
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// offsets[v] = number of sorted tokens below v, v = 0..vocab (binary search).
+__global__ void __launch_bounds__(256)
+token_offsets(unsigned* __restrict__ offsets, const uint16_t* __restrict__ sorted, size_t rows,
+              unsigned vocab) {
+    const unsigned v = blockIdx.x * 256 + threadIdx.x;
+    if (v > vocab) return;
+    size_t lo = 0, hi = rows;
+    while (lo < hi) {
+        const size_t mid = (lo + hi) / 2;
+        if (sorted[mid] < v) lo = mid + 1;
+        else hi = mid;
+    }
+    offsets[v] = unsigned(lo);
+}
+
+// dwte[v][c..c+3]: compensated sum of dx rows with token v in ascending row
+// order. Grid (vocab, column tiles of 256); a thread owns 4 columns.
+__global__ void __launch_bounds__(64)
+embedding_words(float* __restrict__ dwte, const float* __restrict__ dx,
+                const unsigned* __restrict__ sorted_rows, const unsigned* __restrict__ offsets,
+                size_t width, int accumulate) {
+    const size_t v = blockIdx.x;
+    const size_t col = (size_t(blockIdx.y) * 64 + threadIdx.x) * 4;
+    if (col >= width) return;
+    const unsigned lo = offsets[v];
+    const unsigned hi = offsets[v + 1];
+    f4* out = reinterpret_cast<f4*>(dwte + v * width + col);
+    if (lo == hi) {
+        if (!accumulate) *out = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        return;
+    }
+    Comp s[4];
+    for (unsigned i = lo; i < hi; ++i) {
+        const f4 d = *reinterpret_cast<const f4*>(dx + size_t(sorted_rows[i]) * width + col);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) comp_add(s[j], d[j]);
+    }
+    f4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        r[j] = __builtin_isfinite(s[j].sum) ? add_rn(s[j].sum, s[j].error) : s[j].sum;
+    if (accumulate) {
+        const f4 old = *out;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = add_rn(old[j], r[j]);
+    }
+    *out = r;
+}
+
+struct EmbLayout {
+    size_t partials, sorted_tokens, sorted_rows, offsets, pass_tokens, pass_rows, counts, bytes;
+};
+
+size_t align16(size_t b) { return (b + 15) / 16 * 16; }
+
+// Workspace layout, region by region (sizes as ref src/kernels/embedding_backward.cuh:44-88
+// fixes them, since the workspace size is part of the ABI): position partials,
+// sorted tokens, sorted rows, token offsets, first-pass tokens and rows,
+// per-tile digit counts.
+EmbLayout emb_layout(size_t sequences, size_t length, size_t vocab, size_t width) {
+    const size_t rows = sequences * length;
+    const size_t tiles = (rows + kSortTile - 1) / kSortTile;
+    EmbLayout l{};
+    size_t at = align16(bias_gradient_workspace(sequences, length * width));
+    l.partials = 0;
+    l.sorted_tokens = at;
+    at += align16(rows * 2);
+    l.sorted_rows = at;
+    at += align16(rows * 4);
+    l.offsets = at;
+    at += align16((vocab + 1) * 4);
+    l.pass_tokens = at;
+    at += align16(rows * 2);
+    l.pass_rows = at;
+    at += align16(rows * 4);
+    l.counts = at;
+    at += align16(tiles * kDigits * 4);
+    l.bytes = at;
+    return l;
+}
+
+// Column partials of an FP32 matrix (bias-gradient order), for dwpe.
+__global__ void __launch_bounds__(64)
+column_partials_f32(float* __restrict__ partial, const float* __restrict__ dy, size_t rows,
+                    size_t cols) {
+    __shared__ float sums[8][8][8];
+    __shared__ float errs[8][8][8];
+    const int px = threadIdx.x & 7;
+    const int ph = threadIdx.x >> 3;
+    const size_t pieces = cols / 8;
+    const size_t piece = size_t(blockIdx.x) * 8 + px;
+    const size_t first = size_t(blockIdx.y) * 256;
+    const size_t end = rows - first < 256 ? rows : first + 256;
+    Comp acc[8];
+    if (piece < pieces) {
+        for (size_t r = first + ph; r < end; r += 8) {
+            const f4* p = reinterpret_cast<const f4*>(dy + r * cols + piece * 8);
+            const f4 a = p[0], b = p[1];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) comp_add(acc[j], a[j]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) comp_add(acc[j + 4], b[j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        sums[ph][px][j] = acc[j].sum;
+        errs[ph][px][j] = acc[j].error;
+    }
+    __syncthreads();
+    if (ph != 0 || piece >= pieces) return;
+    for (int o = 1; o < 8; ++o) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) comp_merge(acc[j], sums[o][px][j], errs[o][px][j]);
+    }
+    float* srow = partial + size_t(blockIdx.y) * 2 * cols + piece * 8;
+    f4* s4 = reinterpret_cast<f4*>(srow);
+    f4* e4 = reinterpret_cast<f4*>(srow + cols);
+    s4[0] = f4{acc[0].sum, acc[1].sum, acc[2].sum, acc[3].sum};
+    s4[1] = f4{acc[4].sum, acc[5].sum, acc[6].sum, acc[7].sum};
+    e4[0] = f4{acc[0].error, acc[1].error, acc[2].error, acc[3].error};
+    e4[1] = f4{acc[4].error, acc[5].error, acc[6].error, acc[7].error};
+}
+
+}  // namespace
+
+hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    if (aligned16(dst) && aligned16(src)) {
+        const size_t vecs = bytes / 16;
+        if (vecs > 0) {
+            hipLaunchKernelGGL(copy_vec, dim3(grid_for(vecs, 256)), dim3(256), 0, stream,
+                               static_cast<u4*>(dst), static_cast<const u4*>(src), vecs);
+        }
+        const size_t tail = bytes - vecs * 16;
+        if (tail > 0) {
+            hipLaunchKernelGGL(copy_bytes, dim3(1), dim3(256), 0, stream,
+                               static_cast<uint8_t*>(dst) + vecs * 16,
+                               static_cast<const uint8_t*>(src) + vecs * 16, tail);
+        }
+    } else {
+        hipLaunchKernelGGL(copy_bytes, dim3(grid_for(bytes, 256)), dim3(256), 0, stream,
+                           static_cast<uint8_t*>(dst), static_cast<const uint8_t*>(src), bytes);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(void* dst, size_t bytes, hipStream_t stream) {
+    const size_t vecs = bytes / 16;
+    if (vecs > 0) {
+        hipLaunchKernelGGL(fill_zero_vec, dim3(grid_for(vecs, 256)), dim3(256), 0, stream,
+                           static_cast<u4*>(dst), vecs);
+    }
+    const size_t tail = bytes - vecs * 16;
+    if (tail > 0) {
+        hipLaunchKernelGGL(fill_zero_bytes, dim3(1), dim3(256), 0, stream,
+                           static_cast<uint8_t*>(dst) + vecs * 16, tail);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_fp32_to_fp16(void* y, const void* x, size_t count, hipStream_t stream) {
+    hipLaunchKernelGGL(fp32_to_fp16, dim3(grid_for(std::max<size_t>(count / 4, 1), 256)),
+                       dim3(256), 0, stream, static_cast<_Float16*>(y),
+                       static_cast<const float*>(x), count);
+    return hipGetLastError();
+}
+
+hipError_t launch_heads(void* y, const void* x, size_t batches, size_t length, size_t heads,
+                        size_t head_width, size_t row_width, size_t first, bool merge,
+                        hipStream_t stream) {
+    const size_t rows = batches * length;
+    const size_t total = rows * heads * (head_width / 8);
+    hipLaunchKernelGGL(heads_move, dim3(grid_for(total, 256)), dim3(256), 0, stream,
+                       static_cast<h8*>(y), static_cast<const h8*>(x), rows, length, int(heads),
+                       int(head_width / 8), int(row_width / 8), int(first / 8), merge ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_embedding_forward(void* x, const void* tokens, const void* wte,
+                                    const void* wpe, size_t rows, size_t length, size_t width,
+                                    hipStream_t stream) {
+    hipLaunchKernelGGL(embedding_forward, dim3(grid_for(rows, 4)), dim3(256), 0, stream,
+                       static_cast<float*>(x), static_cast<const uint16_t*>(tokens),
+                       static_cast<const float*>(wte), static_cast<const float*>(wpe), rows,
+                       length, width);
+    return hipGetLastError();
+}
+
+size_t embedding_backward_workspace(size_t sequences, size_t length, size_t vocab, size_t width) {
+    return emb_layout(sequences, length, vocab, width).bytes;
+}
+
+hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, const void* tokens,
+                                     size_t sequences, size_t length, size_t vocab, size_t width,
+                                     bool accumulate_wte, bool accumulate_wpe, void* workspace,
+                                     hipStream_t stream) {
+    const EmbLayout l = emb_layout(sequences, length, vocab, width);
+    auto* ws = static_cast<uint8_t*>(workspace);
+    const size_t rows = sequences * length;
+    const unsigned tiles = unsigned((rows + kSortTile - 1) / kSortTile);
+    auto* counts = reinterpret_cast<unsigned*>(ws + l.counts);
+    auto* pass_tokens = reinterpret_cast<uint16_t*>(ws + l.pass_tokens);
+    auto* pass_rows = reinterpret_cast<unsigned*>(ws + l.pass_rows);
+    auto* sorted_tokens = reinterpret_cast<uint16_t*>(ws + l.sorted_tokens);
+    auto* sorted_rows = reinterpret_cast<unsigned*>(ws + l.sorted_rows);
+    auto* offsets = reinterpret_cast<unsigned*>(ws + l.offsets);
+    const auto* tok = static_cast<const uint16_t*>(tokens);
+
+    // Two stable passes of 8 bits: low byte into the pass buffers, high byte
+    // into the sorted buffers.
+    for (int pass = 0; pass < 2; ++pass) {
+        const int shift = pass * 8;
+        const uint16_t* in_t = pass == 0 ? tok : pass_tokens;
+        const unsigned* in_r = pass == 0 ? nullptr : pass_rows;
+        uint16_t* out_t = pass == 0 ? pass_tokens : sorted_tokens;
+        unsigned* out_r = pass == 0 ? pass_rows : sorted_rows;
+        hipLaunchKernelGGL(sort_count, dim3(tiles), dim3(256), 0, stream, counts, in_t, rows,
+                           shift, tiles);
+        hipLaunchKernelGGL(scan_exclusive, dim3(1), dim3(1024), 0, stream, counts,
+                           size_t(tiles) * kDigits);
+        hipLaunchKernelGGL(sort_scatter, dim3(tiles), dim3(256), 0, stream, out_t, out_r, in_t,
+                           in_r, counts, rows, shift, tiles);
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(token_offsets, dim3(unsigned((vocab + 1 + 255) / 256)), dim3(256), 0,
+                       stream, offsets, sorted_tokens, rows, unsigned(vocab));
+    hipLaunchKernelGGL(embedding_words, dim3(unsigned(vocab), unsigned((width / 4 + 63) / 64)),
+                       dim3(64), 0, stream, static_cast<float*>(dwte),
+                       static_cast<const float*>(dx), sorted_rows, offsets, width,
+                       accumulate_wte ? 1 : 0);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    // dwpe: column sums of dx viewed as sequences x (length * width).
+    const size_t cols = length * width;
+    const dim3 pgrid(unsigned((cols / 8 + 7) / 8), unsigned((sequences + 255) / 256));
+    hipLaunchKernelGGL(column_partials_f32, pgrid, dim3(64), 0, stream,
+                       reinterpret_cast<float*>(ws + l.partials), static_cast<const float*>(dx),
+                       sequences, cols);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    return launch_bias_gradient_finish(dwpe, ws + l.partials, sequences, cols, accumulate_wpe,
+                                       stream);
+}
+
+}  // namespace flint

@@ -1,0 +1,327 @@
+"""ctypes binding of libflint.so's C ABI (include/flint/flint.h).
+
+Mirrors the interface of the reference's test bridge (ref tests/flint_lib.py:
+`SIGNATURES` table :57-408, `Flint` wrapper :440-870): the same method names,
+argument order and meaning, so tests written against the reference read the
+same here. Pointer arguments take a torch tensor (its data pointer), an int
+address, or None for null; stream arguments take a torch.cuda.Stream, an int
+handle, or None for torch's current stream.
+
+The library path comes from FLINT_LIB, else build/release/bin/libflint.so at
+the repository root (the path the reference's loader defaults to). Loading
+fails loudly when the library is missing: there is no fallback.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "flint" / "flint.h"
+LIBRARY = ROOT / "build" / "release" / "bin" / "libflint.so"
+
+OK = 0
+ERROR_INVALID_ARGUMENT = 1
+ERROR_CUDA = 2
+
+P = ctypes.c_void_p
+Z = ctypes.c_size_t
+I = ctypes.c_int
+F = ctypes.c_float
+
+
+class Gpt2Config(ctypes.Structure):
+    """flint_gpt2_config (ref flint.h:455-466)."""
+
+    _fields_ = [
+        ("layers", Z), ("heads", Z), ("width", Z), ("block_size", Z), ("vocab", Z),
+        ("padded_vocab", Z), ("sequences", Z), ("length", Z),
+        ("separate_buffers", I), ("backward", I),
+    ]
+
+
+class Gpt2ParameterInfo(ctypes.Structure):
+    """flint_gpt2_parameter_info (ref flint.h:470-475)."""
+
+    _fields_ = [("name", ctypes.c_char_p), ("data", P), ("rows", Z), ("cols", Z)]
+
+
+# Every function flint.h declares: name -> (restype, argtypes).
+SIGNATURES = {
+    "flint_version": (ctypes.c_char_p, []),
+    "flint_status_string": (ctypes.c_char_p, [I]),
+    "flint_last_error": (ctypes.c_char_p, []),
+    "flint_copy": (I, [P, P, Z, P]),
+    "flint_gemm_nt": (I, [P, P, P, Z, Z, Z, P]),
+    "flint_gemm_nt_bias": (I, [P, P, P, P, Z, Z, Z, P]),
+    "flint_gemm_nt_bias_gelu": (I, [P, P, P, P, P, Z, Z, Z, P]),
+    "flint_gemm_nt_bias_residual": (I, [P, P, P, P, P, Z, Z, Z, P]),
+    "flint_gemm_nn": (I, [P, P, P, Z, Z, Z, P]),
+    "flint_gemm_nn_dgelu": (I, [P, P, P, P, Z, Z, Z, P]),
+    "flint_gemm_tn": (I, [P, P, P, Z, Z, Z, I, P, Z, P]),
+    "flint_gemm_tn_workspace": (I, [Z, Z, Z, ctypes.POINTER(Z)]),
+    "flint_bias_gradient": (I, [P, P, Z, Z, I, P, Z, P]),
+    "flint_bias_gradient_workspace": (I, [Z, Z, ctypes.POINTER(Z)]),
+    "flint_gemm_nt_batched": (I, [P, P, P, Z, Z, Z, Z, F, P]),
+    "flint_gemm_nn_batched": (I, [P, P, P, Z, Z, Z, Z, P]),
+    "flint_gemm_tn_batched": (I, [P, P, P, Z, Z, Z, Z, P]),
+    "flint_layernorm_forward": (I, [P, P, P, P, P, P, Z, Z, F, P]),
+    "flint_layernorm_backward": (I, [P, P, P, P, P, P, P, P, Z, Z, I, I, P, Z, P]),
+    "flint_layernorm_backward_workspace": (I, [Z, Z, ctypes.POINTER(Z)]),
+    "flint_embedding_forward": (I, [P, P, P, P, Z, Z, Z, Z, P]),
+    "flint_embedding_backward": (I, [P, P, P, P, Z, Z, Z, Z, I, I, P, Z, P]),
+    "flint_embedding_backward_workspace": (I, [Z, Z, Z, Z, ctypes.POINTER(Z)]),
+    "flint_fp32_to_fp16": (I, [P, P, Z, P]),
+    "flint_heads_split": (I, [P, P, Z, Z, Z, Z, Z, Z, P]),
+    "flint_heads_merge": (I, [P, P, Z, Z, Z, Z, Z, Z, P]),
+    "flint_causal_softmax_forward": (I, [P, P, Z, Z, P]),
+    "flint_causal_softmax_backward": (I, [P, P, P, Z, Z, F, P]),
+    "flint_softmax_cross_entropy": (I, [P, P, P, P, F, Z, Z, Z, P]),
+    "flint_gpt2_bytes": (I, [ctypes.POINTER(Gpt2Config), ctypes.POINTER(Z)]),
+    "flint_gpt2_create": (I, [ctypes.POINTER(Gpt2Config), ctypes.POINTER(P)]),
+    "flint_gpt2_destroy": (None, [P]),
+    "flint_gpt2_parameter_count": (Z, [P]),
+    "flint_gpt2_parameter": (I, [P, Z, ctypes.POINTER(Gpt2ParameterInfo)]),
+    "flint_gpt2_sync_weights": (I, [P, P]),
+    "flint_gpt2_forward": (I, [P, P, P, F, P]),
+    "flint_gpt2_backward": (I, [P, P, I, P]),
+    "flint_gpt2_gradient": (I, [P, Z, ctypes.POINTER(Gpt2ParameterInfo)]),
+    "flint_gpt2_outputs": (I, [P, ctypes.POINTER(P), ctypes.POINTER(P), ctypes.POINTER(P)]),
+    "flint_gpt2_mean_loss": (I, [P, P, ctypes.POINTER(ctypes.c_double)]),
+}
+
+
+class FlintError(RuntimeError):
+    """A call returned a status other than FLINT_OK."""
+
+    def __init__(self, status, message):
+        super().__init__(message)
+        self.status = status
+
+
+def pointer(value):
+    if value is None or isinstance(value, int):
+        return value
+    return value.data_ptr()
+
+
+def stream_handle(stream):
+    if isinstance(stream, int):
+        return stream
+    import torch
+
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return stream.cuda_stream
+
+
+def library_path():
+    override = os.environ.get("FLINT_LIB")
+    return Path(override) if override else LIBRARY
+
+
+class Flint:
+    """The loaded library with every C signature declared."""
+
+    def __init__(self, path=None):
+        self.path = Path(path) if path else library_path()
+        if not self.path.is_file():
+            raise FileNotFoundError(
+                f"{self.path} not found; build it with `python -c 'import __graft_entry__ as g; "
+                "g.build()'` or `make -C flint_amd`"
+            )
+        self.lib = ctypes.CDLL(str(self.path))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(self.lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+
+    # -- status -------------------------------------------------------------
+    def version(self):
+        return self.lib.flint_version().decode()
+
+    def status_string(self, status):
+        return self.lib.flint_status_string(status).decode()
+
+    def last_error(self):
+        return self.lib.flint_last_error().decode()
+
+    def check(self, status):
+        if status != OK:
+            message = f"{self.status_string(status)} (status {status})"
+            detail = self.last_error()
+            raise FlintError(status, f"{message}: {detail}" if detail else message)
+
+    # -- GEMMs ----------------------------------------------------------------
+    def copy(self, dst, src, nbytes, stream=None):
+        self.check(self.lib.flint_copy(pointer(dst), pointer(src), nbytes, stream_handle(stream)))
+
+    def gemm_nt(self, y, x, w, m, n, k, stream=None):
+        self.check(self.lib.flint_gemm_nt(pointer(y), pointer(x), pointer(w), m, n, k,
+                                          stream_handle(stream)))
+
+    def gemm_nt_bias(self, y, x, w, bias, m, n, k, stream=None):
+        self.check(self.lib.flint_gemm_nt_bias(pointer(y), pointer(x), pointer(w), pointer(bias),
+                                               m, n, k, stream_handle(stream)))
+
+    def gemm_nt_bias_gelu(self, y, pre, x, w, bias, m, n, k, stream=None):
+        self.check(self.lib.flint_gemm_nt_bias_gelu(pointer(y), pointer(pre), pointer(x),
+                                                    pointer(w), pointer(bias), m, n, k,
+                                                    stream_handle(stream)))
+
+    def gemm_nt_bias_residual(self, y, x, w, bias, residual, m, n, k, stream=None):
+        self.check(self.lib.flint_gemm_nt_bias_residual(pointer(y), pointer(x), pointer(w),
+                                                        pointer(bias), pointer(residual), m, n, k,
+                                                        stream_handle(stream)))
+
+    def gemm_nn(self, y, x, w, m, n, k, stream=None):
+        self.check(self.lib.flint_gemm_nn(pointer(y), pointer(x), pointer(w), m, n, k,
+                                          stream_handle(stream)))
+
+    def gemm_nn_dgelu(self, y, x, w, pre, m, n, k, stream=None):
+        self.check(self.lib.flint_gemm_nn_dgelu(pointer(y), pointer(x), pointer(w), pointer(pre),
+                                                m, n, k, stream_handle(stream)))
+
+    def gemm_tn_workspace(self, m, n, k):
+        out = Z(0)
+        self.check(self.lib.flint_gemm_tn_workspace(m, n, k, ctypes.byref(out)))
+        return out.value
+
+    def gemm_tn(self, y, x, w, m, n, k, accumulate=False, workspace=None, workspace_bytes=None,
+                stream=None):
+        """y (+)= x^T w. Allocates the workspace with torch when none is given."""
+        if workspace is None:
+            need = self.gemm_tn_workspace(m, n, k)
+            if need:
+                import torch
+
+                workspace = torch.empty(need, dtype=torch.uint8, device="cuda")
+        if workspace_bytes is None:
+            workspace_bytes = 0 if workspace is None or isinstance(workspace, int) else (
+                workspace.numel() * workspace.element_size())
+        self.check(self.lib.flint_gemm_tn(pointer(y), pointer(x), pointer(w), m, n, k,
+                                          int(bool(accumulate)), pointer(workspace),
+                                          workspace_bytes, stream_handle(stream)))
+
+    def gemm_nt_batched(self, y, x, w, batches, m, n, k, scale=1.0, stream=None):
+        self.check(self.lib.flint_gemm_nt_batched(pointer(y), pointer(x), pointer(w), batches, m,
+                                                  n, k, scale, stream_handle(stream)))
+
+    def gemm_nn_batched(self, y, x, w, batches, m, n, k, stream=None):
+        self.check(self.lib.flint_gemm_nn_batched(pointer(y), pointer(x), pointer(w), batches, m,
+                                                  n, k, stream_handle(stream)))
+
+    def gemm_tn_batched(self, y, x, w, batches, m, n, k, stream=None):
+        self.check(self.lib.flint_gemm_tn_batched(pointer(y), pointer(x), pointer(w), batches, m,
+                                                  n, k, stream_handle(stream)))
+
+    # -- reductions -----------------------------------------------------------
+    def bias_gradient_workspace(self, rows, cols):
+        out = Z(0)
+        self.check(self.lib.flint_bias_gradient_workspace(rows, cols, ctypes.byref(out)))
+        return out.value
+
+    def bias_gradient(self, dbias, dy, rows, cols, accumulate=False, workspace=None,
+                      workspace_bytes=None, stream=None):
+        if workspace is None:
+            import torch
+
+            workspace = torch.empty(max(self.bias_gradient_workspace(rows, cols), 16),
+                                    dtype=torch.uint8, device="cuda")
+        if workspace_bytes is None:
+            workspace_bytes = workspace.numel() * workspace.element_size()
+        self.check(self.lib.flint_bias_gradient(pointer(dbias), pointer(dy), rows, cols,
+                                                int(bool(accumulate)), pointer(workspace),
+                                                workspace_bytes, stream_handle(stream)))
+
+    def layernorm_forward(self, y, mean, rstd, x, gamma, beta, rows, cols, eps=1e-5,
+                          stream=None):
+        self.check(self.lib.flint_layernorm_forward(pointer(y), pointer(mean), pointer(rstd),
+                                                    pointer(x), pointer(gamma), pointer(beta),
+                                                    rows, cols, eps, stream_handle(stream)))
+
+    def layernorm_backward_workspace(self, rows, cols):
+        out = Z(0)
+        self.check(self.lib.flint_layernorm_backward_workspace(rows, cols, ctypes.byref(out)))
+        return out.value
+
+    def layernorm_backward(self, dx, dgamma, dbeta, dy, x, mean, rstd, gamma, rows, cols,
+                           accumulate_dx=False, accumulate_params=False, workspace=None,
+                           workspace_bytes=None, stream=None):
+        if workspace is None:
+            import torch
+
+            workspace = torch.empty(max(self.layernorm_backward_workspace(rows, cols), 16),
+                                    dtype=torch.uint8, device="cuda")
+        if workspace_bytes is None:
+            workspace_bytes = workspace.numel() * workspace.element_size()
+        self.check(self.lib.flint_layernorm_backward(
+            pointer(dx), pointer(dgamma), pointer(dbeta), pointer(dy), pointer(x), pointer(mean),
+            pointer(rstd), pointer(gamma), rows, cols, int(bool(accumulate_dx)),
+            int(bool(accumulate_params)), pointer(workspace), workspace_bytes,
+            stream_handle(stream)))
+
+    def causal_softmax_forward(self, p, s, batches, length, stream=None):
+        self.check(self.lib.flint_causal_softmax_forward(pointer(p), pointer(s), batches, length,
+                                                         stream_handle(stream)))
+
+    def causal_softmax_backward(self, ds, p, dp, batches, length, scale=1.0, stream=None):
+        self.check(self.lib.flint_causal_softmax_backward(pointer(ds), pointer(p), pointer(dp),
+                                                          batches, length, scale,
+                                                          stream_handle(stream)))
+
+    def softmax_cross_entropy(self, dlogits, row_loss, logits, targets, scale, rows, vocab, cols,
+                              stream=None):
+        self.check(self.lib.flint_softmax_cross_entropy(pointer(dlogits), pointer(row_loss),
+                                                        pointer(logits), pointer(targets), scale,
+                                                        rows, vocab, cols, stream_handle(stream)))
+
+    # -- data movement --------------------------------------------------------
+    def fp32_to_fp16(self, y, x, count, stream=None):
+        self.check(self.lib.flint_fp32_to_fp16(pointer(y), pointer(x), count,
+                                               stream_handle(stream)))
+
+    def heads_split(self, y, x, batches, length, heads, head_width, row_width, first,
+                    stream=None):
+        self.check(self.lib.flint_heads_split(pointer(y), pointer(x), batches, length, heads,
+                                              head_width, row_width, first, stream_handle(stream)))
+
+    def heads_merge(self, y, x, batches, length, heads, head_width, row_width, first,
+                    stream=None):
+        self.check(self.lib.flint_heads_merge(pointer(y), pointer(x), batches, length, heads,
+                                              head_width, row_width, first, stream_handle(stream)))
+
+    def embedding_forward(self, x, tokens, wte, wpe, sequences, length, vocab, width,
+                          stream=None):
+        self.check(self.lib.flint_embedding_forward(pointer(x), pointer(tokens), pointer(wte),
+                                                    pointer(wpe), sequences, length, vocab, width,
+                                                    stream_handle(stream)))
+
+    def embedding_backward_workspace(self, sequences, length, vocab, width):
+        out = Z(0)
+        self.check(self.lib.flint_embedding_backward_workspace(sequences, length, vocab, width,
+                                                               ctypes.byref(out)))
+        return out.value
+
+    def embedding_backward(self, dwte, dwpe, dx, tokens, sequences, length, vocab, width,
+                           accumulate_wte=False, accumulate_wpe=False, workspace=None,
+                           workspace_bytes=None, stream=None):
+        if workspace is None:
+            import torch
+
+            need = self.embedding_backward_workspace(sequences, length, vocab, width)
+            workspace = torch.empty(max(need, 16), dtype=torch.uint8, device="cuda")
+        if workspace_bytes is None:
+            workspace_bytes = workspace.numel() * workspace.element_size()
+        self.check(self.lib.flint_embedding_backward(
+            pointer(dwte), pointer(dwpe), pointer(dx), pointer(tokens), sequences, length, vocab,
+            width, int(bool(accumulate_wte)), int(bool(accumulate_wpe)), pointer(workspace),
+            workspace_bytes, stream_handle(stream)))
+
+
+def declared_functions(header=HEADER):
+    """Names of every FLINT_API function the header declares."""
+    import re
+
+    text = Path(header).read_text()
+    return re.findall(r"FLINT_API\s+[^;(]*?\b(flint_\w+)\s*\(", text)

@@ -1,0 +1,262 @@
+"""GEMM family parity on the GPU, through the C ABI, against a PyTorch FP32 CPU
+reference (the north star's: max|err| / max|ref| <= 2e-3) and the exact
+contracts of the reference's tests (ref tests/test_gemm*.py)."""
+
+import numpy as np
+import pytest
+import torch
+
+from inputs import normal, rel_err, uniform
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def ref_nt(x, w):
+    return x.float() @ w.float().T
+
+
+def ref_nn(x, w):
+    return x.float() @ w.float()
+
+
+def ref_tn(x, w):
+    return x.float().T @ w.float()
+
+
+# Odd shapes (edge tiles, k tails), whole-tile shapes, and GPT-2 shapes.
+NT_SHAPES = [(1, 1, 8), (37, 53, 24), (200, 136, 72), (256, 192, 128), (1024, 768, 768),
+             (8192, 2304, 768)]
+NN_SHAPES = [(1, 8, 8), (37, 56, 24), (200, 136, 72), (256, 192, 128), (8192, 768, 3072)]
+
+
+@pytest.mark.parametrize("m,n,k", NT_SHAPES)
+def test_nt(flint, cuda, m, n, k):
+    x = uniform((m, k), 1)
+    w = uniform((n, k), 2)
+    y = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
+    flint.gemm_nt(y, x.to(cuda), w.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu(), ref_nt(x, w)) <= TOL
+
+
+@pytest.mark.parametrize("m,n,k", [(37, 53, 24), (256, 192, 128), (8192, 2304, 768)])
+def test_nt_bias(flint, cuda, m, n, k):
+    x = uniform((m, k), 3)
+    w = normal((n, k), 4, 0.02, torch.float16)
+    b = normal((n,), 5, 0.02)
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nt_bias(y, x.to(cuda), w.to(cuda), b.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu(), ref_nt(x, w) + b) <= TOL
+
+
+@pytest.mark.parametrize("m,n,k", [(37, 53, 24), (256, 192, 128), (8192, 3072, 768)])
+def test_nt_bias_gelu(flint, cuda, m, n, k):
+    x = uniform((m, k), 6)
+    w = normal((n, k), 7, 0.02, torch.float16)
+    b = normal((n,), 8, 0.02)
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    pre = torch.empty_like(y)
+    flint.gemm_nt_bias_gelu(y, pre, x.to(cuda), w.to(cuda), b.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    s = ref_nt(x, w) + b
+    assert rel_err(pre.cpu(), s) <= TOL
+    gelu = torch.nn.functional.gelu(s.double(), approximate="tanh")
+    assert rel_err(y.cpu(), gelu) <= TOL
+    # pre is bit for bit gemm_nt_bias's output (ref tests/test_gemm_bias_gelu.py:129-138).
+    yb = torch.empty_like(y)
+    flint.gemm_nt_bias(yb, x.to(cuda), w.to(cuda), b.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(yb.cpu().view(torch.int16), pre.cpu().view(torch.int16))
+
+
+@pytest.mark.parametrize("m,n,k", [(37, 54, 24), (256, 192, 128), (8192, 768, 768),
+                                   (8192, 768, 3072)])
+def test_nt_bias_residual(flint, cuda, m, n, k):
+    x = uniform((m, k), 9)
+    w = normal((n, k), 10, 0.02, torch.float16)
+    b = normal((n,), 11, 0.02)
+    r = normal((m, n), 12)
+    y = torch.empty((m, n), dtype=torch.float32, device=cuda)
+    flint.gemm_nt_bias_residual(y, x.to(cuda), w.to(cuda), b.to(cuda), r.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu(), r + (ref_nt(x, w) + b)) <= TOL
+    # A -0 residual reproduces gemm_nt_bias's FP32 sums before rounding: check
+    # that y - residual rounds to gemm_nt_bias bit for bit
+    # (ref tests/test_gemm_bias_residual.py:330).
+    z = torch.full((m, n), -0.0, dtype=torch.float32, device=cuda)
+    flint.gemm_nt_bias_residual(y, x.to(cuda), w.to(cuda), b.to(cuda), z, m, n, k)
+    yb = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nt_bias(yb, x.to(cuda), w.to(cuda), b.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(y.half().cpu().view(torch.int16), yb.cpu().view(torch.int16))
+
+
+@pytest.mark.parametrize("m,n,k", NN_SHAPES)
+def test_nn(flint, cuda, m, n, k):
+    x = uniform((m, k), 13)
+    w = uniform((k, n), 14)
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nn(y, x.to(cuda), w.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu(), ref_nn(x, w)) <= TOL
+
+
+@pytest.mark.parametrize("m,n,k", [(37, 56, 24), (256, 192, 128), (8192, 3072, 768)])
+def test_nn_dgelu(flint, cuda, m, n, k):
+    x = normal((m, k), 15, 1e-2, torch.float16)
+    w = normal((k, n), 16, 0.02, torch.float16)
+    pre = normal((m, n), 17, 1.0, torch.float16)
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nn_dgelu(y, x.to(cuda), w.to(cuda), pre.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    from oracle.oracle import gelu_grad64
+
+    dg = torch.from_numpy(gelu_grad64(pre.float().numpy()))
+    assert rel_err(y.cpu(), ref_nn(x, w).double() * dg) <= TOL
+
+
+def test_nn_dgelu_limits(flint, cuda):
+    """pre = +inf gives gemm_nn, -inf gives 0 (ref tests/test_gemm_dgelu.py:422-465)."""
+    m, n, k = 64, 64, 64
+    x = uniform((m, k), 18)
+    w = uniform((k, n), 19)
+    plain = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nn(plain, x.to(cuda), w.to(cuda), m, n, k)
+    for value, expect in ((float("inf"), plain), (float("-inf"), torch.zeros_like(plain))):
+        pre = torch.full((m, n), value, dtype=torch.float16, device=cuda)
+        y = torch.empty_like(plain)
+        flint.gemm_nn_dgelu(y, x.to(cuda), w.to(cuda), pre, m, n, k)
+        torch.cuda.synchronize()
+        assert torch.equal(y.cpu().float(), expect.cpu().float())
+
+
+TN_SHAPES = [(8, 8, 1), (8, 8, 16384), (136, 120, 3000), (296, 200, 2049), (768, 768, 8192),
+             (3072, 768, 8192), (2304, 768, 1024)]
+
+
+@pytest.mark.parametrize("m,n,k", TN_SHAPES)
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_tn(flint, cuda, m, n, k, accumulate):
+    x = normal((k, m), 20, 1e-2, torch.float16)
+    w = uniform((k, n), 21)
+    y0 = normal((m, n), 22)
+    y = y0.clone().to(cuda)
+    flint.gemm_tn(y, x.to(cuda), w.to(cuda), m, n, k, accumulate=accumulate)
+    torch.cuda.synchronize()
+    ref = ref_tn(x, w) + (y0 if accumulate else 0)
+    assert rel_err(y.cpu(), ref) <= TOL
+    if accumulate:
+        # Accumulating equals y0 + the plain result bit for bit (ref tests/test_gemm_tn.py:304).
+        plain = torch.empty((m, n), device=cuda)
+        flint.gemm_tn(plain, x.to(cuda), w.to(cuda), m, n, k, accumulate=False)
+        torch.cuda.synchronize()
+        assert torch.equal(y.cpu(), y0 + plain.cpu())
+
+
+def test_tn_workspace_contract(flint, cuda):
+    """Workspace sizes the reference's tests pin (ref tests/test_gemm_tn.py:193-237)."""
+    for m, n, k in [(64, 64, 1000), (50304, 768, 65536), (4096, 4096, 65536), (2304, 768, 1024)]:
+        assert flint.gemm_tn_workspace(m, n, k) == 0, (m, n, k)
+    for m, n, k in [(8, 8, 16384), (136, 120, 3000), (296, 200, 2049), (1032, 8, 4096),
+                    (2056, 16, 8192)]:
+        b = flint.gemm_tn_workspace(m, n, k)
+        assert b > 0 and b % (m * n * 4) == 0 and b // (m * n * 4) <= 16, (m, n, k, b)
+
+
+def test_integer_exact(flint, cuda):
+    """Inputs in {-1, 0, 1} at k = 2^16 sum exactly (ref tests/test_gemm.py:522-534)."""
+    m, n, k = 64, 64, 65536
+    g = torch.Generator().manual_seed(23)
+    x = torch.randint(-1, 2, (m, k), generator=g).half()
+    w = torch.randint(-1, 2, (n, k), generator=g).half()
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nt(y, x.to(cuda), w.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    exact = (x.double() @ w.double().T).half()
+    assert torch.equal(y.cpu(), exact)
+    xt = x.T.contiguous()
+    yt = torch.empty((m, n), device=cuda)
+    flint.gemm_tn(yt, xt.to(cuda), w.T.contiguous().to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(yt.cpu(), (x.double() @ w.double().T).float())
+
+
+@pytest.mark.parametrize("batches,m,n,k", [(3, 40, 56, 24), (96, 1024, 1024, 64)])
+def test_nt_batched(flint, cuda, batches, m, n, k):
+    x = uniform((batches, m, k), 24)
+    w = uniform((batches, n, k), 25)
+    y = torch.empty((batches, m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nt_batched(y, x.to(cuda), w.to(cuda), batches, m, n, k, 0.125)
+    torch.cuda.synchronize()
+    ref = torch.bmm(x.float(), w.float().transpose(1, 2).contiguous()) * 0.125
+    assert rel_err(y.cpu(), ref) <= TOL
+    # Scale 1 equals gemm_nt per batch bit for bit (ref tests/test_gemm_batched.py:390).
+    flint.gemm_nt_batched(y, x.to(cuda), w.to(cuda), batches, m, n, k, 1.0)
+    one = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nt(one, x[-1].contiguous().to(cuda), w[-1].contiguous().to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(y[-1].cpu().view(torch.int16), one.cpu().view(torch.int16))
+
+
+@pytest.mark.parametrize("batches,m,n,k", [(3, 40, 56, 24), (96, 1024, 64, 1024)])
+def test_nn_batched(flint, cuda, batches, m, n, k):
+    x = uniform((batches, m, k), 26)
+    w = uniform((batches, k, n), 27)
+    y = torch.empty((batches, m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nn_batched(y, x.to(cuda), w.to(cuda), batches, m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu(), torch.bmm(x.float(), w.float())) <= TOL
+
+
+@pytest.mark.parametrize("batches,m,n,k", [(3, 40, 56, 24), (96, 1024, 64, 1024)])
+def test_tn_batched(flint, cuda, batches, m, n, k):
+    x = uniform((batches, k, m), 28)
+    w = uniform((batches, k, n), 29)
+    y = torch.empty((batches, m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_tn_batched(y, x.to(cuda), w.to(cuda), batches, m, n, k)
+    torch.cuda.synchronize()
+    ref = torch.bmm(x.float().transpose(1, 2).contiguous(), w.float())
+    assert rel_err(y.cpu(), ref) <= TOL
+
+
+def test_logits_head(flint, cuda):
+    """Config 4's NT 8192 x 50304 x 768, with the padding columns of w zero."""
+    m, n, k, vocab = 8192, 50304, 768, 50257
+    x = uniform((m, k), 30)
+    w = normal((n, k), 31, 0.02, torch.float16)
+    w[vocab:] = 0
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nt(y, x.to(cuda), w.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    rows = torch.arange(0, m, 97)
+    ref = x[rows].float() @ w.float().T
+    assert rel_err(y.cpu()[rows], ref) <= TOL
+    assert torch.all(y[:, vocab:] == 0).item()
+
+
+def test_overflow_gives_inf(flint, cuda):
+    """Each output rounds once: sums past FP16's range give inf (ref tests/test_gemm.py:359-389)."""
+    m, n, k = 32, 32, 64
+    x = torch.full((m, k), 60.0, dtype=torch.float16)
+    w = torch.full((n, k), 60.0, dtype=torch.float16)
+    w[1] = -60.0
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nt(y, x.to(cuda), w.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    yc = y.cpu().float()
+    assert torch.all(yc[:, 0] == float("inf")) and torch.all(yc[:, 1] == float("-inf"))
+
+
+def test_deterministic(flint, cuda):
+    m, n, k = 1024, 768, 3072
+    x = uniform((m, k), 32).to(cuda)
+    w = uniform((n, k), 33).to(cuda)
+    a = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    b = torch.full((m, n), 7.0, dtype=torch.float16, device=cuda)
+    flint.gemm_nt(a, x, w, m, n, k)
+    flint.gemm_nt(b, x, w, m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))

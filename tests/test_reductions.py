@@ -1,0 +1,197 @@
+"""LayerNorm, bias gradient, causal softmax and softmax + cross-entropy parity on
+the GPU through the C ABI. Tolerances are the north star's (1e-3 relative for
+LayerNorm, softmax and loss); where the reference fixes a shape-only
+summation order, the C oracle restates it and the kernel must match it bit
+for bit. Target gathers are bit-exact."""
+
+import numpy as np
+import pytest
+import torch
+
+from inputs import normal, rel_err, targets, uniform
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _bits(t):
+    return t.cpu().contiguous().view(torch.int16 if t.element_size() == 2 else torch.int32)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (5, 3), (33, 768), (8192, 768), (7, 1000),
+                                       (64, 4096), (3, 8000)])
+def test_layernorm_forward(flint, cuda, rows, cols):
+    x = normal((rows, cols), 1)
+    x[:, ::97] += 3000.0  # GPT-2-like outlier channels
+    gamma = 1 + normal((cols,), 2, 0.1)
+    beta = normal((cols,), 3, 0.1)
+    y = torch.empty((rows, cols), dtype=torch.float16, device=cuda)
+    mean = torch.empty(rows, device=cuda)
+    rstd = torch.empty(rows, device=cuda)
+    flint.layernorm_forward(y, mean, rstd, x.to(cuda), gamma.to(cuda), beta.to(cuda), rows, cols)
+    torch.cuda.synchronize()
+    ref_y, ref_mu, ref_rs = oracle.layernorm64(x.numpy(), gamma.numpy(), beta.numpy(), 1e-5)
+    assert rel_err(y.cpu(), torch.from_numpy(ref_y)) <= TOL
+    assert np.allclose(mean.cpu().numpy(), ref_mu, rtol=1e-6, atol=1e-6)
+    assert np.allclose(rstd.cpu().numpy(), ref_rs, rtol=1e-5)
+    ey, emu, ers = oracle.layernorm_forward(x.numpy(), gamma.numpy(), beta.numpy(), 1e-5)
+    # The compensated sums make the order nearly irrelevant: >= 99.9% equal bits.
+    same = (y.cpu().numpy().view(np.int16) == ey.view(np.int16)).mean()
+    assert same >= 0.999
+
+
+def test_layernorm_exact_cases(flint, cuda):
+    """Constant rows give y = beta; gamma = 0 gives beta (ref tests/test_layernorm.py:342-411)."""
+    rows, cols = 4, 768
+    x = torch.full((rows, cols), 3.25)
+    gamma = normal((cols,), 4)
+    beta = normal((cols,), 5)
+    y = torch.empty((rows, cols), dtype=torch.float16, device=cuda)
+    mean = torch.empty(rows, device=cuda)
+    rstd = torch.empty(rows, device=cuda)
+    flint.layernorm_forward(y, mean, rstd, x.to(cuda), gamma.to(cuda), beta.to(cuda), rows, cols)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), beta.half().expand(rows, cols))
+    assert torch.all(mean.cpu() == 3.25)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 8), (300, 24), (8192, 768), (1000, 3072), (517, 2056)])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_bias_gradient(flint, cuda, rows, cols, accumulate):
+    dy = normal((rows, cols), 6, 1.0, torch.float16)
+    old = normal((cols,), 7)
+    out = old.clone().to(cuda)
+    flint.bias_gradient(out, dy.to(cuda), rows, cols, accumulate=accumulate)
+    torch.cuda.synchronize()
+    expect = oracle.bias_gradient(dy.numpy(), old.numpy() if accumulate else None)
+    assert np.array_equal(out.cpu().numpy().view(np.int32), expect.view(np.int32))
+    ref = dy.double().sum(0) + (old.double() if accumulate else 0)
+    assert rel_err(out.cpu(), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("rows,cols", [(3, 8), (300, 24), (8192, 768), (100, 4096)])
+@pytest.mark.parametrize("acc", [False, True])
+def test_layernorm_backward(flint, cuda, rows, cols, acc):
+    x = normal((rows, cols), 8)
+    gamma = 1 + normal((cols,), 9, 0.1)
+    beta = normal((cols,), 10, 0.1)
+    dy = normal((rows, cols), 11, 1.0, torch.float16)
+    y = torch.empty((rows, cols), dtype=torch.float16, device=cuda)
+    mean = torch.empty(rows, device=cuda)
+    rstd = torch.empty(rows, device=cuda)
+    flint.layernorm_forward(y, mean, rstd, x.to(cuda), gamma.to(cuda), beta.to(cuda), rows, cols)
+    dx0 = normal((rows, cols), 12)
+    dg0 = normal((cols,), 13)
+    db0 = normal((cols,), 14)
+    dx, dg, db = dx0.clone().to(cuda), dg0.clone().to(cuda), db0.clone().to(cuda)
+    flint.layernorm_backward(dx, dg, db, dy.to(cuda), x.to(cuda), mean, rstd, gamma.to(cuda),
+                             rows, cols, accumulate_dx=acc, accumulate_params=acc)
+    torch.cuda.synchronize()
+    mu, rs = mean.cpu().numpy(), rstd.cpu().numpy()
+    edx, edg, edb = oracle.layernorm_backward(
+        dy.numpy(), x.numpy(), mu, rs, gamma.numpy(),
+        dx0.numpy() if acc else None, dg0.numpy() if acc else None, db0.numpy() if acc else None)
+    for got, want in ((dx, edx), (dg, edg), (db, edb)):
+        assert np.array_equal(got.cpu().numpy().view(np.int32), want.view(np.int32))
+    rdx, rdg, rdb = oracle.layernorm_backward64(dy.numpy(), x.numpy(), mu, rs, gamma.numpy())
+    if acc:
+        rdx, rdg, rdb = rdx + dx0.numpy(), rdg + dg0.numpy(), rdb + db0.numpy()
+    for got, want in ((dx, rdx), (dg, rdg), (db, rdb)):
+        assert rel_err(got.cpu(), torch.from_numpy(want)) <= TOL
+
+
+@pytest.mark.parametrize("batches,length", [(1, 8), (3, 40), (4, 1024), (96, 1024)])
+def test_causal_softmax_forward(flint, cuda, batches, length):
+    s = normal((batches, length, length), 15, 4.0, torch.float16)
+    p = torch.full_like(s, float("nan")).to(cuda)
+    flint.causal_softmax_forward(p, s.to(cuda), batches, length)
+    torch.cuda.synchronize()
+    pc = p.cpu()
+    pick = slice(0, min(batches, 8))
+    ref = oracle.causal_softmax64(s[pick].numpy(), length).reshape(-1, length, length)
+    assert rel_err(pc[pick], torch.from_numpy(ref)) <= TOL
+    emu = oracle.softmax_forward(s[pick].numpy(), length).reshape(-1, length, length)
+    same = (pc[pick].numpy().view(np.int16) == emu.view(np.int16)).mean()
+    assert same >= 0.999
+    upper = torch.triu(torch.ones(length, length, dtype=torch.bool), 1)
+    assert torch.all(pc[:, upper] == 0) and not torch.any(torch.signbit(pc[:, upper]))
+
+
+def test_causal_softmax_equal_scores(flint, cuda):
+    """Equal scores give RN16(1 / (t + 1)) (ref tests/test_softmax.py:470-497)."""
+    length = 64
+    s = torch.full((1, length, length), 0.5, dtype=torch.float16)
+    p = torch.empty_like(s).to(cuda)
+    flint.causal_softmax_forward(p, s.to(cuda), 1, length)
+    torch.cuda.synchronize()
+    for t in range(length):
+        want = torch.tensor(1.0 / (t + 1), dtype=torch.float32).half()
+        assert torch.all(p[0, t, : t + 1].cpu() == want), t
+
+
+@pytest.mark.parametrize("batches,length", [(1, 8), (3, 40), (96, 1024)])
+@pytest.mark.parametrize("in_place", [False, True])
+def test_causal_softmax_backward(flint, cuda, batches, length, in_place):
+    s = normal((batches, length, length), 16, 4.0, torch.float16)
+    p = torch.empty_like(s).to(cuda)
+    flint.causal_softmax_forward(p, s.to(cuda), batches, length)
+    dp = normal((batches, length, length), 17, 1.0, torch.float16)
+    dpg = dp.clone().to(cuda)
+    ds = dpg if in_place else torch.empty_like(dpg)
+    flint.causal_softmax_backward(ds, p, dpg, batches, length, 0.125)
+    torch.cuda.synchronize()
+    pick = slice(0, min(batches, 8))
+    pn = p.cpu()[pick].numpy()
+    ref = oracle.causal_softmax_backward64(pn, dp[pick].numpy(), length, 0.125)
+    assert rel_err(ds.cpu()[pick], torch.from_numpy(ref.reshape(-1, length, length))) <= TOL
+    emu = oracle.softmax_backward(pn, dp[pick].numpy(), length, 0.125)
+    # Values, not bits: where p underflowed to 0 the kernel may store +0 for -0.
+    same = (ds.cpu()[pick].numpy().reshape(-1, length) == emu).mean()
+    assert same >= 0.999
+
+
+@pytest.mark.parametrize("rows,vocab,cols", [(1, 1, 8), (7, 1001, 1032), (64, 50257, 50304),
+                                             (8192, 50257, 50304), (3, 65536, 65536)])
+def test_softmax_cross_entropy(flint, cuda, rows, vocab, cols):
+    logits = normal((rows, cols), 18, 2.0, torch.float16)
+    t32, t16 = targets(rows, vocab, 19)
+    dl = torch.full((rows, cols), float("nan"), dtype=torch.float16, device=cuda)
+    loss = torch.empty(rows, device=cuda)
+    scale = 1024.0 / 8192.0
+    flint.softmax_cross_entropy(dl, loss, logits.to(cuda), t16.to(cuda), scale, rows, vocab,
+                                cols)
+    torch.cuda.synchronize()
+    pick = torch.arange(0, rows, max(1, rows // 64))
+    ref_loss, ref_d = oracle.cross_entropy64(logits[pick].numpy(), t32[pick].numpy(), vocab, scale)
+    assert rel_err(loss.cpu()[pick], torch.from_numpy(ref_loss)) <= TOL
+    assert rel_err(dl.cpu()[pick], torch.from_numpy(ref_d)) <= TOL
+    el, ed = oracle.cross_entropy(logits[pick].numpy(), t32[pick].numpy(), vocab, scale)
+    same = (dl.cpu()[pick].numpy().view(np.int16) == ed.view(np.int16)).mean()
+    assert same >= 0.999
+    # Bit-exact target gather: dlogits at the target carries p - 1 (negative)
+    # and every other visible value is >= 0.
+    d = dl.cpu()[pick].float()
+    tcol = t32[pick].long()
+    assert torch.all(d[torch.arange(len(pick)), tcol] <= 0)
+    if cols > vocab:
+        assert torch.all(dl.cpu()[:, vocab:] == 0)
+
+
+def test_cross_entropy_exact_cases(flint, cuda):
+    """Equal logits give loss log(vocab); vocab 1 gives loss 0
+    (ref tests/test_cross_entropy.py:891-933)."""
+    rows, cols, vocab = 4, 1024, 1000
+    logits = torch.full((rows, cols), 1.5, dtype=torch.float16)
+    _, t16 = targets(rows, vocab, 20)
+    dl = torch.empty((rows, cols), dtype=torch.float16, device=cuda)
+    loss = torch.empty(rows, device=cuda)
+    flint.softmax_cross_entropy(dl, loss, logits.to(cuda), t16.to(cuda), 1.0, rows, vocab, cols)
+    torch.cuda.synchronize()
+    assert np.allclose(loss.cpu().numpy(), np.log(vocab), rtol=1e-6)
+    flint.softmax_cross_entropy(dl, loss, logits.to(cuda), torch.zeros(rows, dtype=torch.int16,
+                                device=cuda), 1.0, rows, 1, cols)
+    torch.cuda.synchronize()
+    assert torch.all(loss.cpu() == 0)
+    assert torch.all(dl.cpu()[:, 0] == 0)
