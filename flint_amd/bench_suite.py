@@ -1,0 +1,288 @@
+"""Per-kernel measurement of every hot-path function at the GPT-2 124M shapes
+(8,192 tokens) on one MI355X -- the MI355X counterpart of the reference's
+`flint_bench` (ref bench/harness.cpp:158-288 for the protocol):
+
+  * inputs seeded and resident in HBM; buffer sets rotated so that one pass over
+    them exceeds 2x the 256 MB Infinity Cache;
+  * HIP-event timing of back-to-back launches after a warm-up, median of
+    rounds;
+  * absolute TFLOP/s (GEMMs, 2mnk) or GB/s (reductions: each input read once,
+    each output written once) and the fraction of MI355X's dense FP16 MFMA
+    peak (2,516.6 TFLOP/s) or HBM peak (8 TB/s);
+  * beside each figure, the same op in PyTorch: on the GPU (torch.matmul, i.e.
+    hipBLASLt, for plain GEMMs -- the reference's "% of cuBLAS" view) and in
+    FP32 on the host CPU on a row sample, with the thread count stated.
+
+Used by `bench.py --suite PATH`; writes one JSON object per kernel.
+"""
+
+import json
+import math
+import os
+import statistics
+import time
+from pathlib import Path
+
+PEAK_TF = 2516.6
+PEAK_GBS = 8000.0
+CACHE = 256 << 20
+M, C, V, VP, T, H = 8192, 768, 50257, 50304, 1024, 12
+
+
+def _time_gpu(torch, fn, sets, rounds=5, per_round=None):
+    """Median per-launch ms over rounds of back-to-back launches (HIP events)."""
+    for i in range(3):
+        fn(sets[i % len(sets)])
+    torch.cuda.synchronize()
+    n = per_round or max(len(sets), 4)
+    res = []
+    for _ in range(rounds):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(n):
+            fn(sets[i % len(sets)])
+        b.record()
+        torch.cuda.synchronize()
+        res.append(a.elapsed_time(b) / n)
+    return statistics.median(res)
+
+
+def _time_cpu(fn, reps=3):
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _nsets(bytes_per_set):
+    return max(1, math.ceil(2 * CACHE / max(bytes_per_set, 1)))
+
+
+def run(f, torch, dev, path):
+    import sys
+
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent / "tests"))
+    from inputs import normal, targets, uniform
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    F = torch.nn.functional
+    out = []
+
+    def record(name, kind, work, ms, cpu_s=None, cpu_work=None, peer_ms=None, note=""):
+        if kind == "gemm":
+            rate = work / (ms * 1e-3) / 1e12
+            entry = {"kernel": name, "ms": round(ms, 5), "tflops": round(rate, 1),
+                     "frac_mfma_peak": round(rate / PEAK_TF, 4)}
+            if cpu_s:
+                entry["cpu_fp32_tflops"] = round(cpu_work / cpu_s / 1e12, 4)
+            if peer_ms:
+                entry["hipblaslt_tflops"] = round(work / (peer_ms * 1e-3) / 1e12, 1)
+                entry["vs_hipblaslt"] = round(peer_ms / ms, 3)
+        else:
+            rate = work / (ms * 1e-3) / 1e9
+            entry = {"kernel": name, "ms": round(ms, 5), "gbs": round(rate, 1),
+                     "frac_hbm_peak": round(rate / PEAK_GBS, 4)}
+            if cpu_s:
+                entry["cpu_fp32_gbs"] = round(cpu_work / cpu_s / 1e9, 2)
+        entry["cpu_threads"] = threads
+        if note:
+            entry["note"] = note
+        out.append(entry)
+        print(json.dumps(entry), flush=True)
+
+    # ---------------------------------------------------------------- GEMMs
+    def gemm_case(name, layout, epi, m, n, k, sample_rows=512):
+        flops = 2 * m * n * k
+        per = (m * k + n * k) * 2 + m * n * (4 if epi in ("res", "tn") else 2) * (
+            2 if epi in ("gelu", "res") else 1)
+        nsets = _nsets(per)
+        sets = []
+        for r in range(nsets):
+            if layout == "tn":
+                x = uniform((k, m), 10 * r + 1).to(dev)
+                w = uniform((k, n), 10 * r + 2).to(dev)
+            elif layout == "nn":
+                x = uniform((m, k), 10 * r + 1).to(dev)
+                w = normal((k, n), 10 * r + 2, 0.02, torch.float16).to(dev)
+            else:
+                x = uniform((m, k), 10 * r + 1).to(dev)
+                w = normal((n, k), 10 * r + 2, 0.02, torch.float16).to(dev)
+            b = normal((n,), 10 * r + 3, 0.02).to(dev)
+            ydt = torch.float32 if epi in ("res", "tn") else torch.float16
+            y = torch.empty((m, n), dtype=ydt, device=dev)
+            aux = None
+            if epi == "gelu":
+                aux = torch.empty((m, n), dtype=torch.float16, device=dev)
+            elif epi == "res":
+                aux = normal((m, n), 10 * r + 4).to(dev)
+            elif epi == "dgelu":
+                aux = normal((m, n), 10 * r + 4, 1.0, torch.float16).to(dev)
+            sets.append((x, w, b, y, aux))
+        ws = None
+        if layout == "tn":
+            need = f.gemm_tn_workspace(m, n, k)
+            ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev) if need else None
+
+        def call(st):
+            x, w, b, y, aux = st
+            if layout == "nt":
+                if epi == "none":
+                    f.gemm_nt(y, x, w, m, n, k)
+                elif epi == "bias":
+                    f.gemm_nt_bias(y, x, w, b, m, n, k)
+                elif epi == "gelu":
+                    f.gemm_nt_bias_gelu(y, aux, x, w, b, m, n, k)
+                elif epi == "res":
+                    f.gemm_nt_bias_residual(y, x, w, b, aux, m, n, k)
+            elif layout == "nn":
+                if epi == "dgelu":
+                    f.gemm_nn_dgelu(y, x, w, aux, m, n, k)
+                else:
+                    f.gemm_nn(y, x, w, m, n, k)
+            else:
+                f.gemm_tn(y, x, w, m, n, k, accumulate=True, workspace=ws)
+
+        ms = _time_gpu(torch, call, sets)
+        peer = None
+        if epi in ("none", "bias", "tn") or layout == "nn" and epi == "none":
+            x, w = sets[0][0], sets[0][1]
+            if layout == "nt":
+                pf = lambda st: torch.matmul(st[0], st[1].T)  # noqa: E731
+            elif layout == "nn":
+                pf = lambda st: torch.matmul(st[0], st[1])  # noqa: E731
+            else:
+                pf = lambda st: torch.matmul(st[0].T, st[1])  # noqa: E731
+            peer = _time_gpu(torch, pf, sets)
+        # CPU fp32 on a row sample of the output.
+        rows = min(sample_rows, m)
+        xs = sets[0][0].float().cpu()
+        ws_ = sets[0][1].float().cpu()
+        bs = sets[0][2].cpu()
+        if layout == "nt":
+            xs = xs[:rows]
+            cpu_fn = lambda: F.gelu(xs @ ws_.T + bs, approximate="tanh") if epi == "gelu" else xs @ ws_.T + bs  # noqa: E731,E501
+        elif layout == "nn":
+            xs = xs[:rows]
+            cpu_fn = lambda: xs @ ws_  # noqa: E731
+        else:
+            xs = xs[:, :rows]
+            cpu_fn = lambda: xs.T @ ws_  # noqa: E731
+        cpu_s = _time_cpu(cpu_fn, reps=2)
+        record(name, "gemm", flops, ms, cpu_s, 2 * rows * n * k, peer,
+               note=f"{len(sets)} rotating sets; CPU sample {rows} rows")
+        del sets
+        torch.cuda.empty_cache()
+
+    gemm_case("flint_gemm_nt_bias qkv 8192x2304x768", "nt", "bias", M, 3 * C, C)
+    gemm_case("flint_gemm_nt_bias_gelu mlp-up 8192x3072x768", "nt", "gelu", M, 4 * C, C)
+    gemm_case("flint_gemm_nt_bias_residual mlp-down 8192x768x3072", "nt", "res", M, C, 4 * C)
+    gemm_case("flint_gemm_nt_bias_residual attn-proj 8192x768x768", "nt", "res", M, C, C)
+    gemm_case("flint_gemm_nt logits 8192x50304x768", "nt", "none", M, VP, C, sample_rows=128)
+    gemm_case("flint_gemm_nn mlp-up dX 8192x768x3072", "nn", "none", M, C, 4 * C)
+    gemm_case("flint_gemm_nn_dgelu 8192x3072x768", "nn", "dgelu", M, 4 * C, C)
+    gemm_case("flint_gemm_nn logits dX 8192x768x50304", "nn", "none", M, C, VP, sample_rows=128)
+    gemm_case("flint_gemm_tn mlp-up dW 3072x768x8192 (accumulate)", "tn", "tn", 4 * C, C, M)
+    gemm_case("flint_gemm_tn attn dW 768x768x8192 (accumulate)", "tn", "tn", C, C, M)
+    gemm_case("flint_gemm_tn logits dW 50304x768x8192 (accumulate)", "tn", "tn", VP, C, M,
+              sample_rows=128)
+
+    # Batched attention GEMMs, 96 heads x 1024 tokens x 64.
+    B = 8 * H
+    q = uniform((B, T, 64), 1).to(dev)
+    kk = uniform((B, T, 64), 2).to(dev)
+    s = torch.empty((B, T, T), dtype=torch.float16, device=dev)
+    ms = _time_gpu(torch, lambda st: f.gemm_nt_batched(s, q, kk, B, T, T, 64, 0.125), [0])
+    record("flint_gemm_nt_batched S=QK^T/8 96x1024x1024x64", "gemm", 2 * B * T * T * 64, ms,
+           note="HBM-bound: writes 201 MB")
+    p = uniform((B, T, T), 3).to(dev)
+    o = torch.empty((B, T, 64), dtype=torch.float16, device=dev)
+    ms = _time_gpu(torch, lambda st: f.gemm_nn_batched(o, p, kk, B, T, 64, T), [0])
+    record("flint_gemm_nn_batched O=PV 96x1024x64x1024", "gemm", 2 * B * T * T * 64, ms)
+    ms = _time_gpu(torch, lambda st: f.gemm_tn_batched(o, p, kk, B, T, 64, T), [0])
+    record("flint_gemm_tn_batched dV=P^T dO 96x1024x64x1024", "gemm", 2 * B * T * T * 64, ms)
+    del q, kk, s, p, o
+    torch.cuda.empty_cache()
+
+    # ----------------------------------------------------------- reductions
+    def red_sets(make, per_bytes):
+        return [make(r) for r in range(_nsets(per_bytes))]
+
+    # LayerNorm forward 8192 x 768: x FP32 in, y FP16 + mean/rstd out.
+    ln_bytes = M * C * 4 + M * C * 2 + 2 * M * 4 + 2 * C * 4
+    sets = red_sets(lambda r: (normal((M, C), r).to(dev), torch.empty((M, C), dtype=torch.float16,
+                    device=dev), torch.empty(M, device=dev), torch.empty(M, device=dev)), ln_bytes)
+    g = (1 + normal((C,), 9, 0.1)).to(dev)
+    bta = normal((C,), 10, 0.1).to(dev)
+    ms = _time_gpu(torch, lambda st: f.layernorm_forward(st[1], st[2], st[3], st[0], g, bta, M, C),
+                   sets, per_round=64)
+    xc = sets[0][0][:2048].cpu()
+    cpu_s = _time_cpu(lambda: F.layer_norm(xc, (C,), g.cpu(), bta.cpu()))
+    record("flint_layernorm_forward 8192x768", "red", ln_bytes, ms, cpu_s, ln_bytes / 4)
+    # LayerNorm backward (accumulate_dx): dy FP16, x FP32, dx FP32 read+write.
+    lnb_bytes = M * C * 2 + M * C * 4 + M * C * 4 * 2 + 2 * M * 4 + 3 * C * 4
+    wsb = torch.empty(f.layernorm_backward_workspace(M, C), dtype=torch.uint8, device=dev)
+    dsets = [(normal((M, C), 20 + r, 1.0, torch.float16).to(dev), torch.zeros((M, C), device=dev))
+             for r in range(len(sets))]
+    dg = torch.zeros(C, device=dev)
+    db = torch.zeros(C, device=dev)
+    ms = _time_gpu(torch, lambda st: f.layernorm_backward(
+        st[1][1], dg, db, st[1][0], st[0][0], st[0][2], st[0][3], g, M, C, accumulate_dx=True,
+        workspace=wsb), list(zip(sets, dsets)), per_round=64)
+    record("flint_layernorm_backward 8192x768 (accumulate_dx)", "red", lnb_bytes, ms,
+           note="5 kernels: dbeta, dgamma (partials + finish each), dx")
+    bg_bytes = M * C * 2 + C * 4
+    wsg = torch.empty(f.bias_gradient_workspace(M, 4 * C), dtype=torch.uint8, device=dev)
+    dy3 = [normal((M, 4 * C), 30 + r, 1.0, torch.float16).to(dev) for r in range(4)]
+    dbias = torch.zeros(4 * C, device=dev)
+    ms = _time_gpu(torch, lambda st: f.bias_gradient(dbias, st, M, 4 * C, workspace=wsg), dy3,
+                   per_round=64)
+    record("flint_bias_gradient 8192x3072", "red", M * 4 * C * 2 + 4 * C * 4, ms)
+    del sets, dsets, dy3
+    torch.cuda.empty_cache()
+
+    # Causal softmax 96 x 1024 x 1024 (visible half read, full write).
+    sm_bytes = B * (T * (T + 1) // 2) * 2 + B * T * T * 2
+    ss = [normal((B, T, T), 40 + r, 4.0, torch.float16).to(dev) for r in range(2)]
+    pp = [torch.empty((B, T, T), dtype=torch.float16, device=dev) for _ in range(2)]
+    ms = _time_gpu(torch, lambda st: f.causal_softmax_forward(pp[st], ss[st], B, T), [0, 1],
+                   per_round=16)
+    sc = ss[0][:4].float().cpu()
+    mask = torch.triu(torch.ones(T, T, dtype=torch.bool), 1)
+    cpu_s = _time_cpu(lambda: torch.softmax(sc.masked_fill(mask, float("-inf")), -1))
+    record("flint_causal_softmax_forward 96x1024x1024", "red", sm_bytes, ms, cpu_s,
+           sm_bytes * 4 / B)
+    smb_bytes = 2 * B * (T * (T + 1) // 2) * 2 + B * T * T * 2
+    ms = _time_gpu(torch, lambda st: f.causal_softmax_backward(ss[st], pp[st], ss[st], B, T,
+                                                               0.125), [0, 1], per_round=16)
+    record("flint_causal_softmax_backward 96x1024x1024 (in place)", "red", smb_bytes, ms)
+    del ss, pp
+    torch.cuda.empty_cache()
+
+    # Softmax + cross-entropy 8192 x 50304 (vocab 50257).
+    ce_bytes = M * VP * 2 * 2 + M * 2 + M * 4
+    lg = normal((M, VP), 50, 2.0, torch.float16).to(dev)
+    _, t16 = targets(M, V, 51)
+    t16 = t16.to(dev)
+    dl = torch.empty_like(lg)
+    loss = torch.empty(M, device=dev)
+    ms = _time_gpu(torch, lambda st: f.softmax_cross_entropy(dl, loss, lg, t16, 0.125, M, V, VP),
+                   [0], per_round=8)
+    lc = lg[:256, :V].float().cpu()
+    tc = (t16[:256].long() & 0xFFFF).cpu()   # uint16 targets held in int16
+
+    def ce_cpu():
+        l_ = lc.clone().requires_grad_(True)
+        F.cross_entropy(l_, tc, reduction="sum").backward()
+
+    cpu_s = _time_cpu(ce_cpu)
+    record("flint_softmax_cross_entropy 8192x50304", "red", ce_bytes, ms, cpu_s,
+           ce_bytes * 256 / M, note="one set (824 MB logits) exceeds the cache")
+    del lg, dl
+    torch.cuda.empty_cache()
+    Path(path).write_text(json.dumps(out, indent=1))
+    return out

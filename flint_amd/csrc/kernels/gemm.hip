@@ -7,31 +7,35 @@
 //   TN  y(m x n) = x(k x m)^T w(k x n)     weight gradient, FP32 out, split-K
 //
 // Design (MI355X-first, not a translation of the reference's warp tiling):
-//  * A workgroup of 256 threads (4 wave64s) owns a BM x BN macro-tile and walks
-//    k in steps of 64. Both operands are staged in LDS as k-contiguous rows
-//    ([row][64] halves, 128 B per row), so the MFMA fragment of a lane is one
-//    ds_read_b128. 16-byte chunks are XOR-swizzled by (row ^ row>>3) & 7, which
-//    keeps any 8 (32-bank) or 16 (64-bank) consecutive lanes of a fragment read
-//    on distinct banks.
-//  * Operands whose rows run along k in HBM (NT's x and w, NN's x) are copied as
-//    16-byte chunks. Operands stored k-major (NN's w, both TN operands) are read
-//    as 8x8 blocks of halves (8 rows of 16 bytes), transposed in registers and
-//    written as 8 LDS rows, so the main loop is the same for every layout.
-//  * Two LDS stages: the next k-step's global loads are in flight while the
-//    current stage feeds the MFMAs; one barrier per k-step.
+//  * A workgroup of 256 threads (4 wave64s, WAVES_M x WAVES_N) owns a BM x BN
+//    macro-tile and walks k in steps of BK (32 or 64). Both operands sit in
+//    LDS as k-contiguous rows, so a lane's MFMA fragment is one ds_read_b128.
+//    16-byte chunks are XOR-swizzled per row so that any 8 (32-bank) or 16
+//    (64-bank) consecutive lanes of a fragment read hit distinct banks.
+//  * Whole NT tiles stream global -> LDS with global_load_lds_dwordx4 (no
+//    register staging) through a ring of STAGES buffers, STAGES - 1 k-steps
+//    ahead of the MFMAs: one barrier per k-step, global latency hidden by
+//    up to three k-steps of math.
+//  * Operands stored k-major (NN's w, both TN operands), and edge tiles that
+//    need bounds checks, go through registers: 8x8 blocks of halves are read
+//    as 8 rows of 16 bytes, transposed in registers and written as 8 LDS rows
+//    one k-step ahead, so the LDS layout and the MFMA loop are the same.
 //  * The MFMA's A operand is the w tile and its B operand the x tile, so a
 //    lane's 16 accumulators are 4 runs of 4 consecutive output columns of one
-//    output row: the epilogue does 8-byte (FP16) or 16-byte (FP32) vector
-//    stores and 16-byte bias / residual loads.
-//  * Tiles are numbered so that each of the 8 XCDs (which take workgroups
-//    round-robin) owns a contiguous, grouped block of tiles and reuses its
-//    operand rows from its own L2.
+//    output row: 8-byte (FP16) / 16-byte (FP32) stores and 16-byte bias and
+//    residual loads in the epilogue.
+//  * Workgroup ids are remapped so each of the 8 XCDs (which take workgroups
+//    round-robin) owns a contiguous, grouped block of tiles and reuses operand
+//    rows from its own L2.
 //  * Epilogues (bias, bias+GELU writing pre and y, bias+residual into FP32,
 //    dGELU, scale) run on the FP32 accumulators before the single rounding.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
 
 #include "common/common.h"
 #include "kernels/kernels.h"
@@ -43,25 +47,35 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) _Float16 lds_half;
 
 constexpr int kThreads = 256;
-constexpr int kBK = 64;               // k per main-loop step
-constexpr int kChunksK = kBK / 8;     // 16-byte chunks per LDS row
 
 enum class Layout { kNT, kNN, kTN };
 // What the kernel's store stage does. kTn writes FP32 (plain, accumulate or a
 // split's partial); kTnHalf is the batched TN's FP16 output.
 enum class Store { kNone, kBias, kBiasGelu, kBiasResidual, kDGelu, kScale, kTn, kTnHalf };
 
+// Position of 16-byte chunk `chunk` of LDS row `row` (BK / 8 chunks a row).
+// BK 64: 128-byte rows, key (row ^ row >> 3) & 7; BK 32: 64-byte rows, key
+// (row >> 1 ^ row >> 2) & 3. Either keeps the 8 / 16 rows that one LDS cycle
+// serves (32 / 64 banks) on distinct banks for a fragment read.
+template <int BK>
 __device__ __forceinline__ int swizzle(int row, int chunk) {
-    return chunk ^ ((row ^ (row >> 3)) & 7);
+    if constexpr (BK == 64) return chunk ^ ((row ^ (row >> 3)) & 7);
+    else return chunk ^ (((row >> 1) ^ (row >> 2)) & 3);
 }
 
 // GPT-2's tanh GELU. 0.5 s (1 + tanh u) equals s / (1 + exp(-2u)), which has
-// no cancellation for negative s; u = sqrt(2/pi) (s + 0.044715 s^3).
+// no cancellation for negative s; u = sqrt(2/pi) (s + 0.044715 s^3). The
+// exponential is 2^(s (c0 + c1 s^2)) on v_exp_f32 and the quotient one
+// v_rcp_f32 multiply: about 1e-6 relative error, far inside FP16's rounding.
+// +inf gives +inf, -inf gives NaN (as the tanh form does), large negative s -0.
 __device__ __forceinline__ float gelu(float s) {
-    const float two_u = 1.5957691216057308f * s * __builtin_fmaf(0.044715f, s * s, 1.0f);
-    return s / (1.0f + expf(-two_u));
+    constexpr float c0 = -2.3022082f;          // -2 sqrt(2/pi) log2(e)
+    constexpr float c1 = -0.10294324f;         // c0 * 0.044715
+    const float e = __builtin_amdgcn_exp2f(s * __builtin_fmaf(c1, s * s, c0));
+    return s * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // d/ds [s sigma(2u)] = sigma + s sigma (1 - sigma) 2u', 2u' = 2 sqrt(2/pi)
@@ -69,8 +83,10 @@ __device__ __forceinline__ float gelu(float s) {
 // precision as sigma -> 1) and directly for s < 0 (e may overflow there).
 // Infinite s returns GELU's limits; NaN propagates.
 __device__ __forceinline__ float gelu_grad(float s) {
-    const float e = expf(-1.5957691216057308f * s * __builtin_fmaf(0.044715f, s * s, 1.0f));
-    const float sigma = 1.0f / (1.0f + e);
+    constexpr float c0 = -2.3022082f;
+    constexpr float c1 = -0.10294324f;
+    const float e = __builtin_amdgcn_exp2f(s * __builtin_fmaf(c1, s * s, c0));
+    const float sigma = __builtin_amdgcn_rcpf(1.0f + e);
     const float one_minus = s < 0.0f ? 1.0f - sigma : e * sigma;
     const float q = s * one_minus * __builtin_fmaf(0.21406444860866706f, s * s, 1.5957691216057308f);
     const float g = __builtin_fmaf(sigma, q, sigma);
@@ -82,7 +98,7 @@ struct TileArgs {
     int tiles_per_slice;      // tiles_m * tiles_n
     int slices;               // batches, or k splits for TN
     int group_m;              // grouped ordering width (in m tiles)
-    int split_len;            // TN: k per split (multiple of kBK)
+    int split_len;            // TN: k per split (multiple of 64)
 };
 
 // Maps the linear workgroup id to (slice, tile_m, tile_n). Workgroup b runs on
@@ -106,11 +122,58 @@ __device__ __forceinline__ bool map_tile(const TileArgs& t, int* slice, int* tm,
     return true;
 }
 
-// Copies a ROWS x 64 tile of a k-contiguous matrix (row r at base + r*ld) into
-// LDS rows, 16-byte chunks.
-template <int ROWS, bool CHECK>
+// Streams a ROWS x BK tile of a k-contiguous matrix (row r at base + r*ld)
+// straight into LDS with global_load_lds_dwordx4. Instruction i of wave w
+// fills 1 KB of LDS, rows [(4i + w) R, +R) with R = 512 / BK; lane l writes
+// the 16 bytes at position l % C of row l / C (C = BK / 8 chunks a row), so
+// it loads the global chunk the swizzle puts there.
+template <int ROWS, int BK>
+struct LdsTile {
+    static constexpr int kC = BK / 8;
+    static constexpr int kRowsPerInstr = 64 / kC;
+    static constexpr int kInstr = ROWS * kC / kThreads;   // per thread
+    static_assert(ROWS * kC % kThreads == 0, "whole wave instructions");
+
+    __device__ __forceinline__ static void load(const _Float16* __restrict__ base, size_t ld,
+                                                lds_half* lds, int tid) {
+        const int lane = tid & 63;
+        const int wave = tid >> 6;
+#pragma unroll
+        for (int i = 0; i < kInstr; ++i) {
+            const int row0 = (i * 4 + wave) * kRowsPerInstr;
+            const int row = row0 + lane / kC;
+            const int kc = swizzle<BK>(row, lane % kC);
+            __builtin_amdgcn_global_load_lds(base + size_t(row) * ld + kc * 8, lds + row0 * BK,
+                                             16, 0, 0);
+        }
+    }
+};
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima), gfx9
+// encoding: vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Waits until at most `tiles` tiles of PER loads each are outstanding.
+template <int PER, int MAX>
+__device__ __forceinline__ void wait_tiles(int tiles) {
+    if constexpr (MAX <= 0) {
+        wait_vmcnt<0>();
+    } else {
+        if (tiles >= MAX) wait_vmcnt<MAX * PER>();
+        else wait_tiles<PER, MAX - 1>(tiles);
+    }
+}
+
+// Copies a ROWS x BK tile of a k-contiguous matrix into LDS rows through
+// registers (16-byte chunks), with optional bounds checks.
+template <int ROWS, int BK, bool CHECK>
 struct DirectTile {
-    static constexpr int kChunks = ROWS * kChunksK;
+    static constexpr int kC = BK / 8;
+    static constexpr int kChunks = ROWS * kC;
     static constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
     f16x8 r[kPer];
 
@@ -120,8 +183,8 @@ struct DirectTile {
         for (int i = 0; i < kPer; ++i) {
             const int c = tid + i * kThreads;
             if (kChunks % kThreads != 0 && c >= kChunks) continue;
-            const int row = c / kChunksK;
-            const int kc = c % kChunksK;
+            const int row = c / kC;
+            const int kc = c % kC;
             const _Float16* p = base + size_t(row) * ld + kc * 8;
             if (CHECK) {
                 r[i] = (row < rows_valid && kc * 8 < k_valid) ? *reinterpret_cast<const f16x8*>(p)
@@ -136,21 +199,21 @@ struct DirectTile {
         for (int i = 0; i < kPer; ++i) {
             const int c = tid + i * kThreads;
             if (kChunks % kThreads != 0 && c >= kChunks) continue;
-            const int row = c / kChunksK;
-            const int kc = c % kChunksK;
-            *reinterpret_cast<f16x8*>(lds + row * kBK + swizzle(row, kc) * 8) = r[i];
+            const int row = c / kC;
+            const int kc = c % kC;
+            *reinterpret_cast<f16x8*>(lds + row * BK + swizzle<BK>(row, kc) * 8) = r[i];
         }
     }
 };
 
-// Copies the transpose of a 64 x ROWS tile of a matrix stored with k as its row
-// index (element (k, c) at base + k*ld + c) into ROWS LDS rows of 64 k values:
+// Copies the transpose of a BK x ROWS tile of a matrix stored with k as its row
+// index (element (k, c) at base + k*ld + c) into ROWS LDS rows of BK k values:
 // 8x8 blocks of halves are read as 8 rows of 16 bytes and transposed in
 // registers.
-template <int ROWS, bool CHECK>
+template <int ROWS, int BK, bool CHECK>
 struct TransposedTile {
     static constexpr int kColBlocks = ROWS / 8;
-    static constexpr int kBlocks = kColBlocks * kChunksK;
+    static constexpr int kBlocks = kColBlocks * (BK / 8);
     static constexpr int kPer = (kBlocks + kThreads - 1) / kThreads;
     f16x8 r[kPer][8];
 
@@ -189,7 +252,7 @@ struct TransposedTile {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) o[e] = r[i][e][j];
                 const int row = cb * 8 + j;
-                *reinterpret_cast<f16x8*>(lds + row * kBK + swizzle(row, kb) * 8) = o;
+                *reinterpret_cast<f16x8*>(lds + row * BK + swizzle<BK>(row, kb) * 8) = o;
             }
         }
     }
@@ -207,7 +270,7 @@ struct Operands {
     int m, n, k;
 };
 
-template <int BM, int BN, int WAVES_M, Layout L, Store S, bool CHECK>
+template <int BM, int BN, int BK, int STAGES, int WAVES_M, Layout L, Store S, bool CHECK>
 __global__ void __launch_bounds__(kThreads)
 gemm_kernel(Operands op, TileArgs ta) {
     constexpr int WAVES_N = 4 / WAVES_M;
@@ -215,15 +278,20 @@ gemm_kernel(Operands op, TileArgs ta) {
     constexpr int WTN = BN / WAVES_N;   // wave tile cols (n)
     constexpr int FM = WTM / 32;
     constexpr int FN = WTN / 32;
+    constexpr int KK = BK / 16;         // MFMA k sub-steps per k-step
+    // STAGES 0 selects the register-staged pipeline for NT as well.
+    constexpr bool kDirect = L == Layout::kNT && !CHECK && STAGES >= 2;
+    constexpr int kStages = kDirect ? STAGES : 2;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tiles are whole 32x32 MFMA blocks");
+    static_assert(kStages >= 2, "at least double buffering");
 
-    using TileA = typename std::conditional<L == Layout::kTN, TransposedTile<BM, CHECK>,
-                                            DirectTile<BM, CHECK>>::type;
-    using TileB = typename std::conditional<L == Layout::kNT, DirectTile<BN, CHECK>,
-                                            TransposedTile<BN, CHECK>>::type;
+    using TileA = typename std::conditional<L == Layout::kTN, TransposedTile<BM, BK, CHECK>,
+                                            DirectTile<BM, BK, CHECK>>::type;
+    using TileB = typename std::conditional<L == Layout::kNT, DirectTile<BN, BK, CHECK>,
+                                            TransposedTile<BN, BK, CHECK>>::type;
 
-    __shared__ __attribute__((aligned(16))) _Float16 lds_a[2][BM * kBK];
-    __shared__ __attribute__((aligned(16))) _Float16 lds_b[2][BN * kBK];
+    // Stage s: A tile (BM rows) then B tile (BN rows), BK halves per row.
+    __shared__ __attribute__((aligned(16))) _Float16 lds[kStages][(BM + BN) * BK];
 
     int slice, tm, tn;
     if (!map_tile(ta, &slice, &tm, &tn)) return;
@@ -247,34 +315,23 @@ gemm_kernel(Operands op, TileArgs ta) {
         y_batch = size_t(slice) * m * n;
     }
 
-    // Each operand's tile origin and how many rows / k values are in range.
     const _Float16* a_ptr;
     const _Float16* b_ptr;
-    size_t a_ld, b_ld;
-    size_t a_step, b_step;
+    size_t a_ld, b_ld, a_step, b_step;
     if (L == Layout::kTN) {      // x is k x m
-        a_ptr = x + size_t(k_begin) * m + m0; a_ld = m; a_step = size_t(kBK) * m;
+        a_ptr = x + size_t(k_begin) * m + m0; a_ld = m; a_step = size_t(BK) * m;
     } else {                     // x is m x k
-        a_ptr = x + size_t(m0) * op.k + k_begin; a_ld = op.k; a_step = kBK;
+        a_ptr = x + size_t(m0) * op.k + k_begin; a_ld = op.k; a_step = BK;
     }
     if (L == Layout::kNT) {      // w is n x k
-        b_ptr = w + size_t(n0) * op.k + k_begin; b_ld = op.k; b_step = kBK;
+        b_ptr = w + size_t(n0) * op.k + k_begin; b_ld = op.k; b_step = BK;
     } else {                     // w is k x n
-        b_ptr = w + size_t(k_begin) * n + n0; b_ld = n; b_step = size_t(kBK) * n;
+        b_ptr = w + size_t(k_begin) * n + n0; b_ld = n; b_step = size_t(BK) * n;
     }
     const int a_rows_valid = m - m0;
     const int b_rows_valid = n - n0;
-
-    TileA ta_regs;
-    TileB tb_regs;
     const int k_len = k_end - k_begin;
-    const int steps = (k_len + kBK - 1) / kBK;
-
-    ta_regs.load(a_ptr, a_ld, a_rows_valid, k_len, tid);
-    tb_regs.load(b_ptr, b_ld, b_rows_valid, k_len, tid);
-    ta_regs.store(lds_a[0], tid);
-    tb_regs.store(lds_b[0], tid);
-    __syncthreads();
+    const int steps = (k_len + BK - 1) / BK;
 
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -289,42 +346,102 @@ gemm_kernel(Operands op, TileArgs ta) {
 #pragma unroll
         for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
 
-    for (int s = 0; s < steps; ++s) {
-        const int cur = s & 1;
-        const bool more = s + 1 < steps;
-        if (more) {
-            const int k_left = k_len - (s + 1) * kBK;
-            ta_regs.load(a_ptr + (s + 1) * a_step, a_ld, a_rows_valid, k_left, tid);
-            tb_regs.load(b_ptr + (s + 1) * b_step, b_ld, b_rows_valid, k_left, tid);
+    // Fragment reads of k16 sub-step kk from LDS stage `st`.
+    auto read_frags = [&](int st, int kk, f16x8 (&xa)[FM], f16x8 (&wb)[FN]) {
+        const _Float16* la = lds[st];
+        const _Float16* lb = lds[st] + BM * BK;
+        const int chunk = kk * 2 + frag_chunk;
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+            const int row = wm * WTM + j * 32 + frag_row;
+            xa[j] = *reinterpret_cast<const f16x8*>(la + row * BK + swizzle<BK>(row, chunk) * 8);
         }
-        const _Float16* la = lds_a[cur];
-        const _Float16* lb = lds_b[cur];
 #pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            const int chunk = kk * 2 + frag_chunk;
-            f16x8 xa[FM];
-            f16x8 wb[FN];
-#pragma unroll
-            for (int j = 0; j < FM; ++j) {
-                const int row = wm * WTM + j * 32 + frag_row;
-                xa[j] = *reinterpret_cast<const f16x8*>(la + row * kBK + swizzle(row, chunk) * 8);
-            }
-#pragma unroll
-            for (int i = 0; i < FN; ++i) {
-                const int row = wn * WTN + i * 32 + frag_row;
-                wb[i] = *reinterpret_cast<const f16x8*>(lb + row * kBK + swizzle(row, chunk) * 8);
-            }
-#pragma unroll
-            for (int i = 0; i < FN; ++i)
-#pragma unroll
-                for (int j = 0; j < FM; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wb[i], xa[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < FN; ++i) {
+            const int row = wn * WTN + i * 32 + frag_row;
+            wb[i] = *reinterpret_cast<const f16x8*>(lb + row * BK + swizzle<BK>(row, chunk) * 8);
         }
-        if (more) {
-            ta_regs.store(lds_a[cur ^ 1], tid);
-            tb_regs.store(lds_b[cur ^ 1], tid);
+    };
+    // One k-step of MFMAs from LDS stage `st`. Fragments are double-buffered
+    // in registers: sub-step kk + 1's reads are issued before sub-step kk's
+    // MFMAs, and scheduling fences keep the compiler from sinking them back
+    // next to their uses (it otherwise reuses one register set and waits on
+    // every read). `between(kk)` runs after sub-step kk's MFMAs.
+    auto compute_step = [&](int st, auto&& between) {
+        f16x8 xa[2][FM];
+        f16x8 wb[2][FN];
+        read_frags(st, 0, xa[0], wb[0]);
+        // The first kLead MFMAs of sub-step kk go out before sub-step kk + 1's
+        // reads, so the wait those reads need lands behind the rest of kk's
+        // MFMAs rather than in front of them.
+        constexpr int kLead = FM * FN > 2 ? 2 : 1;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            const int cb = kk & 1;
+#pragma unroll
+            for (int q = 0; q < FM * FN; ++q) {
+                const int i = q / FM, j = q % FM;
+                if (q == kLead) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (kk + 1 < KK) read_frags(st, kk + 1, xa[cb ^ 1], wb[cb ^ 1]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wb[cb][i], xa[cb][j], acc[i][j],
+                                                                   0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            between(kk);
+        }
+    };
+
+    if constexpr (kDirect) {
+        // Tile t lives in stage t % STAGES and is issued STAGES - 1 steps ahead.
+        constexpr int kPer = LdsTile<BM, BK>::kInstr + LdsTile<BN, BK>::kInstr;
+        auto issue = [&](int t) {
+            _Float16* st = lds[t % STAGES];
+            LdsTile<BM, BK>::load(a_ptr + t * a_step, a_ld, (lds_half*)st, tid);
+            LdsTile<BN, BK>::load(b_ptr + t * b_step, b_ld, (lds_half*)(st + BM * BK), tid);
+        };
+#pragma unroll
+        for (int t = 0; t < STAGES - 1; ++t)
+            if (t < steps) issue(t);
+        for (int s = 0; s < steps; ++s) {
+            // Tile s has landed once only the tiles issued after it remain.
+            wait_tiles<kPer, STAGES - 2>(min(steps - 1 - s, STAGES - 2));
+            __syncthreads();   // tile s visible; stage (s - 1) % STAGES idle
+            if (s + STAGES - 1 < steps) issue(s + STAGES - 1);
+            compute_step(s % STAGES, [](int) {});
+        }
+    } else {
+        // Register-staged: tile s + 1 is written to the idle stage during
+        // sub-step 0 of step s, and tile s + 2's global loads go out after it.
+        TileA ta_regs;
+        TileB tb_regs;
+        ta_regs.load(a_ptr, a_ld, a_rows_valid, k_len, tid);
+        tb_regs.load(b_ptr, b_ld, b_rows_valid, k_len, tid);
+        ta_regs.store(lds[0], tid);
+        tb_regs.store(lds[0] + BM * BK, tid);
+        if (steps > 1) {
+            const int k_left = k_len - BK;
+            ta_regs.load(a_ptr + a_step, a_ld, a_rows_valid, k_left, tid);
+            tb_regs.load(b_ptr + b_step, b_ld, b_rows_valid, k_left, tid);
         }
         __syncthreads();
+        for (int s = 0; s < steps; ++s) {
+            const int cur = s & 1;
+            compute_step(cur, [&](int kk) {
+                if (kk == 0 && s + 1 < steps) {
+                    ta_regs.store(lds[cur ^ 1], tid);
+                    tb_regs.store(lds[cur ^ 1] + BM * BK, tid);
+                    if (s + 2 < steps) {
+                        const int k_left = k_len - (s + 2) * BK;
+                        ta_regs.load(a_ptr + (s + 2) * a_step, a_ld, a_rows_valid, k_left, tid);
+                        tb_regs.load(b_ptr + (s + 2) * b_step, b_ld, b_rows_valid, k_left, tid);
+                    }
+                }
+            });
+            __syncthreads();
+        }
     }
 
     // Store stage. Lane holds output row m0 + wm*WTM + j*32 + (lane & 31) and,
@@ -434,29 +551,72 @@ tn_reduce(float* __restrict__ y, const float* __restrict__ partials, size_t quad
 }
 
 struct Config {
-    int bm, bn, waves_m;
+    int bm, bn, bk, stages, waves_m;
 };
 
-// The macro-tile for an m x n output with `slices` independent slices,
-// minimising (whole waves of tiles over the CUs) x (tile cost), where a tile's
-// cost is its MFMA work over the tile shape's measured relative efficiency.
-Config pick_config(size_t m, size_t n, size_t slices, int cus) {
-    struct Cand { int bm, bn, wm; double eff; };
-    static const Cand cands[] = {
-        {256, 192, 2, 1.00}, {256, 128, 2, 0.95}, {128, 192, 2, 0.90},
-        {128, 128, 2, 0.80}, {128, 64, 4, 0.55}, {64, 128, 1, 0.55},
-    };
-    Config best{128, 128, 2};
+// Every instantiated tile configuration. `occ` is how many workgroups of it
+// share one CU (LDS and register limits), `eff` its measured throughput per
+// unit of tile area at that occupancy, relative to 128x192 (GPT-2 shapes at
+// 8,192 tokens on MI355X; the selector below uses both).
+struct Cand {
+    Config c;
+    int occ;
+    double eff;
+    bool pick;   // considered by the selector (the rest: FLINT_GEMM_CONFIG only)
+};
+constexpr Cand kCands[] = {
+    {{128, 192, 64, 2, 2}, 2, 1.00, true},  {{256, 192, 64, 2, 2}, 1, 0.93, true},
+    {{128, 128, 64, 2, 2}, 2, 0.92, true},  {{64, 128, 64, 2, 1}, 3, 0.70, true},
+    {{128, 64, 64, 2, 4}, 3, 0.70, true},   {{128, 256, 64, 2, 2}, 1, 0.90, true},
+    {{256, 128, 64, 2, 2}, 1, 0.85, false}, {{128, 192, 64, 3, 2}, 1, 0.80, false},
+    {{128, 128, 64, 4, 2}, 1, 0.70, false}, {{256, 192, 32, 4, 2}, 1, 0.85, false},
+    {{128, 192, 32, 4, 2}, 2, 0.90, false}, {{128, 192, 64, 0, 2}, 2, 1.00, false},
+    {{256, 192, 64, 0, 2}, 1, 0.90, false}, {{256, 256, 64, 2, 2}, 1, 0.85, false},
+};
+
+// FLINT_GEMM_CONFIG="bm,bn,bk,stages,waves_m" forces one of the instantiated
+// configurations (for tuning sweeps; read on every call so a sweep can change
+// it in-process); unset or unknown, the cost model below picks.
+bool forced_config(Config* out) {
+    const char* e = std::getenv("FLINT_GEMM_CONFIG");
+    if (e == nullptr) return false;
+    Config c{};
+    if (std::sscanf(e, "%d,%d,%d,%d,%d", &c.bm, &c.bn, &c.bk, &c.stages, &c.waves_m) != 5) {
+        return false;
+    }
+    for (const Cand& k : kCands) {
+        if (k.c.bm == c.bm && k.c.bn == c.bn && k.c.bk == c.bk && k.c.stages == c.stages &&
+            k.c.waves_m == c.waves_m) {
+            *out = c;
+            return true;
+        }
+    }
+    return false;
+}
+
+// The macro-tile for an m x n output with `slices` independent slices:
+// minimises (rounds of tiles over CUs x occupancy) x (tile area x occupancy /
+// efficiency). Epilogue-heavy GELU output prefers the 256x192 tile (one
+// workgroup per CU), and TN's transposed loads the 128x256 one.
+Config pick_config(size_t m, size_t n, size_t slices, int cus, bool gelu, bool tn) {
+    Config forced;
+    if (forced_config(&forced)) return forced;
+    Config best = kCands[0].c;
     double best_cost = 1e300;
-    for (const Cand& c : cands) {
+    for (const Cand& k : kCands) {
+        if (!k.pick) continue;
+        const Config& c = k.c;
         if (c.bn > 64 && n <= 64) continue;
+        double eff = k.eff;
+        if (gelu && c.bm == 256 && c.bn == 192) eff = 1.15;
+        if (tn && c.bm == 128 && c.bn == 256) eff = 1.15;
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn) *
                              double(slices);
-        const double waves = std::ceil(tiles / cus);
-        const double cost = waves * double(c.bm) * double(c.bn) / c.eff;
+        const double rounds = std::ceil(tiles / (double(cus) * k.occ));
+        const double cost = rounds * double(c.bm) * double(c.bn) * k.occ / eff;
         if (cost < best_cost * 0.999) {
             best_cost = cost;
-            best = Config{c.bm, c.bn, c.wm};
+            best = c;
         }
     }
     return best;
@@ -465,18 +625,26 @@ Config pick_config(size_t m, size_t n, size_t slices, int cus) {
 template <Layout L, Store S, bool CHECK>
 hipError_t dispatch(const Config& c, dim3 grid, const Operands& op, const TileArgs& ta,
                     hipStream_t stream) {
-#define FLINT_GEMM_CASE(BM_, BN_, WM_)                                                   \
-    if (c.bm == BM_ && c.bn == BN_ && c.waves_m == WM_) {                                \
-        hipLaunchKernelGGL((gemm_kernel<BM_, BN_, WM_, L, S, CHECK>), grid, dim3(kThreads), 0, \
-                           stream, op, ta);                                              \
-        return hipGetLastError();                                                        \
+#define FLINT_GEMM_CASE(BM_, BN_, BK_, ST_, WM_)                                          \
+    if (c.bm == BM_ && c.bn == BN_ && c.bk == BK_ && c.stages == ST_ && c.waves_m == WM_) { \
+        hipLaunchKernelGGL((gemm_kernel<BM_, BN_, BK_, ST_, WM_, L, S, CHECK>), grid,       \
+                           dim3(kThreads), 0, stream, op, ta);                               \
+        return hipGetLastError();                                                         \
     }
-    FLINT_GEMM_CASE(256, 192, 2)
-    FLINT_GEMM_CASE(256, 128, 2)
-    FLINT_GEMM_CASE(128, 192, 2)
-    FLINT_GEMM_CASE(128, 128, 2)
-    FLINT_GEMM_CASE(128, 64, 4)
-    FLINT_GEMM_CASE(64, 128, 1)
+    FLINT_GEMM_CASE(128, 192, 64, 2, 2)
+    FLINT_GEMM_CASE(256, 192, 64, 2, 2)
+    FLINT_GEMM_CASE(128, 128, 64, 2, 2)
+    FLINT_GEMM_CASE(64, 128, 64, 2, 1)
+    FLINT_GEMM_CASE(128, 64, 64, 2, 4)
+    FLINT_GEMM_CASE(128, 256, 64, 2, 2)
+    FLINT_GEMM_CASE(256, 128, 64, 2, 2)
+    FLINT_GEMM_CASE(128, 192, 64, 3, 2)
+    FLINT_GEMM_CASE(128, 128, 64, 4, 2)
+    FLINT_GEMM_CASE(256, 192, 32, 4, 2)
+    FLINT_GEMM_CASE(128, 192, 32, 4, 2)
+    FLINT_GEMM_CASE(128, 192, 64, 0, 2)
+    FLINT_GEMM_CASE(256, 192, 64, 0, 2)
+    FLINT_GEMM_CASE(256, 256, 64, 2, 2)
 #undef FLINT_GEMM_CASE
     return hipErrorInvalidValue;
 }
@@ -487,7 +655,8 @@ hipError_t run(Operands op, size_t slices, int split_len, hipStream_t stream) {
     if (hipError_t e = device_cus(&cus); e != hipSuccess) return e;
     const bool split = S == Store::kTn && op.partials != nullptr;
     // A TN split's tile shape is the one gemm_tn_splits planned with.
-    const Config c = pick_config(op.m, op.n, S == Store::kTn ? 1 : slices, cus);
+    const Config c = pick_config(op.m, op.n, S == Store::kTn ? 1 : slices, cus,
+                                 S == Store::kBiasGelu, L == Layout::kTN);
     TileArgs ta;
     ta.tiles_m = (op.m + c.bm - 1) / c.bm;
     ta.tiles_n = (op.n + c.bn - 1) / c.bn;
@@ -501,8 +670,8 @@ hipError_t run(Operands op, size_t slices, int split_len, hipStream_t stream) {
     const dim3 grid(gx, gy);
     // The unchecked kernel needs whole tiles and whole k-steps in every slice.
     const int k_piece = split ? split_len : op.k;
-    const bool exact = op.m % c.bm == 0 && op.n % c.bn == 0 && k_piece % kBK == 0 &&
-                       op.k % kBK == 0;
+    const bool exact = op.m % c.bm == 0 && op.n % c.bn == 0 && k_piece % c.bk == 0 &&
+                       op.k % c.bk == 0;
     return exact ? dispatch<L, S, false>(c, grid, op, ta, stream)
                  : dispatch<L, S, true>(c, grid, op, ta, stream);
 }
@@ -521,8 +690,8 @@ Operands make_ops(void* y, const void* x, const void* w, size_t m, size_t n, siz
 
 // TN's split of k. The count is the smallest that keeps at least 3/4 of the
 // CUs busy over all waves of tiles (or the fullest, up to 16 splits), each split
-// at least 1,024 long and a multiple of the 64-step; the last split takes the
-// rest. (Policy follows ref src/kernels/gemm.cu:737-784, with CUs for slots.)
+// at least 1,024 long and a multiple of 64; the last split takes the rest.
+// (Policy follows ref src/kernels/gemm.cu:737-784, with CUs for slots.)
 constexpr int kMinSplitK = 1024;
 constexpr int kMaxSplits = 16;
 
@@ -531,7 +700,7 @@ constexpr int kMaxSplits = 16;
 hipError_t gemm_tn_splits(size_t m, size_t n, size_t k, int* splits, int* split_len) {
     int cus = 256;
     if (hipError_t e = device_cus(&cus); e != hipSuccess) return e;
-    const Config c = pick_config(m, n, 1, cus);
+    const Config c = pick_config(m, n, 1, cus, false, true);
     const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn);
     const int most = std::min<int>(kMaxSplits, std::max<int>(1, int(k / kMinSplitK)));
     int want = 1;
@@ -550,7 +719,7 @@ hipError_t gemm_tn_splits(size_t m, size_t n, size_t k, int* splits, int* split_
         }
     }
     const size_t per = (k + want - 1) / want;
-    const size_t len = (per + kBK - 1) / kBK * kBK;
+    const size_t len = (per + 63) / 64 * 64;
     *split_len = int(len);
     *splits = int((k + len - 1) / len);
     return hipSuccess;
