@@ -43,7 +43,23 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--suite", type=str, default=None)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--calibrate-copy", type=int, default=0,
+                   help="only run flint_copy of this many bytes 5 times (PMC calibration)")
     return p.parse_args()
+
+
+TRAFFIC = ROOT / "profiles" / "gemm_nt_bias_gelu_8192x3072x768_traffic.md"
+
+
+def traffic_bytes():
+    """HBM bytes per launch of the dominant kernel, from the committed
+    FETCH_SIZE / WRITE_SIZE summary (a line `traffic_bytes_per_launch: N`)."""
+    if not TRAFFIC.is_file():
+        return None
+    for line in TRAFFIC.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def fused_workload(torch, dev, seed=0):
@@ -158,6 +174,14 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
     f = Flint()
+    if args.calibrate_copy:
+        src = torch.ones(args.calibrate_copy, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            f.copy(dst, src, args.calibrate_copy)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": args.calibrate_copy}))
+        return
     # Enough sets that the rotation exceeds the Infinity Cache.
     sets = [fused_workload(torch, dev, 0)]
     per_set = set_bytes(sets[0])
@@ -218,7 +242,8 @@ def main():
         "frac_of_peak": round(value / PEAK_FP16_TFLOPS, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-                     "traffic": None, "kernel": KERNELS[dom][0]},
+                     "traffic": traffic_bytes() if dom == 0 else None,
+                     "kernel": KERNELS[dom][0]},
         "kernels": kernels,
         "parity_max_rel_err": err,
         "rotation_sets": len(sets),

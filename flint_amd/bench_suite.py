@@ -13,7 +13,12 @@
     hipBLASLt, for plain GEMMs -- the reference's "% of cuBLAS" view) and in
     FP32 on the host CPU on a row sample, with the thread count stated.
 
-Used by `bench.py --suite PATH`; writes one JSON object per kernel.
+Used by `bench.py --suite PATH`, or directly:
+
+    python3 -m flint_amd.bench_suite --out suite.json [--only SUBSTRING]
+
+which writes one JSON object per kernel (`--only` keeps the kernels whose name
+contains SUBSTRING, e.g. for a rocprofv3 counter pass over one kernel).
 """
 
 import json
@@ -27,6 +32,7 @@ PEAK_TF = 2516.6
 PEAK_GBS = 8000.0
 CACHE = 256 << 20
 M, C, V, VP, T, H = 8192, 768, 50257, 50304, 1024, 12
+B = 8 * H   # attention batch: 8 sequences x 12 heads
 
 
 def _time_gpu(torch, fn, sets, rounds=5, per_round=None):
@@ -62,7 +68,7 @@ def _nsets(bytes_per_set):
     return max(1, math.ceil(2 * CACHE / max(bytes_per_set, 1)))
 
 
-def run(f, torch, dev, path):
+def run(f, torch, dev, path, only=None):
     import sys
 
     sys.path.insert(0, str(Path(__file__).resolve().parent.parent / "tests"))
@@ -72,6 +78,9 @@ def run(f, torch, dev, path):
     torch.set_num_threads(threads)
     F = torch.nn.functional
     out = []
+
+    def want(name):
+        return not only or only in name
 
     def record(name, kind, work, ms, cpu_s=None, cpu_work=None, peer_ms=None, note=""):
         if kind == "gemm":
@@ -97,6 +106,8 @@ def run(f, torch, dev, path):
 
     # ---------------------------------------------------------------- GEMMs
     def gemm_case(name, layout, epi, m, n, k, sample_rows=512):
+        if not want(name):
+            return
         flops = 2 * m * n * k
         per = (m * k + n * k) * 2 + m * n * (4 if epi in ("res", "tn") else 2) * (
             2 if epi in ("gelu", "res") else 1)
@@ -191,98 +202,132 @@ def run(f, torch, dev, path):
     gemm_case("flint_gemm_tn logits dW 50304x768x8192 (accumulate)", "tn", "tn", VP, C, M,
               sample_rows=128)
 
-    # Batched attention GEMMs, 96 heads x 1024 tokens x 64.
-    B = 8 * H
-    q = uniform((B, T, 64), 1).to(dev)
-    kk = uniform((B, T, 64), 2).to(dev)
-    s = torch.empty((B, T, T), dtype=torch.float16, device=dev)
-    ms = _time_gpu(torch, lambda st: f.gemm_nt_batched(s, q, kk, B, T, T, 64, 0.125), [0])
-    record("flint_gemm_nt_batched S=QK^T/8 96x1024x1024x64", "gemm", 2 * B * T * T * 64, ms,
-           note="HBM-bound: writes 201 MB")
-    p = uniform((B, T, T), 3).to(dev)
-    o = torch.empty((B, T, 64), dtype=torch.float16, device=dev)
-    ms = _time_gpu(torch, lambda st: f.gemm_nn_batched(o, p, kk, B, T, 64, T), [0])
-    record("flint_gemm_nn_batched O=PV 96x1024x64x1024", "gemm", 2 * B * T * T * 64, ms)
-    ms = _time_gpu(torch, lambda st: f.gemm_tn_batched(o, p, kk, B, T, 64, T), [0])
-    record("flint_gemm_tn_batched dV=P^T dO 96x1024x64x1024", "gemm", 2 * B * T * T * 64, ms)
-    del q, kk, s, p, o
-    torch.cuda.empty_cache()
+    def section_batched():
+        # Batched attention GEMMs, 96 heads x 1024 tokens x 64.
+        q = uniform((B, T, 64), 1).to(dev)
+        kk = uniform((B, T, 64), 2).to(dev)
+        s = torch.empty((B, T, T), dtype=torch.float16, device=dev)
+        ms = _time_gpu(torch, lambda st: f.gemm_nt_batched(s, q, kk, B, T, T, 64, 0.125), [0])
+        record("flint_gemm_nt_batched S=QK^T/8 96x1024x1024x64", "gemm", 2 * B * T * T * 64, ms,
+               note="HBM-bound: writes 201 MB")
+        p = uniform((B, T, T), 3).to(dev)
+        o = torch.empty((B, T, 64), dtype=torch.float16, device=dev)
+        ms = _time_gpu(torch, lambda st: f.gemm_nn_batched(o, p, kk, B, T, 64, T), [0])
+        record("flint_gemm_nn_batched O=PV 96x1024x64x1024", "gemm", 2 * B * T * T * 64, ms)
+        ms = _time_gpu(torch, lambda st: f.gemm_tn_batched(o, p, kk, B, T, 64, T), [0])
+        record("flint_gemm_tn_batched dV=P^T dO 96x1024x64x1024", "gemm", 2 * B * T * T * 64, ms)
+        del q, kk, s, p, o
+        torch.cuda.empty_cache()
 
     # ----------------------------------------------------------- reductions
     def red_sets(make, per_bytes):
         return [make(r) for r in range(_nsets(per_bytes))]
 
-    # LayerNorm forward 8192 x 768: x FP32 in, y FP16 + mean/rstd out.
-    ln_bytes = M * C * 4 + M * C * 2 + 2 * M * 4 + 2 * C * 4
-    sets = red_sets(lambda r: (normal((M, C), r).to(dev), torch.empty((M, C), dtype=torch.float16,
-                    device=dev), torch.empty(M, device=dev), torch.empty(M, device=dev)), ln_bytes)
-    g = (1 + normal((C,), 9, 0.1)).to(dev)
-    bta = normal((C,), 10, 0.1).to(dev)
-    ms = _time_gpu(torch, lambda st: f.layernorm_forward(st[1], st[2], st[3], st[0], g, bta, M, C),
-                   sets, per_round=64)
-    xc = sets[0][0][:2048].cpu()
-    cpu_s = _time_cpu(lambda: F.layer_norm(xc, (C,), g.cpu(), bta.cpu()))
-    record("flint_layernorm_forward 8192x768", "red", ln_bytes, ms, cpu_s, ln_bytes / 4)
-    # LayerNorm backward (accumulate_dx): dy FP16, x FP32, dx FP32 read+write.
-    lnb_bytes = M * C * 2 + M * C * 4 + M * C * 4 * 2 + 2 * M * 4 + 3 * C * 4
-    wsb = torch.empty(f.layernorm_backward_workspace(M, C), dtype=torch.uint8, device=dev)
-    dsets = [(normal((M, C), 20 + r, 1.0, torch.float16).to(dev), torch.zeros((M, C), device=dev))
-             for r in range(len(sets))]
-    dg = torch.zeros(C, device=dev)
-    db = torch.zeros(C, device=dev)
-    ms = _time_gpu(torch, lambda st: f.layernorm_backward(
-        st[1][1], dg, db, st[1][0], st[0][0], st[0][2], st[0][3], g, M, C, accumulate_dx=True,
-        workspace=wsb), list(zip(sets, dsets)), per_round=64)
-    record("flint_layernorm_backward 8192x768 (accumulate_dx)", "red", lnb_bytes, ms,
-           note="5 kernels: dbeta, dgamma (partials + finish each), dx")
-    bg_bytes = M * C * 2 + C * 4
-    wsg = torch.empty(f.bias_gradient_workspace(M, 4 * C), dtype=torch.uint8, device=dev)
-    dy3 = [normal((M, 4 * C), 30 + r, 1.0, torch.float16).to(dev) for r in range(4)]
-    dbias = torch.zeros(4 * C, device=dev)
-    ms = _time_gpu(torch, lambda st: f.bias_gradient(dbias, st, M, 4 * C, workspace=wsg), dy3,
-                   per_round=64)
-    record("flint_bias_gradient 8192x3072", "red", M * 4 * C * 2 + 4 * C * 4, ms)
-    del sets, dsets, dy3
-    torch.cuda.empty_cache()
+    def section_layernorm():
+        # LayerNorm forward 8192 x 768: x FP32 in, y FP16 + mean/rstd out.
+        ln_bytes = M * C * 4 + M * C * 2 + 2 * M * 4 + 2 * C * 4
+        sets = red_sets(lambda r: (normal((M, C), r).to(dev), torch.empty((M, C), dtype=torch.float16,
+                        device=dev), torch.empty(M, device=dev), torch.empty(M, device=dev)), ln_bytes)
+        g = (1 + normal((C,), 9, 0.1)).to(dev)
+        bta = normal((C,), 10, 0.1).to(dev)
+        ms = _time_gpu(torch, lambda st: f.layernorm_forward(st[1], st[2], st[3], st[0], g, bta, M, C),
+                       sets, per_round=64)
+        xc = sets[0][0][:2048].cpu()
+        cpu_s = _time_cpu(lambda: F.layer_norm(xc, (C,), g.cpu(), bta.cpu()))
+        record("flint_layernorm_forward 8192x768", "red", ln_bytes, ms, cpu_s, ln_bytes / 4)
+        # LayerNorm backward (accumulate_dx): dy FP16, x FP32, dx FP32 read+write.
+        lnb_bytes = M * C * 2 + M * C * 4 + M * C * 4 * 2 + 2 * M * 4 + 3 * C * 4
+        wsb = torch.empty(f.layernorm_backward_workspace(M, C), dtype=torch.uint8, device=dev)
+        dsets = [(normal((M, C), 20 + r, 1.0, torch.float16).to(dev), torch.zeros((M, C), device=dev))
+                 for r in range(len(sets))]
+        dg = torch.zeros(C, device=dev)
+        db = torch.zeros(C, device=dev)
+        ms = _time_gpu(torch, lambda st: f.layernorm_backward(
+            st[1][1], dg, db, st[1][0], st[0][0], st[0][2], st[0][3], g, M, C, accumulate_dx=True,
+            workspace=wsb), list(zip(sets, dsets)), per_round=64)
+        record("flint_layernorm_backward 8192x768 (accumulate_dx)", "red", lnb_bytes, ms,
+               note="5 kernels: dbeta, dgamma (partials + finish each), dx")
+        bg_bytes = M * C * 2 + C * 4
+        wsg = torch.empty(f.bias_gradient_workspace(M, 4 * C), dtype=torch.uint8, device=dev)
+        dy3 = [normal((M, 4 * C), 30 + r, 1.0, torch.float16).to(dev) for r in range(4)]
+        dbias = torch.zeros(4 * C, device=dev)
+        ms = _time_gpu(torch, lambda st: f.bias_gradient(dbias, st, M, 4 * C, workspace=wsg), dy3,
+                       per_round=64)
+        record("flint_bias_gradient 8192x3072", "red", M * 4 * C * 2 + 4 * C * 4, ms)
+        del sets, dsets, dy3
+        torch.cuda.empty_cache()
 
-    # Causal softmax 96 x 1024 x 1024 (visible half read, full write).
-    sm_bytes = B * (T * (T + 1) // 2) * 2 + B * T * T * 2
-    ss = [normal((B, T, T), 40 + r, 4.0, torch.float16).to(dev) for r in range(2)]
-    pp = [torch.empty((B, T, T), dtype=torch.float16, device=dev) for _ in range(2)]
-    ms = _time_gpu(torch, lambda st: f.causal_softmax_forward(pp[st], ss[st], B, T), [0, 1],
-                   per_round=16)
-    sc = ss[0][:4].float().cpu()
-    mask = torch.triu(torch.ones(T, T, dtype=torch.bool), 1)
-    cpu_s = _time_cpu(lambda: torch.softmax(sc.masked_fill(mask, float("-inf")), -1))
-    record("flint_causal_softmax_forward 96x1024x1024", "red", sm_bytes, ms, cpu_s,
-           sm_bytes * 4 / B)
-    smb_bytes = 2 * B * (T * (T + 1) // 2) * 2 + B * T * T * 2
-    ms = _time_gpu(torch, lambda st: f.causal_softmax_backward(ss[st], pp[st], ss[st], B, T,
-                                                               0.125), [0, 1], per_round=16)
-    record("flint_causal_softmax_backward 96x1024x1024 (in place)", "red", smb_bytes, ms)
-    del ss, pp
-    torch.cuda.empty_cache()
+    def section_softmax():
+        # Causal softmax 96 x 1024 x 1024 (visible half read, full write).
+        sm_bytes = B * (T * (T + 1) // 2) * 2 + B * T * T * 2
+        ss = [normal((B, T, T), 40 + r, 4.0, torch.float16).to(dev) for r in range(2)]
+        pp = [torch.empty((B, T, T), dtype=torch.float16, device=dev) for _ in range(2)]
+        ms = _time_gpu(torch, lambda st: f.causal_softmax_forward(pp[st], ss[st], B, T), [0, 1],
+                       per_round=16)
+        sc = ss[0][:4].float().cpu()
+        mask = torch.triu(torch.ones(T, T, dtype=torch.bool), 1)
+        cpu_s = _time_cpu(lambda: torch.softmax(sc.masked_fill(mask, float("-inf")), -1))
+        record("flint_causal_softmax_forward 96x1024x1024", "red", sm_bytes, ms, cpu_s,
+               sm_bytes * 4 / B)
+        smb_bytes = 2 * B * (T * (T + 1) // 2) * 2 + B * T * T * 2
+        ms = _time_gpu(torch, lambda st: f.causal_softmax_backward(ss[st], pp[st], ss[st], B, T,
+                                                                   0.125), [0, 1], per_round=16)
+        record("flint_causal_softmax_backward 96x1024x1024 (in place)", "red", smb_bytes, ms)
+        del ss, pp
+        torch.cuda.empty_cache()
 
-    # Softmax + cross-entropy 8192 x 50304 (vocab 50257).
-    ce_bytes = M * VP * 2 * 2 + M * 2 + M * 4
-    lg = normal((M, VP), 50, 2.0, torch.float16).to(dev)
-    _, t16 = targets(M, V, 51)
-    t16 = t16.to(dev)
-    dl = torch.empty_like(lg)
-    loss = torch.empty(M, device=dev)
-    ms = _time_gpu(torch, lambda st: f.softmax_cross_entropy(dl, loss, lg, t16, 0.125, M, V, VP),
-                   [0], per_round=8)
-    lc = lg[:256, :V].float().cpu()
-    tc = (t16[:256].long() & 0xFFFF).cpu()   # uint16 targets held in int16
+    def section_ce():
+        # Softmax + cross-entropy 8192 x 50304 (vocab 50257).
+        ce_bytes = M * VP * 2 * 2 + M * 2 + M * 4
+        lg = normal((M, VP), 50, 2.0, torch.float16).to(dev)
+        _, t16 = targets(M, V, 51)
+        t16 = t16.to(dev)
+        dl = torch.empty_like(lg)
+        loss = torch.empty(M, device=dev)
+        ms = _time_gpu(torch, lambda st: f.softmax_cross_entropy(dl, loss, lg, t16, 0.125, M, V, VP),
+                       [0], per_round=8)
+        lc = lg[:256, :V].float().cpu()
+        tc = (t16[:256].long() & 0xFFFF).cpu()   # uint16 targets held in int16
 
-    def ce_cpu():
-        l_ = lc.clone().requires_grad_(True)
-        F.cross_entropy(l_, tc, reduction="sum").backward()
+        def ce_cpu():
+            l_ = lc.clone().requires_grad_(True)
+            F.cross_entropy(l_, tc, reduction="sum").backward()
 
-    cpu_s = _time_cpu(ce_cpu)
-    record("flint_softmax_cross_entropy 8192x50304", "red", ce_bytes, ms, cpu_s,
-           ce_bytes * 256 / M, note="one set (824 MB logits) exceeds the cache")
-    del lg, dl
-    torch.cuda.empty_cache()
+        cpu_s = _time_cpu(ce_cpu)
+        record("flint_softmax_cross_entropy 8192x50304", "red", ce_bytes, ms, cpu_s,
+               ce_bytes * 256 / M, note="one set (824 MB logits) exceeds the cache")
+        del lg, dl
+        torch.cuda.empty_cache()
+
+    if any(want(x) for x in ("flint_gemm_nt_batched", "flint_gemm_nn_batched", "flint_gemm_tn_batched")):
+        section_batched()
+    if any(want(x) for x in ("flint_layernorm_forward", "flint_layernorm_backward", "flint_bias_gradient")):
+        section_layernorm()
+    if any(want(x) for x in ("flint_causal_softmax_forward", "flint_causal_softmax_backward")):
+        section_softmax()
+    if any(want(x) for x in ("flint_softmax_cross_entropy",)):
+        section_ce()
     Path(path).write_text(json.dumps(out, indent=1))
     return out
+
+
+def main():
+    import argparse
+    import sys
+
+    import torch
+
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+    from flint_amd.flint_lib import Flint
+
+    ap = argparse.ArgumentParser(description="Per-kernel measurement at the GPT-2 124M shapes.")
+    ap.add_argument("--out", default="suite.json")
+    ap.add_argument("--only", default=None, help="keep kernels whose name contains this")
+    a = ap.parse_args()
+    if not torch.cuda.is_available():
+        raise SystemExit("bench_suite needs a GPU")
+    run(Flint(), torch, torch.device("cuda:0"), a.out, a.only)
+
+
+if __name__ == "__main__":
+    main()
