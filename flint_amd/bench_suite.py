@@ -299,14 +299,75 @@ def run(f, torch, dev, path, only=None):
         del lg, dl
         torch.cuda.empty_cache()
 
-    if any(want(x) for x in ("flint_gemm_nt_batched", "flint_gemm_nn_batched", "flint_gemm_tn_batched")):
+    def section_support():
+        # flint_copy over 824 MB: the practical read+write HBM rate of this part,
+        # the ceiling the other bandwidth-bound kernels are read against.
+        if want("flint_copy"):
+            nb = M * VP * 2
+            src = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(2)]
+            for t_ in src:
+                t_.fill_(1)
+            dst = torch.empty(nb, dtype=torch.uint8, device=dev)
+            ms = _time_gpu(torch, lambda st: f.copy(dst, src[st], nb), [0, 1], per_round=8)
+            record("flint_copy 824 MB", "red", 2 * nb, ms,
+                   note="read + write; the practical HBM ceiling for the kernels below")
+            del src, dst
+        if want("flint_fp32_to_fp16"):
+            count = 124_475_904   # GPT-2 124M parameters, as synced each step
+            xs = [normal((count,), 60 + r).to(dev) for r in range(2)]
+            ys = torch.empty(count, dtype=torch.float16, device=dev)
+            ms = _time_gpu(torch, lambda st: f.fp32_to_fp16(ys, xs[st], count), [0, 1],
+                           per_round=8)
+            record("flint_fp32_to_fp16 124.5M", "red", count * 6, ms)
+            del xs, ys
+        if want("flint_heads_split") or want("flint_heads_merge"):
+            qkv = [uniform((M, 3 * C), 70 + r).to(dev) for r in range(4)]
+            hd = torch.empty((B, T, 64), dtype=torch.float16, device=dev)
+            ms = _time_gpu(torch, lambda st: f.heads_split(hd, st, 8, T, H, 64, 3 * C, C), qkv,
+                           per_round=16)
+            record("flint_heads_split k 8192x2304 -> 96x1024x64", "red", 2 * M * C * 2, ms)
+            ms = _time_gpu(torch, lambda st: f.heads_merge(st, hd, 8, T, H, 64, 3 * C, C), qkv,
+                           per_round=16)
+            record("flint_heads_merge 96x1024x64 -> 8192x2304", "red", 2 * M * C * 2, ms)
+            del qkv, hd
+        if want("flint_embedding"):
+            wte = normal((V, C), 80, 0.02).to(dev)
+            wpe = normal((T, C), 81, 0.01).to(dev)
+            tok32, tok16 = targets(M, V, 82)
+            tok16 = tok16.to(dev)
+            xs = [torch.empty((M, C), device=dev) for _ in range(4)]
+            emb_bytes = M * C * 4 * 2 + T * C * 4 + M * 2
+            ms = _time_gpu(torch, lambda st: f.embedding_forward(st, tok16, wte, wpe, 8, T, V, C),
+                           xs, per_round=16)
+            record("flint_embedding_forward 8192x768", "red", emb_bytes, ms)
+            distinct = int(torch.unique(tok32).numel())
+            dx = [normal((M, C), 83 + r).to(dev) for r in range(4)]
+            dwte = torch.zeros((V, C), device=dev)
+            dwpe = torch.zeros((T, C), device=dev)
+            ws = torch.empty(max(f.embedding_backward_workspace(8, T, V, C), 16),
+                             dtype=torch.uint8, device=dev)
+            ms = _time_gpu(torch, lambda st: f.embedding_backward(
+                dwte, dwpe, st, tok16, 8, T, V, C, accumulate_wte=True, accumulate_wpe=True,
+                workspace=ws), dx, per_round=16)
+            bwd_bytes = M * C * 4 + 2 * distinct * C * 4 + 2 * T * C * 4 + M * 2
+            record("flint_embedding_backward 8192x768 (accumulate)", "red", bwd_bytes, ms,
+                   note=f"{distinct} distinct tokens; rows read + written once")
+            del wte, wpe, xs, dx, dwte, dwpe, ws
+        torch.cuda.empty_cache()
+
+    if any(want(x) for x in ("flint_gemm_nt_batched", "flint_gemm_nn_batched",
+                             "flint_gemm_tn_batched")):
         section_batched()
-    if any(want(x) for x in ("flint_layernorm_forward", "flint_layernorm_backward", "flint_bias_gradient")):
+    if any(want(x) for x in ("flint_layernorm_forward", "flint_layernorm_backward",
+                             "flint_bias_gradient")):
         section_layernorm()
     if any(want(x) for x in ("flint_causal_softmax_forward", "flint_causal_softmax_backward")):
         section_softmax()
-    if any(want(x) for x in ("flint_softmax_cross_entropy",)):
+    if want("flint_softmax_cross_entropy"):
         section_ce()
+    if any(want(x) for x in ("flint_copy", "flint_fp32_to_fp16", "flint_heads_split",
+                             "flint_heads_merge", "flint_embedding")):
+        section_support()
     Path(path).write_text(json.dumps(out, indent=1))
     return out
 

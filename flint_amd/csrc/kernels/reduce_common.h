@@ -81,6 +81,15 @@ __device__ __forceinline__ float sum_reduce(float v) {
     return v;
 }
 
+// IEEE maximum (NaN-propagating) over `width` lanes.
+template <int WIDTH>
+__device__ __forceinline__ float maximum_reduce(float v) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off /= 2)
+        v = __builtin_elementwise_maximum(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
 template <int WIDTH>
 __device__ __forceinline__ float max_reduce(float v) {
 #pragma unroll

@@ -17,6 +17,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
+#include <cstdlib>
 #include <cstdint>
 
 #include "common/common.h"
@@ -135,66 +137,78 @@ layernorm_forward_any(_Float16* __restrict__ y, float* __restrict__ mean,
 
 constexpr int kChunkRows = int(kBiasGradientChunkRows);
 constexpr int kPhases = 8;   // row phases per chunk: thread y adds rows y, y+8, ...
-constexpr int kPieceCols = 8;  // 16 bytes of FP16
 
-// Partial (sum, error) pairs per 256-row chunk and column. One wave per block:
-// 8 pieces of 8 columns across, 8 row phases down. Thread (px, y) adds rows
-// y, y + 8, ... of the chunk in order; then phase 0 merges phases 1..7 in
-// order. With DGAMMA the values are dy * xhat, xhat = (x - mean) * rstd;
+constexpr int kTileCols = 64;   // one column per lane
+
+// Partial (sum, error) pairs per 256-row chunk and column, in the reference's
+// order (ref bias_gradient.cu:1-25, layernorm_backward.cu:120-200): for each
+// column, row phase y (0..7) adds rows y, y + 8, ... of the chunk in order,
+// then phase 0 merges phases 1..7 in order. With DGAMMA the values are
+// dy * xhat, xhat = (x - mean) * rstd, the product's rounding error kept;
 // otherwise dy. The chunk's sums go to workspace row 2c, its errors to 2c + 1.
+//
+// Workgroup = one chunk x 64 columns: wave y is phase y and lane l column l,
+// so a wave reads 128 B of dy (and 256 B of x) per row. A lane issues all of
+// its (up to 32) row loads before the first add: every workgroup keeps its
+// whole chunk slice in flight, which is what makes this pass bandwidth- rather
+// than latency-bound. Chunks run along grid x (up to 2^31 - 1 of them); column
+// tiles along grid y, strided past 65,535.
 template <bool DGAMMA>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(kPhases * 64)
 column_partials(float* __restrict__ partial, const _Float16* __restrict__ dy,
                 const float* __restrict__ x, const float* __restrict__ mean,
-                const float* __restrict__ rstd, size_t rows, int cols) {
-    __shared__ float sums[kPhases][8][kPieceCols];
-    __shared__ float errs[kPhases][8][kPieceCols];
-    const int px = threadIdx.x & 7;
-    const int ph = threadIdx.x >> 3;
-    const int pieces = cols / kPieceCols;
-    const int piece = blockIdx.x * 8 + px;
-    const size_t first = size_t(blockIdx.y) * kChunkRows;
-    const size_t end = rows - first < size_t(kChunkRows) ? rows : first + kChunkRows;
-    Comp acc[kPieceCols];
-    if (piece < pieces) {
-        for (size_t r = first + ph; r < end; r += kPhases) {
-            const h8 d = *reinterpret_cast<const h8*>(dy + r * cols + piece * kPieceCols);
-            if (DGAMMA) {
-                const float mu = mean[r];
-                const float rs = rstd[r];
-                const f4* xp = reinterpret_cast<const f4*>(x + r * cols + piece * kPieceCols);
-                const f4 x0 = xp[0];
-                const f4 x1 = xp[1];
+                const float* __restrict__ rstd, size_t rows, int cols, int tiles) {
+    constexpr int kPer = kChunkRows / kPhases;   // 32 rows per phase
+    __shared__ float sums[kPhases - 1][kTileCols];
+    __shared__ float errs[kPhases - 1][kTileCols];
+    const int lane = threadIdx.x & 63;
+    const int ph = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const size_t chunk = blockIdx.x;
+    const size_t first = chunk * kChunkRows;
+    const int count = rows - first < size_t(kChunkRows) ? int(rows - first) : kChunkRows;
+    const int n = count > ph ? (count - ph + kPhases - 1) / kPhases : 0;   // rows of this phase
+    for (int tile = blockIdx.y; tile < tiles; tile += gridDim.y) {
+        const int col = tile * kTileCols + lane;
+        const bool live = col < cols;
+        // Rows past the chunk's end and columns past cols load element 0
+        // instead (always valid) and are never added: no branch around the
+        // loads, so all of them issue before the first wait.
+        const size_t step = size_t(kPhases) * size_t(cols);
+        size_t at = (first + ph) * size_t(cols) + col;
+        _Float16 d[kPer];
+        float xv[kPer];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float xv = j < 4 ? x0[j] : x1[j - 4];
-                    comp_add_product(acc[j], float(d[j]), mul_rn(sub_rn(xv, mu), rs));
+        for (int k = 0; k < kPer; ++k) {
+            const size_t use = k < n && live ? at : 0;
+            d[k] = dy[use];
+            if (DGAMMA) xv[k] = x[use];
+            at += step;
+        }
+        Comp acc;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            if (k < n) {
+                if (DGAMMA) {
+                    const size_t r = first + ph + size_t(k) * kPhases;
+                    comp_add_product(acc, float(d[k]), mul_rn(sub_rn(xv[k], mean[r]), rstd[r]));
+                } else {
+                    comp_add(acc, float(d[k]));
                 }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) comp_add(acc[j], float(d[j]));
             }
         }
-    }
+        if (ph > 0) {
+            sums[ph - 1][lane] = acc.sum;
+            errs[ph - 1][lane] = acc.error;
+        }
+        __syncthreads();
+        if (ph == 0 && live) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        sums[ph][px][j] = acc[j].sum;
-        errs[ph][px][j] = acc[j].error;
+            for (int o = 0; o < kPhases - 1; ++o) comp_merge(acc, sums[o][lane], errs[o][lane]);
+            partial[chunk * 2 * cols + col] = acc.sum;
+            partial[(chunk * 2 + 1) * cols + col] = acc.error;
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    if (ph != 0 || piece >= pieces) return;
-    for (int o = 1; o < kPhases; ++o) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) comp_merge(acc[j], sums[o][px][j], errs[o][px][j]);
-    }
-    float* srow = partial + size_t(blockIdx.y) * 2 * cols + piece * kPieceCols;
-    float* erow = srow + cols;
-    f4* s4 = reinterpret_cast<f4*>(srow);
-    f4* e4 = reinterpret_cast<f4*>(erow);
-    s4[0] = f4{acc[0].sum, acc[1].sum, acc[2].sum, acc[3].sum};
-    s4[1] = f4{acc[4].sum, acc[5].sum, acc[6].sum, acc[7].sum};
-    e4[0] = f4{acc[0].error, acc[1].error, acc[2].error, acc[3].error};
-    e4[1] = f4{acc[4].error, acc[5].error, acc[6].error, acc[7].error};
 }
 
 // The merged value of a compensated sum. A non-finite sum is returned alone:
@@ -237,17 +251,17 @@ hipError_t launch_partials(bool dgamma, float* partial, const void* dy, const vo
                            const void* mean, const void* rstd, size_t rows, size_t cols,
                            hipStream_t stream) {
     const unsigned chunks = unsigned((rows + kChunkRows - 1) / kChunkRows);
-    const unsigned tiles = unsigned((cols / kPieceCols + 7) / 8);
-    const dim3 grid(tiles, chunks);
+    const int tiles = int((cols + kTileCols - 1) / kTileCols);
+    const dim3 grid(chunks, unsigned(std::min(tiles, 65535)));
     if (dgamma) {
-        hipLaunchKernelGGL(column_partials<true>, grid, dim3(64), 0, stream, partial,
+        hipLaunchKernelGGL(column_partials<true>, grid, dim3(kPhases * 64), 0, stream, partial,
                            static_cast<const _Float16*>(dy), static_cast<const float*>(x),
                            static_cast<const float*>(mean), static_cast<const float*>(rstd),
-                           rows, int(cols));
+                           rows, int(cols), tiles);
     } else {
-        hipLaunchKernelGGL(column_partials<false>, grid, dim3(64), 0, stream, partial,
+        hipLaunchKernelGGL(column_partials<false>, grid, dim3(kPhases * 64), 0, stream, partial,
                            static_cast<const _Float16*>(dy), nullptr, nullptr, nullptr, rows,
-                           int(cols));
+                           int(cols), tiles);
     }
     return hipGetLastError();
 }
@@ -473,70 +487,101 @@ causal_softmax_backward(h8* ds, const h8* __restrict__ p, const h8* dp, size_t r
 
 // --------------------------------------------------- softmax + cross-entropy
 
-constexpr int kCeThreads = 512;
-constexpr int kCeWaves = kCeThreads / 64;
-
-// One workgroup per row. Thread t holds vocab chunks t, t + 512, ... (up to
-// CPT of them) from a single HBM read: max, then e = exp(l - max) kept in
-// registers with a compensated sum (merged lane -> wave -> workgroup in a fixed
-// order), then dlogits = RN16(scale (e / sum - [c == target])) and
-// row_loss = log(sum) - (l_target - max).
-template <int CPT>
-__global__ void __launch_bounds__(kCeThreads)
+// One workgroup of THREADS per row; thread t holds vocab chunks t, t + THREADS,
+// ... (up to CPT of them) from a single HBM read, as FP16 (4 VGPRs a chunk).
+// Columns at or past vocab are loaded as -inf, so they drop out of the max and
+// add exp(-inf) = 0 to the sum.
+//   1. mx = max over the row: packed FP16 maximum per chunk, then wave and
+//      workgroup. The maximum propagates NaN (the reference's fmaxf skips it),
+//      which changes no output: a NaN logit makes the reference's sum, loss and
+//      every dlogit NaN through expf(NaN), and a NaN mx does the same here.
+//   2. sum = sum of e = exp(l - mx), as 2^((l - mx) log2 e) on v_exp_f32. The
+//      gap l - mx is exact for FP16 inputs, so the row's maximum gets e = 1
+//      exactly; elsewhere e is within about |l - mx| * 7e-8 relative plus an
+//      ulp. Each chunk's 8 values are added pairwise and the chunk total
+//      enters a compensated (TwoSum) sum, merged lane -> wave -> workgroup in
+//      a fixed order.
+//   3. e is formed again from the registers (cheaper than holding 8 FP32
+//      values a chunk, which would halve the rows in flight per CU), and
+//      dlogits = RN16(scale RN(RN(e / sum) - [c == target])), 0 past vocab;
+//      row_loss = log(sum) - (l_target - mx) when target < vocab
+//      (ref cross_entropy.cu:106-172 for the formulas).
+// Only the lane holding the target's chunk or the partial last chunk takes the
+// per-column branch.
+template <int THREADS, int CPT, bool POW2_SCALE>
+__global__ void __launch_bounds__(THREADS)
 softmax_cross_entropy(h8* __restrict__ dlogits, float* __restrict__ row_loss,
                       const h8* __restrict__ logits, const uint16_t* __restrict__ targets,
-                      float scale, int vocab, int cols) {
-    __shared__ float red_a[kCeWaves];
-    __shared__ float red_b[kCeWaves];
+                      float scale, float one, int vocab, int cols) {
+    constexpr int kWaves = THREADS / 64;
+    constexpr float kLog2e = 1.44269502162933349609375f;
+    __shared__ float red_a[kWaves];
+    __shared__ float red_b[kWaves];
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const size_t row = blockIdx.x;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int chunks = cols >> 3;
     const int vocab_chunks = (vocab + 7) >> 3;
+    const int last = vocab_chunks - 1;
+    const int last_count = vocab - last * 8;   // 1..8 values of the last chunk count
     const h8* lr = logits + row * chunks;
     h8* dr = dlogits + row * chunks;
+    const _Float16 neg_inf = -__builtin_huge_valf16();
 
-    float v[CPT][8];
-    float mx = -__builtin_huge_valf();
+    // l - mx rounded once, as an fma with the FP16 value as a mixed-precision
+    // operand (one v_fma_mix_f32); `one` is 1.0f passed at run time so that the
+    // compiler keeps the fma instead of a convert and a subtract.
+    float mx_g = 0.0f;
+    auto gap = [&](_Float16 l) { return __builtin_fmaf(float(l), one, -mx_g); };
+
+    h8 raw[CPT];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-        const int c = tid + i * kCeThreads;
-        if (c < vocab_chunks) {
-            unpack8(lr[c], v[i]);
-            const int cnt = min(vocab - c * 8, 8);
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (j < cnt) mx = fmaxf(mx, v[i][j]);
-        }
+        const int c = tid + i * THREADS;
+        raw[i] = c < vocab_chunks ? lr[c] : h8(neg_inf);
     }
-    mx = max_reduce<64>(mx);
+    if (last_count < 8 && last >= tid && (last - tid) % THREADS == 0) {
+        const int i = (last - tid) / THREADS;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k)
+            if (k == i) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (j >= last_count) raw[k][j] = neg_inf;
+            }
+    }
+
+    // 1. Row max.
+    h8 m8 = raw[0];
+#pragma unroll
+    for (int i = 1; i < CPT; ++i) m8 = __builtin_elementwise_maximum(m8, raw[i]);
+    h2 m2 = __builtin_elementwise_maximum(h2{m8[0], m8[1]}, h2{m8[2], m8[3]});
+    m2 = __builtin_elementwise_maximum(m2, __builtin_elementwise_maximum(h2{m8[4], m8[5]},
+                                                                          h2{m8[6], m8[7]}));
+    float mx = __builtin_elementwise_maximum(float(m2[0]), float(m2[1]));
+    mx = maximum_reduce<64>(mx);
     if (lane == 0) red_a[wave] = mx;
     __syncthreads();
     mx = red_a[0];
 #pragma unroll
-    for (int w = 1; w < kCeWaves; ++w) mx = fmaxf(mx, red_a[w]);
+    for (int w = 1; w < kWaves; ++w) mx = __builtin_elementwise_maximum(mx, red_a[w]);
     __syncthreads();
+    mx_g = mx;
 
-    const int target = targets[row];
-    float gap_t = 0.0f;
-    bool own_target = false;
+    // 2. Compensated sum of e.
     Comp s;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-        const int c = tid + i * kCeThreads;
+        const int c = tid + i * THREADS;
         if (c < vocab_chunks) {
-            const int cnt = min(vocab - c * 8, 8);
+            float e[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float gap = v[i][j] - mx;
-                if (j < cnt && c * 8 + j == target) {
-                    gap_t = gap;
-                    own_target = true;
-                }
-                v[i][j] = j < cnt ? exp_accurate(gap) : 0.0f;
-                if (j < cnt) comp_add(s, v[i][j]);
-            }
+            for (int j = 0; j < 8; ++j)
+                e[j] = __builtin_amdgcn_exp2f(mul_rn(gap(raw[i][j]), kLog2e));
+            comp_add(s, add_rn(add_rn(add_rn(e[0], e[1]), add_rn(e[2], e[3])),
+                               add_rn(add_rn(e[4], e[5]), add_rn(e[6], e[7]))));
         }
     }
     s = comp_reduce<64>(s);
@@ -549,29 +594,47 @@ softmax_cross_entropy(h8* __restrict__ dlogits, float* __restrict__ row_loss,
     tot.sum = red_a[0];
     tot.error = red_b[0];
 #pragma unroll
-    for (int w = 1; w < kCeWaves; ++w) comp_merge(tot, red_a[w], red_b[w]);
+    for (int w = 1; w < kWaves; ++w) comp_merge(tot, red_a[w], red_b[w]);
     const float sum = add_rn(tot.sum, tot.error);
     const float inv = __fdiv_rn(1.0f, sum);
-    if (own_target) row_loss[row] = sub_rn(logf(sum), gap_t);
+    // With a power-of-two scale, RN(RN(e inv) scale) = RN(e (inv scale)): both
+    // scalings are exact unless the value falls below FP32's normal range,
+    // far under FP16's smallest subnormal, where both round to 0 in FP16.
+    const float inv_scale = mul_rn(inv, scale);
+
+    // 3. Loss and dlogits.
+    const int target = targets[row];
+    if (tid == 0 && target < vocab) {
+        const float gap_t = gap(reinterpret_cast<const _Float16*>(lr)[target]);
+        row_loss[row] = sub_rn(logf(sum), gap_t);
+    }
+    const int tchunk = target >> 3;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-        const int c = tid + i * kCeThreads;
-        if (c < vocab_chunks) {
-            float o[8];
+        const int c = tid + i * THREADS;
+        if (c >= vocab_chunks) continue;
+        // An empty asm on the chunk keeps the compiler from carrying pass 2's
+        // FP32 gaps (8 VGPRs a chunk) over to here instead of the FP16 chunk.
+        asm volatile("" : "+v"(raw[i]));
+        float e[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float pj = mul_rn(v[i][j], inv);
-                if (c * 8 + j == target) pj = sub_rn(pj, 1.0f);
-                o[j] = mul_rn(pj, scale);
-            }
-            const int cnt = min(vocab - c * 8, 8);
+        for (int j = 0; j < 8; ++j) e[j] = __builtin_amdgcn_exp2f(mul_rn(gap(raw[i][j]), kLog2e));
+        float o[8];
+        if (c != tchunk && c != last) {
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                if (j >= cnt) o[j] = 0.0f;
-            dr[c] = pack8(o);
+                o[j] = POW2_SCALE ? mul_rn(e[j], inv_scale) : mul_rn(mul_rn(e[j], inv), scale);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float p = mul_rn(e[j], inv);
+                if (c * 8 + j == target) p = sub_rn(p, 1.0f);
+                o[j] = c * 8 + j < vocab ? mul_rn(p, scale) : 0.0f;
+            }
         }
+        dr[c] = pack8(o);
     }
-    for (int c = vocab_chunks + tid; c < chunks; c += kCeThreads) dr[c] = h8{};
+    for (int c = vocab_chunks + tid; c < chunks; c += THREADS) dr[c] = h8{};
 }
 
 }  // namespace
@@ -692,25 +755,51 @@ hipError_t launch_causal_softmax_backward(void* ds, const void* p, const void* d
 hipError_t launch_softmax_cross_entropy(void* dlogits, void* row_loss, const void* logits,
                                         const void* targets, float scale, size_t rows,
                                         size_t vocab, size_t cols, hipStream_t stream) {
-    const size_t vocab_chunks = (vocab + 7) / 8;
-    const size_t per = (vocab_chunks + kCeThreads - 1) / kCeThreads;
+    const size_t vc = (vocab + 7) / 8;
     auto* d = static_cast<h8*>(dlogits);
     auto* l = static_cast<float*>(row_loss);
     const auto* lg = static_cast<const h8*>(logits);
     const auto* tg = static_cast<const uint16_t*>(targets);
+    // FLINT_CE_THREADS=256|512|1024 forces the workgroup size (tuning sweeps);
+    // the chunks per thread follow from it.
+    int threads = vc <= 2048 ? 256 : 512;
+    if (const char* e = std::getenv("FLINT_CE_THREADS")) {
+        const int t = std::atoi(e);
+        if (t == 256 || t == 512 || t == 1024) threads = t;
+    }
+    const size_t per = (vc + threads - 1) / threads;
+    // A power of two (of either sign) in FP32's normal range.
+    int exp2_of_scale = 0;
+    const bool pow2 = std::isfinite(scale) && scale != 0.0f &&
+                      std::fabs(std::frexp(scale, &exp2_of_scale)) == 0.5f &&
+                      std::fpclassify(scale) == FP_NORMAL;
     // Grid x holds up to 2^31 - 1 rows per launch; larger row counts go in slices.
     for (size_t done = 0; done < rows;) {
         const size_t n = std::min<size_t>(rows - done, size_t{1} << 22);
-#define FLINT_CE(CPT)                                                                        \
-    hipLaunchKernelGGL(softmax_cross_entropy<CPT>, dim3(unsigned(n)), dim3(kCeThreads), 0,     \
-                       stream, d + done * (cols / 8), l + done, lg + done * (cols / 8),      \
-                       tg + done, scale, int(vocab), int(cols))
-        if (per <= 1) FLINT_CE(1);
-        else if (per <= 2) FLINT_CE(2);
-        else if (per <= 4) FLINT_CE(4);
-        else if (per <= 8) FLINT_CE(8);
-        else if (per <= 13) FLINT_CE(13);
-        else FLINT_CE(16);
+#define FLINT_CE(THREADS, CPT)                                                                   \
+    if (pow2)                                                                                    \
+        hipLaunchKernelGGL((softmax_cross_entropy<THREADS, CPT, true>), dim3(unsigned(n)),       \
+                           dim3(THREADS), 0, stream, d + done * (cols / 8), l + done,            \
+                           lg + done * (cols / 8), tg + done, scale, 1.0f, int(vocab),           \
+                           int(cols));                                                           \
+    else                                                                                         \
+        hipLaunchKernelGGL((softmax_cross_entropy<THREADS, CPT, false>), dim3(unsigned(n)),      \
+                           dim3(THREADS), 0, stream, d + done * (cols / 8), l + done,            \
+                           lg + done * (cols / 8), tg + done, scale, 1.0f, int(vocab),           \
+                           int(cols))
+#define FLINT_CE_PER(THREADS)                                                                    \
+    if (per <= 1) FLINT_CE(THREADS, 1);                                                          \
+    else if (per <= 2) FLINT_CE(THREADS, 2);                                                     \
+    else if (per <= 4) FLINT_CE(THREADS, 4);                                                     \
+    else if (per <= 8) FLINT_CE(THREADS, 8);                                                     \
+    else if (per <= 13) FLINT_CE(THREADS, 13);                                                   \
+    else if (per <= 16) FLINT_CE(THREADS, 16);                                                   \
+    else if (per <= 25) FLINT_CE(THREADS, 25);                                                   \
+    else FLINT_CE(THREADS, 32);
+        if (threads == 256) { FLINT_CE_PER(256) }
+        else if (threads == 512) { FLINT_CE_PER(512) }
+        else { FLINT_CE_PER(1024) }
+#undef FLINT_CE_PER
 #undef FLINT_CE
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
         done += n;

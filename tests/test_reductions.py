@@ -71,6 +71,19 @@ def test_bias_gradient(flint, cuda, rows, cols, accumulate):
     assert rel_err(out.cpu(), ref) <= 1e-5
 
 
+def test_bias_gradient_past_65535_chunks(flint, cuda):
+    """More chunks of 256 rows than a grid's y dimension holds (the reference's limits
+    cover rows up to 2^31 - 1 chunks): small-integer dy, so every sum is exact."""
+    rows, cols = 65536 * 256 + 77, 8
+    vals = (np.arange(rows * cols, dtype=np.int64) % 7 - 3).reshape(rows, cols)
+    vals[::3] *= -2
+    dy = torch.from_numpy(vals.astype(np.float16))
+    out = torch.full((cols,), float("nan"), device=cuda)
+    flint.bias_gradient(out, dy.to(cuda), rows, cols)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), vals.sum(0).astype(np.float32))
+
+
 @pytest.mark.parametrize("rows,cols", [(3, 8), (300, 24), (8192, 768), (100, 4096)])
 @pytest.mark.parametrize("acc", [False, True])
 def test_layernorm_backward(flint, cuda, rows, cols, acc):
@@ -177,6 +190,38 @@ def test_softmax_cross_entropy(flint, cuda, rows, vocab, cols):
     assert torch.all(d[torch.arange(len(pick)), tcol] <= 0)
     if cols > vocab:
         assert torch.all(dl.cpu()[:, vocab:] == 0)
+
+
+def test_cross_entropy_special_values(flint, cuda):
+    """NaN and infinities follow the reference's arithmetic (ref cross_entropy.cu:123-171):
+    a NaN or +inf logit makes the row's loss and every visible dlogit NaN, -inf logits add
+    exp(-inf) = 0, an all -inf row is NaN, and padding columns never matter."""
+    rows, vocab, cols = 6, 1001, 1008
+    logits = normal((rows, cols), 21, 2.0, torch.float16)
+    logits[0, 5] = float("nan")
+    logits[1, 17] = float("inf")
+    logits[2, 1::3] = float("-inf")
+    logits[3, :vocab] = float("-inf")
+    logits[4, vocab:] = float("nan")
+    logits[5, vocab - 1] = 30.0
+    t32 = torch.tensor([3, 9, 0, 4, 1000, 1000], dtype=torch.int32)
+    t16 = t32.to(torch.int16)
+    dl = torch.empty((rows, cols), dtype=torch.float16, device=cuda)
+    loss = torch.empty(rows, device=cuda)
+    flint.softmax_cross_entropy(dl, loss, logits.to(cuda), t16.to(cuda), 0.125, rows, vocab, cols)
+    torch.cuda.synchronize()
+    el, ed = oracle.cross_entropy(logits.numpy(), t32.numpy(), vocab, 0.125)
+    got_l = loss.cpu().numpy()
+    got_d = dl.cpu().float().numpy()
+    ed = ed.astype(np.float32)
+    assert np.array_equal(np.isnan(got_l), np.isnan(el)), (got_l, el)
+    assert np.isnan(got_l[[0, 1, 3]]).all() and np.isfinite(got_l[[2, 4, 5]]).all()
+    fin = np.isfinite(el)
+    assert np.allclose(got_l[fin], el[fin], rtol=1e-5, atol=0)
+    assert np.array_equal(np.isnan(got_d), np.isnan(ed))
+    assert (got_d[:, vocab:] == 0).all()
+    fin = np.isfinite(ed)
+    assert np.allclose(got_d[fin], ed[fin], rtol=2e-3, atol=6e-8)
 
 
 def test_cross_entropy_exact_cases(flint, cuda):
