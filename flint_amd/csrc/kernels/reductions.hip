@@ -138,8 +138,6 @@ layernorm_forward_any(_Float16* __restrict__ y, float* __restrict__ mean,
 constexpr int kChunkRows = int(kBiasGradientChunkRows);
 constexpr int kPhases = 8;   // row phases per chunk: thread y adds rows y, y+8, ...
 
-constexpr int kTileCols = 64;   // one column per lane
-
 // Partial (sum, error) pairs per 256-row chunk and column, in the reference's
 // order (ref bias_gradient.cu:1-25, layernorm_backward.cu:120-200): for each
 // column, row phase y (0..7) adds rows y, y + 8, ... of the chunk in order,
@@ -147,65 +145,89 @@ constexpr int kTileCols = 64;   // one column per lane
 // dy * xhat, xhat = (x - mean) * rstd, the product's rounding error kept;
 // otherwise dy. The chunk's sums go to workspace row 2c, its errors to 2c + 1.
 //
-// Workgroup = one chunk x 64 columns: wave y is phase y and lane l column l,
-// so a wave reads 128 B of dy (and 256 B of x) per row. A lane issues all of
-// its (up to 32) row loads before the first add: every workgroup keeps its
-// whole chunk slice in flight, which is what makes this pass bandwidth- rather
-// than latency-bound. Chunks run along grid x (up to 2^31 - 1 of them); column
-// tiles along grid y, strided past 65,535.
-template <bool DGAMMA>
+// Workgroup = one chunk x 64 * CPL columns: wave y is phase y, lane l holds
+// CPL adjacent columns, so a wave reads 128 * CPL B of dy (twice that of x) per
+// row. A lane issues all of its (up to 32) row loads before the first add:
+// every workgroup keeps its whole chunk slice in flight, which makes the pass
+// bandwidth- rather than latency-bound. Workgroup ids run over chunks first
+// (measured faster than tiles first on 8192 x 768 and 8192 x 3072).
+template <bool DGAMMA, int CPL>
 __global__ void __launch_bounds__(kPhases * 64)
 column_partials(float* __restrict__ partial, const _Float16* __restrict__ dy,
                 const float* __restrict__ x, const float* __restrict__ mean,
-                const float* __restrict__ rstd, size_t rows, int cols, int tiles) {
+                const float* __restrict__ rstd, size_t rows, int cols, size_t chunks,
+                size_t blocks) {
     constexpr int kPer = kChunkRows / kPhases;   // 32 rows per phase
-    __shared__ float sums[kPhases - 1][kTileCols];
-    __shared__ float errs[kPhases - 1][kTileCols];
+    constexpr int kTile = 64 * CPL;
+    typedef _Float16 hv __attribute__((ext_vector_type(CPL)));
+    typedef float fv __attribute__((ext_vector_type(CPL)));
+    __shared__ float sums[kPhases - 1][kTile];
+    __shared__ float errs[kPhases - 1][kTile];
     const int lane = threadIdx.x & 63;
     const int ph = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
-    const size_t chunk = blockIdx.x;
-    const size_t first = chunk * kChunkRows;
-    const int count = rows - first < size_t(kChunkRows) ? int(rows - first) : kChunkRows;
-    const int n = count > ph ? (count - ph + kPhases - 1) / kPhases : 0;   // rows of this phase
-    for (int tile = blockIdx.y; tile < tiles; tile += gridDim.y) {
-        const int col = tile * kTileCols + lane;
-        const bool live = col < cols;
+    for (size_t b = blockIdx.x; b < blocks; b += gridDim.x) {
+        const int tile = int(b / chunks);
+        const size_t chunk = b - size_t(tile) * chunks;
+        const size_t first = chunk * kChunkRows;
+        const int count = rows - first < size_t(kChunkRows) ? int(rows - first) : kChunkRows;
+        const int n = count > ph ? (count - ph + kPhases - 1) / kPhases : 0;
+        const int col = tile * kTile + lane * CPL;
+        const bool live = col < cols;   // cols is a multiple of 8, so of CPL
         // Rows past the chunk's end and columns past cols load element 0
         // instead (always valid) and are never added: no branch around the
         // loads, so all of them issue before the first wait.
         const size_t step = size_t(kPhases) * size_t(cols);
         size_t at = (first + ph) * size_t(cols) + col;
-        _Float16 d[kPer];
-        float xv[kPer];
+        hv d[kPer];
+        fv xv[kPer];
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const size_t use = k < n && live ? at : 0;
-            d[k] = dy[use];
-            if (DGAMMA) xv[k] = x[use];
+            d[k] = *reinterpret_cast<const hv*>(dy + use);
+            if (DGAMMA) xv[k] = *reinterpret_cast<const fv*>(x + use);
             at += step;
         }
-        Comp acc;
+        Comp acc[CPL];
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             if (k < n) {
                 if (DGAMMA) {
                     const size_t r = first + ph + size_t(k) * kPhases;
-                    comp_add_product(acc, float(d[k]), mul_rn(sub_rn(xv[k], mean[r]), rstd[r]));
+                    const float mu = mean[r];
+                    const float rs = rstd[r];
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j)
+                        comp_add_product(acc[j], float(d[k][j]),
+                                         mul_rn(sub_rn(xv[k][j], mu), rs));
                 } else {
-                    comp_add(acc, float(d[k]));
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) comp_add(acc[j], float(d[k][j]));
                 }
             }
         }
         if (ph > 0) {
-            sums[ph - 1][lane] = acc.sum;
-            errs[ph - 1][lane] = acc.error;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                sums[ph - 1][lane * CPL + j] = acc[j].sum;
+                errs[ph - 1][lane * CPL + j] = acc[j].error;
+            }
         }
         __syncthreads();
         if (ph == 0 && live) {
 #pragma unroll
-            for (int o = 0; o < kPhases - 1; ++o) comp_merge(acc, sums[o][lane], errs[o][lane]);
-            partial[chunk * 2 * cols + col] = acc.sum;
-            partial[(chunk * 2 + 1) * cols + col] = acc.error;
+            for (int o = 0; o < kPhases - 1; ++o) {
+#pragma unroll
+                for (int j = 0; j < CPL; ++j)
+                    comp_merge(acc[j], sums[o][lane * CPL + j], errs[o][lane * CPL + j]);
+            }
+            fv sv, ev;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                sv[j] = acc[j].sum;
+                ev[j] = acc[j].error;
+            }
+            *reinterpret_cast<fv*>(partial + chunk * 2 * cols + col) = sv;
+            *reinterpret_cast<fv*>(partial + (chunk * 2 + 1) * cols + col) = ev;
         }
         __syncthreads();
     }
@@ -250,19 +272,28 @@ column_finish(float* __restrict__ out, const float* __restrict__ partial, size_t
 hipError_t launch_partials(bool dgamma, float* partial, const void* dy, const void* x,
                            const void* mean, const void* rstd, size_t rows, size_t cols,
                            hipStream_t stream) {
-    const unsigned chunks = unsigned((rows + kChunkRows - 1) / kChunkRows);
-    const int tiles = int((cols + kTileCols - 1) / kTileCols);
-    const dim3 grid(chunks, unsigned(std::min(tiles, 65535)));
+    const size_t chunks = (rows + kChunkRows - 1) / kChunkRows;
+    // FLINT_PARTIALS_CPL=1|2 forces the columns per lane (tuning sweeps).
+    int cpl = 1;
+    if (const char* e = std::getenv("FLINT_PARTIALS_CPL")) cpl = std::atoi(e) == 2 ? 2 : 1;
+    const int tiles = int((cols + 64 * cpl - 1) / (64 * cpl));
+    const size_t blocks = chunks * size_t(tiles);
+    const dim3 grid(unsigned(std::min<size_t>(blocks, kMaxBlocks)));
+    const auto* dyh = static_cast<const _Float16*>(dy);
+    const auto* xf = static_cast<const float*>(x);
+    const auto* mf = static_cast<const float*>(mean);
+    const auto* rf = static_cast<const float*>(rstd);
+#define FLINT_PARTIALS(DG, CPL)                                                                 \
+    hipLaunchKernelGGL((column_partials<DG, CPL>), grid, dim3(kPhases * 64), 0, stream, partial, \
+                       dyh, xf, mf, rf, rows, int(cols), chunks, blocks)
     if (dgamma) {
-        hipLaunchKernelGGL(column_partials<true>, grid, dim3(kPhases * 64), 0, stream, partial,
-                           static_cast<const _Float16*>(dy), static_cast<const float*>(x),
-                           static_cast<const float*>(mean), static_cast<const float*>(rstd),
-                           rows, int(cols), tiles);
+        if (cpl == 1) FLINT_PARTIALS(true, 1);
+        else FLINT_PARTIALS(true, 2);
     } else {
-        hipLaunchKernelGGL(column_partials<false>, grid, dim3(kPhases * 64), 0, stream, partial,
-                           static_cast<const _Float16*>(dy), nullptr, nullptr, nullptr, rows,
-                           int(cols), tiles);
+        if (cpl == 1) FLINT_PARTIALS(false, 1);
+        else FLINT_PARTIALS(false, 2);
     }
+#undef FLINT_PARTIALS
     return hipGetLastError();
 }
 

@@ -319,6 +319,91 @@ class Flint:
             workspace_bytes, stream_handle(stream)))
 
 
+class Gpt2:
+    """A flint_gpt2 model through the C ABI (ref tests/flint_lib.py's Gpt2 helper):
+    parameters and gradients are (name, device address, rows, cols) and move in
+    and out of torch tensors with flint_copy."""
+
+    def __init__(self, flint, layers, heads, width, block_size, vocab, padded_vocab, sequences,
+                 length, separate_buffers=False, backward=True):
+        self.flint = flint
+        self.config = Gpt2Config(layers, heads, width, block_size, vocab, padded_vocab,
+                                 sequences, length, int(bool(separate_buffers)),
+                                 int(bool(backward)))
+        self.handle = P()
+        flint.check(flint.lib.flint_gpt2_create(ctypes.byref(self.config),
+                                                ctypes.byref(self.handle)))
+
+    def close(self):
+        if self.handle:
+            self.flint.lib.flint_gpt2_destroy(self.handle)
+            self.handle = P()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def bytes(self):
+        out = Z(0)
+        self.flint.check(self.flint.lib.flint_gpt2_bytes(ctypes.byref(self.config),
+                                                         ctypes.byref(out)))
+        return out.value
+
+    def _infos(self, fn):
+        n = self.flint.lib.flint_gpt2_parameter_count(self.handle)
+        out = []
+        for i in range(n):
+            info = Gpt2ParameterInfo()
+            self.flint.check(fn(self.handle, i, ctypes.byref(info)))
+            out.append((info.name.decode(), info.data, info.rows, info.cols))
+        return out
+
+    def parameters(self):
+        return self._infos(self.flint.lib.flint_gpt2_parameter)
+
+    def gradients(self):
+        return self._infos(self.flint.lib.flint_gpt2_gradient)
+
+    def write(self, address, tensor, stream=None):
+        """Copies a contiguous device tensor to a model address."""
+        self.flint.copy(address, tensor, tensor.numel() * tensor.element_size(), stream)
+
+    def read(self, address, shape, dtype, stream=None):
+        """A new device tensor holding a copy of model memory."""
+        import torch
+
+        out = torch.empty(shape, dtype=dtype, device="cuda")
+        self.flint.copy(out, address, out.numel() * out.element_size(), stream)
+        return out
+
+    def sync_weights(self, stream=None):
+        self.flint.check(self.flint.lib.flint_gpt2_sync_weights(self.handle,
+                                                                stream_handle(stream)))
+
+    def forward(self, tokens, targets, scale, stream=None):
+        self.flint.check(self.flint.lib.flint_gpt2_forward(
+            self.handle, pointer(tokens), pointer(targets), scale, stream_handle(stream)))
+
+    def backward(self, tokens, accumulate=False, stream=None):
+        self.flint.check(self.flint.lib.flint_gpt2_backward(
+            self.handle, pointer(tokens), int(bool(accumulate)), stream_handle(stream)))
+
+    def outputs(self):
+        """(logits, dlogits, row_loss) device addresses."""
+        lg, dl, rl = P(), P(), P()
+        self.flint.check(self.flint.lib.flint_gpt2_outputs(
+            self.handle, ctypes.byref(lg), ctypes.byref(dl), ctypes.byref(rl)))
+        return lg.value, dl.value, rl.value
+
+    def mean_loss(self, stream=None):
+        out = ctypes.c_double(0.0)
+        self.flint.check(self.flint.lib.flint_gpt2_mean_loss(self.handle, stream_handle(stream),
+                                                             ctypes.byref(out)))
+        return out.value
+
+
 def declared_functions(header=HEADER):
     """Names of every FLINT_API function the header declares."""
     import re

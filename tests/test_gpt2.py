@@ -1,0 +1,203 @@
+"""flint_gpt2: the assembled GPT-2 forward and backward passes through the C ABI
+(ref tests/test_gpt2.py, tests/test_gpt2_backward.py for the strategy).
+
+The whole-model gate follows the reference's: from identical FP32 master weights,
+with the FP32 CPU model (tests/gpt2_model.py) as the reference and an FP16 peer
+(the same model rounded to FP16 where the library stores FP16) beside it, the
+library's error against the reference must be at most 2x the peer's, by relative
+L2 and by max-abs (3x for the weight gradients), with a small absolute floor for
+outputs the peer gets almost exactly. It covers logits below vocab, each row's
+loss, dlogits and every master weight's gradient. The assembly's own checks follow:
+parameter names, order and shapes; mean_loss as the exact FP64 mean of row_loss;
+two runs bit-identical; one allocation and separate buffers giving the same bits;
+padded vocabulary rows getting zero gradient; accumulate adding one pass to the
+old gradients."""
+
+import numpy as np
+import pytest
+import torch
+
+import gpt2_model as G
+from flint_amd.flint_lib import FlintError, Gpt2
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(layers=2, heads=2, width=64, block_size=64, vocab=1000, padded_vocab=1024)
+ODD = dict(layers=1, heads=3, width=96, block_size=48, vocab=997, padded_vocab=1000)
+
+
+def _rel_l2(a, b):
+    return float(torch.linalg.vector_norm((a - b).double()) /
+                 max(float(torch.linalg.vector_norm(b.double())), 1e-30))
+
+
+def _rel_max(a, b):
+    return float((a - b).abs().max() / max(float(b.abs().max()), 1e-30))
+
+
+def _gate(name, got, ref, peer, factor, floor):
+    """got's error against ref within factor x peer's, by both measures."""
+    for measure in (_rel_l2, _rel_max):
+        e_got = measure(got, ref)
+        e_peer = measure(peer, ref)
+        bound = max(factor * e_peer, floor)
+        print(f"{name} {measure.__name__}: flint {e_got:.3e} peer {e_peer:.3e} bound {bound:.3e}")
+        assert e_got <= bound, f"{name}: {measure.__name__} {e_got:.3e} > {bound:.3e}"
+
+
+def _make(flint, cfg, sequences, length, separate=False, backward=True):
+    return Gpt2(flint, cfg["layers"], cfg["heads"], cfg["width"], cfg["block_size"],
+                cfg["vocab"], cfg["padded_vocab"], sequences, length, separate, backward)
+
+
+def _load(model, params):
+    for name, address, rows, cols in model.parameters():
+        t = params[name]
+        assert tuple(t.shape) == (rows, cols), name
+        model.write(address, t.contiguous().cuda())
+    model.sync_weights()
+
+
+def _tokens(cfg, sequences, length, seed):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.randint(0, cfg["vocab"], (sequences, length), generator=g)
+    tgt = torch.randint(0, cfg["vocab"], (sequences, length), generator=g)
+    return idx, tgt
+
+
+def _dev16(t):
+    return t.to(torch.int32).to(torch.int16).reshape(-1).cuda()
+
+
+def _run(flint, cfg, sequences, length, params, idx, tgt, scale, separate=False):
+    """(logits, row_loss, dlogits, grads, mean_loss) from the library, on the CPU."""
+    with _make(flint, cfg, sequences, length, separate) as model:
+        _load(model, params)
+        tok, trg = _dev16(idx), _dev16(tgt)
+        model.forward(tok, trg, scale)
+        model.backward(tok)
+        lg, dl, rl = model.outputs()
+        rows = sequences * length
+        pv = cfg["padded_vocab"]
+        logits = model.read(lg, (rows, pv), torch.float16).float().cpu()
+        dlogits = model.read(dl, (rows, pv), torch.float16).float().cpu()
+        row_loss = model.read(rl, (rows,), torch.float32).cpu()
+        grads = {n: model.read(a, (r, c), torch.float32).cpu()
+                 for n, a, r, c in model.gradients()}
+        mean = model.mean_loss()
+        torch.cuda.synchronize()
+    return logits, row_loss, dlogits, grads, mean
+
+
+@pytest.mark.parametrize("cfg,sequences,length", [(TINY, 2, 64), (TINY, 3, 32), (ODD, 2, 48)],
+                         ids=["tiny-2x64", "tiny-3x32", "odd-2x48"])
+@pytest.mark.parametrize("trained", [False, True], ids=["init", "trained"])
+def test_forward_and_backward_pass_the_gate(flint, cuda, cfg, sequences, length, trained):
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=5, trained=trained)
+    # Start from FP16-representable masters, so the FP16 copies equal them.
+    params = {n: t.half().float() for n, t in params.items()}
+    idx, tgt = _tokens(cfg, sequences, length, 6)
+    rows = sequences * length
+    scale = 1024.0 / rows
+    ref = G.gradients(params, idx, tgt, cfg, scale)
+    peer = G.gradients(params, idx, tgt, cfg, scale, fp16=True)
+    logits, row_loss, dlogits, grads, mean = _run(flint, cfg, sequences, length, params, idx,
+                                                  tgt, scale)
+    v = cfg["vocab"]
+    _gate("logits", logits[:, :v], ref[0], peer[0], 2.0, 1e-3)
+    _gate("row_loss", row_loss, ref[1], peer[1], 2.0, 1e-4)
+    _gate("dlogits", dlogits[:, :v], ref[2], peer[2], 2.0, 1e-3)
+    for name, g in grads.items():
+        _gate(name, g, ref[3][name], peer[3][name], 3.0, 2e-3)
+    # Padded vocabulary: zero logits from zero wte rows, zero dlogits and gradient rows.
+    assert (logits[:, v:] == 0).all() and (dlogits[:, v:] == 0).all()
+    assert (grads["wte.weight"][v:] == 0).all()
+    # Rows of wpe past length get +0.
+    assert (grads["wpe.weight"][length:] == 0).all()
+    # mean_loss is the FP64 mean of row_loss.
+    assert mean == pytest.approx(float(row_loss.double().mean()), rel=1e-15, abs=0)
+    assert abs(mean - float(ref[1].double().mean())) <= 1e-3 * abs(float(ref[1].mean()))
+
+
+def test_parameters_are_named_in_order(flint, cuda):
+    cfg = TINY
+    with _make(flint, cfg, 2, 64) as model:
+        got = [(n, r, c) for n, _, r, c in model.parameters()]
+        assert got == G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                         cfg["padded_vocab"])
+        assert [(n, r, c) for n, _, r, c in model.gradients()] == got
+
+
+def test_run_twice_and_separate_buffers_give_the_same_bits(flint, cuda):
+    cfg, sequences, length = TINY, 2, 64
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=7, trained=True)
+    idx, tgt = _tokens(cfg, sequences, length, 8)
+    a = _run(flint, cfg, sequences, length, params, idx, tgt, 0.125)
+    b = _run(flint, cfg, sequences, length, params, idx, tgt, 0.125)
+    c = _run(flint, cfg, sequences, length, params, idx, tgt, 0.125, separate=True)
+    for other in (b, c):
+        for x, y in zip(a[:3], other[:3]):
+            assert torch.equal(x.view(torch.int32) if x.dtype == torch.float32 else x,
+                               y.view(torch.int32) if y.dtype == torch.float32 else y)
+        for n in a[3]:
+            assert torch.equal(a[3][n].view(torch.int32), other[3][n].view(torch.int32)), n
+        assert a[4] == other[4]
+
+
+def test_backward_accumulate_adds_one_pass(flint, cuda):
+    """accumulate: every gradient gets this pass's added with one FP32 add, wte
+    with two (old + output layer's part) + the embedding's part, so only wte may
+    differ from old + fresh in the last bit (ref flint.h:530-545)."""
+    cfg, sequences, length = TINY, 2, 32
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=9, trained=True)
+    idx, tgt = _tokens(cfg, sequences, length, 10)
+    with _make(flint, cfg, sequences, length) as model:
+        _load(model, params)
+        tok, trg = _dev16(idx), _dev16(tgt)
+        model.forward(tok, trg, 0.25)
+        model.backward(tok)
+        fresh = {n: model.read(a, (r, c), torch.float32) for n, a, r, c in model.gradients()}
+        model.backward(tok, accumulate=True)
+        twice = {n: model.read(a, (r, c), torch.float32) for n, a, r, c in model.gradients()}
+        torch.cuda.synchronize()
+    for n in fresh:
+        expect = fresh[n] + fresh[n]
+        if n == "wte.weight":
+            assert torch.allclose(twice[n], expect, rtol=1e-6, atol=1e-12), n
+        elif n == "wpe.weight":
+            # Rows past length are left as they are (+0 from the first pass).
+            assert torch.equal(twice[n][:length], expect[:length]), n
+            assert (twice[n][length:] == 0).all()
+        else:
+            assert torch.equal(twice[n], expect), n
+
+
+def test_backward_needs_a_backward_model(flint, cuda):
+    cfg = TINY
+    with _make(flint, cfg, 1, 8, backward=False) as model:
+        tok = torch.zeros(8, dtype=torch.int16, device=cuda)
+        with pytest.raises(FlintError) as e:
+            model.backward(tok)
+        assert e.value.status == 1
+
+
+def test_mean_loss_of_equal_logits_is_log_vocab(flint, cuda):
+    """All-zero weights: every logit is 0, so each row's loss is log(vocab) exactly
+    as the kernel computes it (ref tests/test_cross_entropy.py:891-933)."""
+    cfg, sequences, length = TINY, 1, 16
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = {n: torch.zeros(r, c) for n, r, c in shapes}
+    for n in params:
+        if n.endswith("ln_1.weight") or n.endswith("ln_2.weight") or n == "ln_f.weight":
+            params[n] += 1
+    idx, tgt = _tokens(cfg, sequences, length, 11)
+    _, row_loss, _, _, mean = _run(flint, cfg, sequences, length, params, idx, tgt, 1.0)
+    assert np.allclose(row_loss.numpy(), np.log(cfg["vocab"]), rtol=1e-6)
+    assert mean == pytest.approx(np.log(cfg["vocab"]), rel=1e-6)
