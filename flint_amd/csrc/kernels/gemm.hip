@@ -49,7 +49,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) _Float16 lds_half;
 
-constexpr int kThreads = 256;
 
 enum class Layout { kNT, kNN, kTN };
 // What the kernel's store stage does. kTn writes FP32 (plain, accumulate or a
@@ -101,51 +100,94 @@ struct TileArgs {
     int split_len;            // TN: k per split (multiple of 64)
 };
 
-// Maps the linear workgroup id to (slice, tile_m, tile_n). Workgroup b runs on
-// XCD b % 8; the remap gives XCD x the contiguous range of logical ids
-// [x * total/8, (x+1) * total/8) when total is a multiple of 8. Within a slice,
-// tiles go in groups of group_m rows of tiles, column by column.
-__device__ __forceinline__ bool map_tile(const TileArgs& t, int* slice, int* tm, int* tn) {
+// Maps logical tile id `id` (< tiles_per_slice * slices) to (slice, tile_m,
+// tile_n). Workgroups run persistently: workgroup b takes ids b, b + G, b + 2G,
+// ... (G = grid size, a multiple of 8 when there are at least 8 ids), so id % 8
+// is the XCD the workgroup runs on (XCDs take workgroups round-robin). The
+// remap gives XCD x the contiguous range [x * total/8, (x+1) * total/8) of
+// tiles when total is a multiple of 8; within a slice, tiles go in groups of
+// group_m rows of tiles, column by column, for L2 reuse.
+__device__ __forceinline__ void map_tile(const TileArgs& t, unsigned id, int* slice, int* tm,
+                                         int* tn) {
     const unsigned total = unsigned(t.tiles_per_slice) * unsigned(t.slices);
-    unsigned bid = blockIdx.x + blockIdx.y * gridDim.x;
-    if (bid >= total) return false;
-    if ((total & 7u) == 0) bid = (bid & 7u) * (total >> 3) + (bid >> 3);
-    *slice = int(bid / unsigned(t.tiles_per_slice));
-    const int id = int(bid % unsigned(t.tiles_per_slice));
+    if ((total & 7u) == 0) id = (id & 7u) * (total >> 3) + (id >> 3);
+    *slice = int(id / unsigned(t.tiles_per_slice));
+    const int in_slice = int(id % unsigned(t.tiles_per_slice));
     const int per_group = t.group_m * t.tiles_n;
-    const int group = id / per_group;
+    const int group = in_slice / per_group;
     const int first_m = group * t.group_m;
     const int rows = min(t.tiles_m - first_m, t.group_m);
-    const int in_group = id - group * per_group;
+    const int in_group = in_slice - group * per_group;
     *tm = first_m + in_group % rows;
     *tn = in_group / rows;
-    return true;
 }
 
-// Streams a ROWS x BK tile of a k-contiguous matrix (row r at base + r*ld)
-// straight into LDS with global_load_lds_dwordx4. Instruction i of wave w
-// fills 1 KB of LDS, rows [(4i + w) R, +R) with R = 512 / BK; lane l writes
-// the 16 bytes at position l % C of row l / C (C = BK / 8 chunks a row), so
-// it loads the global chunk the swizzle puts there.
-template <int ROWS, int BK>
+// Streams a ROWS x BK tile of a k-contiguous matrix straight into LDS with
+// buffer_load_dwordx4 ... lds. The buffer resource covers the tile's rows (base
+// = its first row, every k); the k-step goes in the scalar offset, so a lane's
+// address is one 32-bit vector offset computed once. Instruction i of wave w
+// fills 1 KB of LDS, rows [(4i + w) R, +R) with R = 512 / BK; lane l writes the
+// 16 bytes at position l % C of row l / C (C = BK / 8 chunks a row), so it
+// loads the global chunk the swizzle puts there.
+// (Buffer rather than global addressing: on MI355X the global form stalled the
+// address unit on the L1 for a large share of the GEMM's cycles.)
+// A wave-uniform pointer held in scalar registers (buffer resources need one).
+__device__ __forceinline__ _Float16* uniform_ptr(const _Float16* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+    return reinterpret_cast<_Float16*>((uint64_t(hi) << 32) | lo);
+}
+
+template <int ROWS, int BK, int THREADS>
 struct LdsTile {
+    static constexpr int kWaves = THREADS / 64;
     static constexpr int kC = BK / 8;
     static constexpr int kRowsPerInstr = 64 / kC;
-    static constexpr int kInstr = ROWS * kC / kThreads;   // per thread
-    static_assert(ROWS * kC % kThreads == 0, "whole wave instructions");
+    static constexpr int kInstr = ROWS * kC / THREADS;   // per thread
+    static_assert(ROWS * kC % THREADS == 0, "whole wave instructions");
 
-    __device__ __forceinline__ static void load(const _Float16* __restrict__ base, size_t ld,
-                                                lds_half* lds, int tid) {
+    _Float16* base;
+    unsigned voff[kInstr];
+
+    __device__ __forceinline__ void init(const _Float16* tile_base, size_t ld, int tid) {
+        base = uniform_ptr(tile_base);
         const int lane = tid & 63;
         const int wave = tid >> 6;
 #pragma unroll
         for (int i = 0; i < kInstr; ++i) {
-            const int row0 = (i * 4 + wave) * kRowsPerInstr;
-            const int row = row0 + lane / kC;
+            const int row = (i * kWaves + wave) * kRowsPerInstr + lane / kC;
             const int kc = swizzle<BK>(row, lane % kC);
-            __builtin_amdgcn_global_load_lds(base + size_t(row) * ld + kc * 8, lds + row0 * BK,
-                                             16, 0, 0);
+            voff[i] = unsigned((size_t(row) * ld + kc * 8) * sizeof(_Float16));
         }
+    }
+    // Instruction i of load(): k columns [k0, k0 + BK) of its rows.
+    __device__ __forceinline__ void load_one(int i, int k0, lds_half* lds, int tid) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+        const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+        const int row0 = (i * kWaves + (tid >> 6)) * kRowsPerInstr;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsrc, (__attribute__((address_space(3))) void*)(lds + row0 * BK), 16, voff[i],
+            unsigned(k0) * 2u, 0, 0);
+#endif
+    }
+    // Loads k columns [k0, k0 + BK) (k0 in elements) into `lds`.
+    __device__ __forceinline__ void load(int k0, lds_half* lds, int tid) const {
+        // The host pass of this file never runs kernel code; it only has to
+        // see a kernel it can emit a launch stub for, which the buffer-resource
+        // builtins (device-only types) would prevent.
+#if defined(__HIP_DEVICE_COMPILE__)
+        // 0x00020000: 32-bit data format, the raw-buffer word 3 of gfx9 parts.
+        const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+        const int wave = tid >> 6;
+#pragma unroll
+        for (int i = 0; i < kInstr; ++i) {
+            const int row0 = (i * kWaves + wave) * kRowsPerInstr;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsrc, (__attribute__((address_space(3))) void*)(lds + row0 * BK), 16, voff[i],
+                unsigned(k0) * 2u, 0, 0);
+        }
+#endif
     }
 };
 
@@ -170,19 +212,19 @@ __device__ __forceinline__ void wait_tiles(int tiles) {
 
 // Copies a ROWS x BK tile of a k-contiguous matrix into LDS rows through
 // registers (16-byte chunks), with optional bounds checks.
-template <int ROWS, int BK, bool CHECK>
+template <int ROWS, int BK, bool CHECK, int THREADS>
 struct DirectTile {
     static constexpr int kC = BK / 8;
     static constexpr int kChunks = ROWS * kC;
-    static constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
+    static constexpr int kPer = (kChunks + THREADS - 1) / THREADS;
     f16x8 r[kPer];
 
     __device__ __forceinline__ void load(const _Float16* __restrict__ base, size_t ld,
                                          int rows_valid, int k_valid, int tid) {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const int c = tid + i * kThreads;
-            if (kChunks % kThreads != 0 && c >= kChunks) continue;
+            const int c = tid + i * THREADS;
+            if (kChunks % THREADS != 0 && c >= kChunks) continue;
             const int row = c / kC;
             const int kc = c % kC;
             const _Float16* p = base + size_t(row) * ld + kc * 8;
@@ -197,8 +239,8 @@ struct DirectTile {
     __device__ __forceinline__ void store(_Float16* lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const int c = tid + i * kThreads;
-            if (kChunks % kThreads != 0 && c >= kChunks) continue;
+            const int c = tid + i * THREADS;
+            if (kChunks % THREADS != 0 && c >= kChunks) continue;
             const int row = c / kC;
             const int kc = c % kC;
             *reinterpret_cast<f16x8*>(lds + row * BK + swizzle<BK>(row, kc) * 8) = r[i];
@@ -210,19 +252,19 @@ struct DirectTile {
 // index (element (k, c) at base + k*ld + c) into ROWS LDS rows of BK k values:
 // 8x8 blocks of halves are read as 8 rows of 16 bytes and transposed in
 // registers.
-template <int ROWS, int BK, bool CHECK>
+template <int ROWS, int BK, bool CHECK, int THREADS>
 struct TransposedTile {
     static constexpr int kColBlocks = ROWS / 8;
     static constexpr int kBlocks = kColBlocks * (BK / 8);
-    static constexpr int kPer = (kBlocks + kThreads - 1) / kThreads;
+    static constexpr int kPer = (kBlocks + THREADS - 1) / THREADS;
     f16x8 r[kPer][8];
 
     __device__ __forceinline__ void load(const _Float16* __restrict__ base, size_t ld,
                                          int cols_valid, int k_valid, int tid) {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const int b = tid + i * kThreads;
-            if (kBlocks % kThreads != 0 && b >= kBlocks) continue;
+            const int b = tid + i * THREADS;
+            if (kBlocks % THREADS != 0 && b >= kBlocks) continue;
             const int cb = b % kColBlocks;
             const int kb = b / kColBlocks;
 #pragma unroll
@@ -242,8 +284,8 @@ struct TransposedTile {
     __device__ __forceinline__ void store(_Float16* lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const int b = tid + i * kThreads;
-            if (kBlocks % kThreads != 0 && b >= kBlocks) continue;
+            const int b = tid + i * THREADS;
+            if (kBlocks % THREADS != 0 && b >= kBlocks) continue;
             const int cb = b % kColBlocks;
             const int kb = b / kColBlocks;
 #pragma unroll
@@ -270,10 +312,20 @@ struct Operands {
     int m, n, k;
 };
 
-template <int BM, int BN, int BK, int STAGES, int WAVES_M, Layout L, Store S, bool CHECK>
-__global__ void __launch_bounds__(kThreads)
+// Registers a lane may hold: 512 (one wave per SIMD) when its accumulators
+// alone take 192 or more, else 256 (two waves per SIMD, or two workgroups).
+template <int BM, int BN, int WAVES_M, int NW>
+constexpr int waves_per_simd() {
+    return NW == 8 || (BM / WAVES_M) * (BN / (NW / WAVES_M)) / 64 < 192 ? 2 : 1;
+}
+
+// NW wave64s per workgroup (4 or 8) in a WAVES_M x (NW / WAVES_M) grid.
+template <int BM, int BN, int BK, int STAGES, int WAVES_M, int NW, Layout L, Store S, bool CHECK>
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(waves_per_simd<BM, BN, WAVES_M, NW>())))
 gemm_kernel(Operands op, TileArgs ta) {
-    constexpr int WAVES_N = 4 / WAVES_M;
+    constexpr int kThreads = NW * 64;
+    constexpr int WAVES_N = NW / WAVES_M;
     constexpr int WTM = BM / WAVES_M;   // wave tile rows (m)
     constexpr int WTN = BN / WAVES_N;   // wave tile cols (n)
     constexpr int FM = WTM / 32;
@@ -285,53 +337,20 @@ gemm_kernel(Operands op, TileArgs ta) {
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tiles are whole 32x32 MFMA blocks");
     static_assert(kStages >= 2, "at least double buffering");
 
-    using TileA = typename std::conditional<L == Layout::kTN, TransposedTile<BM, BK, CHECK>,
-                                            DirectTile<BM, BK, CHECK>>::type;
-    using TileB = typename std::conditional<L == Layout::kNT, DirectTile<BN, BK, CHECK>,
-                                            TransposedTile<BN, BK, CHECK>>::type;
+    using TileA =
+        typename std::conditional<L == Layout::kTN, TransposedTile<BM, BK, CHECK, kThreads>,
+                                  DirectTile<BM, BK, CHECK, kThreads>>::type;
+    using TileB =
+        typename std::conditional<L == Layout::kNT, DirectTile<BN, BK, CHECK, kThreads>,
+                                  TransposedTile<BN, BK, CHECK, kThreads>>::type;
 
     // Stage s: A tile (BM rows) then B tile (BN rows), BK halves per row.
     __shared__ __attribute__((aligned(16))) _Float16 lds[kStages][(BM + BN) * BK];
 
-    int slice, tm, tn;
-    if (!map_tile(ta, &slice, &tm, &tn)) return;
-
     const int tid = threadIdx.x;
     const int m = op.m, n = op.n;
-    const int m0 = tm * BM;
-    const int n0 = tn * BN;
-
-    // Slice: a batch (offset every operand) or a TN split of k.
-    const _Float16* x = op.x;
-    const _Float16* w = op.w;
-    int k_begin = 0, k_end = op.k;
-    size_t y_batch = 0;
-    if (S == Store::kTn && op.partials != nullptr) {
-        k_begin = slice * ta.split_len;
-        k_end = min(op.k, k_begin + ta.split_len);
-    } else if (ta.slices > 1) {
-        x += size_t(slice) * m * op.k;
-        w += size_t(slice) * n * op.k;
-        y_batch = size_t(slice) * m * n;
-    }
-
-    const _Float16* a_ptr;
-    const _Float16* b_ptr;
-    size_t a_ld, b_ld, a_step, b_step;
-    if (L == Layout::kTN) {      // x is k x m
-        a_ptr = x + size_t(k_begin) * m + m0; a_ld = m; a_step = size_t(BK) * m;
-    } else {                     // x is m x k
-        a_ptr = x + size_t(m0) * op.k + k_begin; a_ld = op.k; a_step = BK;
-    }
-    if (L == Layout::kNT) {      // w is n x k
-        b_ptr = w + size_t(n0) * op.k + k_begin; b_ld = op.k; b_step = BK;
-    } else {                     // w is k x n
-        b_ptr = w + size_t(k_begin) * n + n0; b_ld = n; b_step = size_t(BK) * n;
-    }
-    const int a_rows_valid = m - m0;
-    const int b_rows_valid = n - n0;
-    const int k_len = k_end - k_begin;
-    const int steps = (k_len + BK - 1) / BK;
+    const unsigned total = unsigned(ta.tiles_per_slice) * unsigned(ta.slices);
+    if (blockIdx.x >= total) return;
 
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -340,11 +359,51 @@ gemm_kernel(Operands op, TileArgs ta) {
     const int frag_row = lane & 31;
     const int frag_chunk = lane >> 5;
 
+    // A tile's place: its slice (a batch, or a TN split of k), output corner,
+    // operand pointers at its first k and its k range.
+    struct Geo {
+        int slice, m0, n0, k_len;
+        size_t y_batch;
+        const _Float16* a;
+        const _Float16* b;
+    };
+    size_t a_ld, b_ld, a_step, b_step;
+    if (L == Layout::kTN) { a_ld = m; a_step = size_t(BK) * m; }
+    else { a_ld = op.k; a_step = BK; }
+    if (L == Layout::kNT) { b_ld = op.k; b_step = BK; }
+    else { b_ld = n; b_step = size_t(BK) * n; }
+    auto geo = [&](unsigned id) {
+        Geo g;
+        int tm, tn;
+        map_tile(ta, id, &g.slice, &tm, &tn);
+        g.m0 = tm * BM;
+        g.n0 = tn * BN;
+        const _Float16* x = op.x;
+        const _Float16* w = op.w;
+        int k_begin = 0, k_end = op.k;
+        g.y_batch = 0;
+        if (S == Store::kTn && op.partials != nullptr) {
+            k_begin = g.slice * ta.split_len;
+            k_end = min(op.k, k_begin + ta.split_len);
+        } else if (ta.slices > 1) {
+            x += size_t(g.slice) * m * op.k;
+            w += size_t(g.slice) * n * op.k;
+            g.y_batch = size_t(g.slice) * m * n;
+        }
+        g.a = L == Layout::kTN ? x + size_t(k_begin) * m + g.m0 : x + size_t(g.m0) * op.k + k_begin;
+        g.b = L == Layout::kNT ? w + size_t(g.n0) * op.k + k_begin : w + size_t(k_begin) * n + g.n0;
+        g.k_len = k_end - k_begin;
+        return g;
+    };
+
     f32x16 acc[FN][FM];
+    auto zero_acc = [&]() {
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
+        for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
+            for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
+    };
+    zero_acc();
 
     // Fragment reads of k16 sub-step kk from LDS stage `st`.
     auto read_frags = [&](int st, int kk, f16x8 (&xa)[FM], f16x8 (&wb)[FN]) {
@@ -367,7 +426,7 @@ gemm_kernel(Operands op, TileArgs ta) {
     // MFMAs, and scheduling fences keep the compiler from sinking them back
     // next to their uses (it otherwise reuses one register set and waits on
     // every read). `between(kk)` runs after sub-step kk's MFMAs.
-    auto compute_step = [&](int st, auto&& between) {
+    auto compute_step = [&](int st, auto&& between, auto&& early) {
         f16x8 xa[2][FM];
         f16x8 wb[2][FN];
         read_frags(st, 0, xa[0], wb[0]);
@@ -384,6 +443,7 @@ gemm_kernel(Operands op, TileArgs ta) {
                 if (q == kLead) {
                     __builtin_amdgcn_sched_barrier(0);
                     if (kk + 1 < KK) read_frags(st, kk + 1, xa[cb ^ 1], wb[cb ^ 1]);
+                    early(kk);
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wb[cb][i], xa[cb][j], acc[i][j],
@@ -394,142 +454,227 @@ gemm_kernel(Operands op, TileArgs ta) {
         }
     };
 
-    if constexpr (kDirect) {
-        // Tile t lives in stage t % STAGES and is issued STAGES - 1 steps ahead.
-        constexpr int kPer = LdsTile<BM, BK>::kInstr + LdsTile<BN, BK>::kInstr;
-        auto issue = [&](int t) {
-            _Float16* st = lds[t % STAGES];
-            LdsTile<BM, BK>::load(a_ptr + t * a_step, a_ld, (lds_half*)st, tid);
-            LdsTile<BN, BK>::load(b_ptr + t * b_step, b_ld, (lds_half*)(st + BM * BK), tid);
-        };
+    // Residual epilogue of the direct path: the tile's residual values and
+    // bias go into registers when its k-loop starts (prefetch()), so their HBM
+    // reads overlap the MFMAs instead of stalling the store stage.
+    constexpr bool kPrefetch = S == Store::kBiasResidual && kDirect;
+    struct Prefetched {
+        f32x4 res[kPrefetch ? FM : 1][kPrefetch ? FN : 1][4];
+        f32x4 bias[kPrefetch ? FN : 1][4];
+    } pre;
+    auto prefetch = [&](const Geo& t) {
+        if constexpr (kPrefetch) {
+            const int col_lane = (lane >> 5) * 4;
+            const float* res = static_cast<const float*>(op.aux);
 #pragma unroll
-        for (int t = 0; t < STAGES - 1; ++t)
-            if (t < steps) issue(t);
-        for (int s = 0; s < steps; ++s) {
-            // Tile s has landed once only the tiles issued after it remain.
-            wait_tiles<kPer, STAGES - 2>(min(steps - 1 - s, STAGES - 2));
-            __syncthreads();   // tile s visible; stage (s - 1) % STAGES idle
-            if (s + STAGES - 1 < steps) issue(s + STAGES - 1);
-            compute_step(s % STAGES, [](int) {});
-        }
-    } else {
-        // Register-staged: tile s + 1 is written to the idle stage during
-        // sub-step 0 of step s, and tile s + 2's global loads go out after it.
-        TileA ta_regs;
-        TileB tb_regs;
-        ta_regs.load(a_ptr, a_ld, a_rows_valid, k_len, tid);
-        tb_regs.load(b_ptr, b_ld, b_rows_valid, k_len, tid);
-        ta_regs.store(lds[0], tid);
-        tb_regs.store(lds[0] + BM * BK, tid);
-        if (steps > 1) {
-            const int k_left = k_len - BK;
-            ta_regs.load(a_ptr + a_step, a_ld, a_rows_valid, k_left, tid);
-            tb_regs.load(b_ptr + b_step, b_ld, b_rows_valid, k_left, tid);
-        }
-        __syncthreads();
-        for (int s = 0; s < steps; ++s) {
-            const int cur = s & 1;
-            compute_step(cur, [&](int kk) {
-                if (kk == 0 && s + 1 < steps) {
-                    ta_regs.store(lds[cur ^ 1], tid);
-                    tb_regs.store(lds[cur ^ 1] + BM * BK, tid);
-                    if (s + 2 < steps) {
-                        const int k_left = k_len - (s + 2) * BK;
-                        ta_regs.load(a_ptr + (s + 2) * a_step, a_ld, a_rows_valid, k_left, tid);
-                        tb_regs.load(b_ptr + (s + 2) * b_step, b_ld, b_rows_valid, k_left, tid);
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    pre.bias[i][g] = *reinterpret_cast<const f32x4*>(
+                        op.bias + t.n0 + wn * WTN + i * 32 + g * 8 + col_lane);
+#pragma unroll
+            for (int j = 0; j < FM; ++j) {
+                const int row = t.m0 + wm * WTM + j * 32 + frag_row;
+#pragma unroll
+                for (int i = 0; i < FN; ++i)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int col = t.n0 + wn * WTN + i * 32 + g * 8 + col_lane;
+                        pre.res[j][i][g] = *reinterpret_cast<const f32x4*>(
+                            res + t.y_batch + size_t(row) * n + col);
                     }
-                }
-            });
-            __syncthreads();
+            }
         }
-    }
+    };
 
-    // Store stage. Lane holds output row m0 + wm*WTM + j*32 + (lane & 31) and,
-    // for each group g, 4 consecutive columns n0 + wn*WTN + i*32 + 8g + 4*(lane>>5).
-    const int col_lane = (lane >> 5) * 4;
-#pragma unroll
-    for (int j = 0; j < FM; ++j) {
-        const int row = m0 + wm * WTM + j * 32 + frag_row;
-        if (CHECK && row >= m) continue;
-#pragma unroll
-        for (int i = 0; i < FN; ++i) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int col = n0 + wn * WTN + i * 32 + g * 8 + col_lane;
-                float v[4] = {acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2],
-                              acc[i][j][g * 4 + 3]};
-                const size_t at = y_batch + size_t(row) * n + col;
-                const bool whole = !CHECK || (col + 3 < n && (n & 3) == 0);
-                if (CHECK && col >= n) continue;
-                if (S == Store::kTn) {
-                    float* out = op.partials ? op.partials + size_t(slice) * m * n
-                                             : static_cast<float*>(op.y);
-                    const bool add = op.partials == nullptr && op.accumulate;
+    // Store stage for tile `t` (the accumulators hold its sums).
+    auto store_tile = [&](const Geo& t) {
+        const int slice = t.slice, m0 = t.m0, n0 = t.n0;
+        const size_t y_batch = t.y_batch;
+        // Store stage. Lane holds output row m0 + wm*WTM + j*32 + (lane & 31) and,
+        // for each group g, 4 consecutive columns n0 + wn*WTN + i*32 + 8g + 4*(lane>>5).
+        const int col_lane = (lane >> 5) * 4;
+    #pragma unroll
+        for (int j = 0; j < FM; ++j) {
+            const int row = m0 + wm * WTM + j * 32 + frag_row;
+            if (CHECK && row >= m) continue;
+    #pragma unroll
+            for (int i = 0; i < FN; ++i) {
+    #pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int col = n0 + wn * WTN + i * 32 + g * 8 + col_lane;
+                    float v[4] = {acc[i][j][g * 4 + 0], acc[i][j][g * 4 + 1], acc[i][j][g * 4 + 2],
+                                  acc[i][j][g * 4 + 3]};
+                    const size_t at = y_batch + size_t(row) * n + col;
+                    const bool whole = !CHECK || (col + 3 < n && (n & 3) == 0);
+                    if (CHECK && col >= n) continue;
+                    if (S == Store::kTn) {
+                        float* out = op.partials ? op.partials + size_t(slice) * m * n
+                                                 : static_cast<float*>(op.y);
+                        const bool add = op.partials == nullptr && op.accumulate;
+                        if (whole) {
+                            f32x4* p = reinterpret_cast<f32x4*>(out + at);
+                            f32x4 r = {v[0], v[1], v[2], v[3]};
+                            if (add) r = *p + r;
+                            *p = r;
+                        } else {
+                            for (int q = 0; q < 4; ++q)
+                                if (col + q < n) out[at + q] = add ? out[at + q] + v[q] : v[q];
+                        }
+                        continue;
+                    }
+                    if (S == Store::kBias || S == Store::kBiasGelu || S == Store::kBiasResidual) {
+                        if constexpr (kPrefetch) {
+                            const f32x4 b = pre.bias[kPrefetch ? i : 0][g];
+                            v[0] += b[0]; v[1] += b[1]; v[2] += b[2]; v[3] += b[3];
+                        } else if (whole) {
+                            const f32x4 b = *reinterpret_cast<const f32x4*>(op.bias + col);
+                            v[0] += b[0]; v[1] += b[1]; v[2] += b[2]; v[3] += b[3];
+                        } else {
+                            for (int q = 0; q < 4; ++q) v[q] += col + q < n ? op.bias[col + q] : 0.0f;
+                        }
+                    }
+                    if (S == Store::kBiasResidual) {
+                        float* out = static_cast<float*>(op.y);
+                        const float* res = static_cast<const float*>(op.aux);
+                        if constexpr (kPrefetch) {
+                            const f32x4 r = pre.res[kPrefetch ? j : 0][kPrefetch ? i : 0][g];
+                            f32x4 o = {r[0] + v[0], r[1] + v[1], r[2] + v[2], r[3] + v[3]};
+                            *reinterpret_cast<f32x4*>(out + at) = o;
+                        } else if (whole) {
+                            const f32x4 r = *reinterpret_cast<const f32x4*>(res + at);
+                            f32x4 o = {r[0] + v[0], r[1] + v[1], r[2] + v[2], r[3] + v[3]};
+                            *reinterpret_cast<f32x4*>(out + at) = o;
+                        } else {
+                            for (int q = 0; q < 4; ++q)
+                                if (col + q < n) out[at + q] = res[at + q] + v[q];
+                        }
+                        continue;
+                    }
+                    if (S == Store::kScale) {
+                        for (int q = 0; q < 4; ++q) v[q] *= op.scale;
+                    }
+                    if (S == Store::kDGelu) {
+                        const _Float16* pre = static_cast<const _Float16*>(op.aux);
+                        if (whole) {
+                            const f16x4 p = *reinterpret_cast<const f16x4*>(pre + at);
+                            for (int q = 0; q < 4; ++q) v[q] *= gelu_grad(float(p[q]));
+                        } else {
+                            for (int q = 0; q < 4; ++q)
+                                if (col + q < n) v[q] *= gelu_grad(float(pre[at + q]));
+                        }
+                    }
+                    _Float16* out = static_cast<_Float16*>(op.y);
+                    if (S == Store::kBiasGelu) {
+                        _Float16* pre = static_cast<_Float16*>(op.aux);
+                        if (whole) {
+                            f16x4 p = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
+                            *reinterpret_cast<f16x4*>(pre + at) = p;
+                        } else {
+                            for (int q = 0; q < 4; ++q)
+                                if (col + q < n) pre[at + q] = _Float16(v[q]);
+                        }
+                        for (int q = 0; q < 4; ++q) v[q] = gelu(v[q]);
+                    }
                     if (whole) {
-                        f32x4* p = reinterpret_cast<f32x4*>(out + at);
-                        f32x4 r = {v[0], v[1], v[2], v[3]};
-                        if (add) r = *p + r;
-                        *p = r;
+                        f16x4 o = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
+                        *reinterpret_cast<f16x4*>(out + at) = o;
                     } else {
                         for (int q = 0; q < 4; ++q)
-                            if (col + q < n) out[at + q] = add ? out[at + q] + v[q] : v[q];
+                            if (col + q < n) out[at + q] = _Float16(v[q]);
                     }
-                    continue;
-                }
-                if (S == Store::kBias || S == Store::kBiasGelu || S == Store::kBiasResidual) {
-                    if (whole) {
-                        const f32x4 b = *reinterpret_cast<const f32x4*>(op.bias + col);
-                        v[0] += b[0]; v[1] += b[1]; v[2] += b[2]; v[3] += b[3];
-                    } else {
-                        for (int q = 0; q < 4; ++q) v[q] += col + q < n ? op.bias[col + q] : 0.0f;
-                    }
-                }
-                if (S == Store::kBiasResidual) {
-                    float* out = static_cast<float*>(op.y);
-                    const float* res = static_cast<const float*>(op.aux);
-                    if (whole) {
-                        const f32x4 r = *reinterpret_cast<const f32x4*>(res + at);
-                        f32x4 o = {r[0] + v[0], r[1] + v[1], r[2] + v[2], r[3] + v[3]};
-                        *reinterpret_cast<f32x4*>(out + at) = o;
-                    } else {
-                        for (int q = 0; q < 4; ++q)
-                            if (col + q < n) out[at + q] = res[at + q] + v[q];
-                    }
-                    continue;
-                }
-                if (S == Store::kScale) {
-                    for (int q = 0; q < 4; ++q) v[q] *= op.scale;
-                }
-                if (S == Store::kDGelu) {
-                    const _Float16* pre = static_cast<const _Float16*>(op.aux);
-                    if (whole) {
-                        const f16x4 p = *reinterpret_cast<const f16x4*>(pre + at);
-                        for (int q = 0; q < 4; ++q) v[q] *= gelu_grad(float(p[q]));
-                    } else {
-                        for (int q = 0; q < 4; ++q)
-                            if (col + q < n) v[q] *= gelu_grad(float(pre[at + q]));
-                    }
-                }
-                _Float16* out = static_cast<_Float16*>(op.y);
-                if (S == Store::kBiasGelu) {
-                    _Float16* pre = static_cast<_Float16*>(op.aux);
-                    if (whole) {
-                        f16x4 p = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
-                        *reinterpret_cast<f16x4*>(pre + at) = p;
-                    } else {
-                        for (int q = 0; q < 4; ++q)
-                            if (col + q < n) pre[at + q] = _Float16(v[q]);
-                    }
-                    for (int q = 0; q < 4; ++q) v[q] = gelu(v[q]);
-                }
-                if (whole) {
-                    f16x4 o = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
-                    *reinterpret_cast<f16x4*>(out + at) = o;
-                } else {
-                    for (int q = 0; q < 4; ++q)
-                        if (col + q < n) out[at + q] = _Float16(v[q]);
                 }
             }
+        }
+
+    };
+
+    if constexpr (kDirect) {
+        // One stream of k-steps over all of this workgroup's tiles (ids
+        // blockIdx.x, + gridDim.x, ...; NT has no k splits, so every tile has
+        // `steps` of them). Step g of the stream lives in stage g % STAGES and
+        // is issued STAGES - 1 steps ahead, across tile boundaries: the next
+        // tile's first loads are in flight while this one's epilogue stores.
+        const int steps = (op.k + BK - 1) / BK;
+        const unsigned n_tiles = (total - 1 - blockIdx.x) / gridDim.x + 1;
+        const int total_steps = int(n_tiles) * steps;
+        constexpr int kPer = LdsTile<BM, BK, kThreads>::kInstr + LdsTile<BN, BK, kThreads>::kInstr;
+        Geo cur = geo(blockIdx.x);
+        LdsTile<BM, BK, kThreads> tile_a;
+        LdsTile<BN, BK, kThreads> tile_b;
+        tile_a.init(cur.a, a_ld, tid);
+        tile_b.init(cur.b, b_ld, tid);
+        int iss_tile = 0;   // tile (index in this workgroup's list) being issued
+        auto issue = [&](int g) {
+            const int t = g / steps;
+            if (t != iss_tile) {
+                iss_tile = t;
+                const Geo ng = geo(blockIdx.x + unsigned(t) * gridDim.x);
+                tile_a.base = uniform_ptr(ng.a);
+                tile_b.base = uniform_ptr(ng.b);
+            }
+            const int k0 = (g - t * steps) * BK;
+            _Float16* st = lds[g % STAGES];
+            tile_a.load(k0, (lds_half*)st, tid);
+            tile_b.load(k0, (lds_half*)(st + BM * BK), tid);
+        };
+#pragma unroll
+        for (int g = 0; g < STAGES - 1; ++g)
+            if (g < total_steps) issue(g);
+        int g = 0;   // position in the stream
+        for (unsigned t = 0; t < n_tiles; ++t) {
+            if (t > 0) cur = geo(blockIdx.x + t * gridDim.x);
+            prefetch(cur);
+            for (int s = 0; s < steps; ++s, ++g) {
+                // Step g has landed once only the steps issued after it remain.
+                wait_tiles<kPer, STAGES - 2>(min(total_steps - 1 - g, STAGES - 2));
+                __syncthreads();   // step g visible; stage (g - 1) % STAGES idle
+                if (g + STAGES - 1 < total_steps) issue(g + STAGES - 1);
+                compute_step(g % STAGES, [](int) {}, [](int) {});
+            }
+            store_tile(cur);
+            zero_acc();
+        }
+    } else {
+        for (unsigned id = blockIdx.x; id < total; id += gridDim.x) {
+            const Geo cur = geo(id);
+            const int a_rows_valid = m - cur.m0;
+            const int b_rows_valid = n - cur.n0;
+            const int k_len = cur.k_len;
+            const int steps = (k_len + BK - 1) / BK;
+            // Register-staged: tile s + 1 is written to the idle stage during
+            // sub-step 0 of step s, and tile s + 2's global loads go out after it.
+            TileA ta_regs;
+            TileB tb_regs;
+            ta_regs.load(cur.a, a_ld, a_rows_valid, k_len, tid);
+            tb_regs.load(cur.b, b_ld, b_rows_valid, k_len, tid);
+            ta_regs.store(lds[0], tid);
+            tb_regs.store(lds[0] + BM * BK, tid);
+            if (steps > 1) {
+                const int k_left = k_len - BK;
+                ta_regs.load(cur.a + a_step, a_ld, a_rows_valid, k_left, tid);
+                tb_regs.load(cur.b + b_step, b_ld, b_rows_valid, k_left, tid);
+            }
+            __syncthreads();
+            for (int s = 0; s < steps; ++s) {
+                const int c = s & 1;
+                compute_step(c, [&](int kk) {
+                    if (kk == 0 && s + 1 < steps) {
+                        ta_regs.store(lds[c ^ 1], tid);
+                        tb_regs.store(lds[c ^ 1] + BM * BK, tid);
+                        if (s + 2 < steps) {
+                            const int k_left = k_len - (s + 2) * BK;
+                            ta_regs.load(cur.a + (s + 2) * a_step, a_ld, a_rows_valid, k_left,
+                                         tid);
+                            tb_regs.load(cur.b + (s + 2) * b_step, b_ld, b_rows_valid, k_left,
+                                         tid);
+                        }
+                    }
+                }, [](int) {});
+                __syncthreads();
+            }
+            store_tile(cur);
+            zero_acc();
         }
     }
 }
@@ -551,7 +696,7 @@ tn_reduce(float* __restrict__ y, const float* __restrict__ partials, size_t quad
 }
 
 struct Config {
-    int bm, bn, bk, stages, waves_m;
+    int bm, bn, bk, stages, waves_m, waves;
 };
 
 // Every instantiated tile configuration. `occ` is how many workgroups of it
@@ -565,28 +710,42 @@ struct Cand {
     bool pick;   // considered by the selector (the rest: FLINT_GEMM_CONFIG only)
 };
 constexpr Cand kCands[] = {
-    {{128, 192, 64, 2, 2}, 2, 1.00, true},  {{256, 192, 64, 2, 2}, 1, 0.93, true},
-    {{128, 128, 64, 2, 2}, 2, 0.92, true},  {{64, 128, 64, 2, 1}, 3, 0.70, true},
-    {{128, 64, 64, 2, 4}, 3, 0.70, true},   {{128, 256, 64, 2, 2}, 1, 0.90, true},
-    {{256, 128, 64, 2, 2}, 1, 0.85, false}, {{128, 192, 64, 3, 2}, 1, 0.80, false},
-    {{128, 128, 64, 4, 2}, 1, 0.70, false}, {{256, 192, 32, 4, 2}, 1, 0.85, false},
-    {{128, 192, 32, 4, 2}, 2, 0.90, false}, {{128, 192, 64, 0, 2}, 2, 1.00, false},
-    {{256, 192, 64, 0, 2}, 1, 0.90, false}, {{256, 256, 64, 2, 2}, 1, 0.85, false},
+    {{128, 192, 64, 2, 2, 4}, 2, 1.00, true},  {{256, 192, 64, 2, 2, 4}, 1, 0.93, true},
+    {{128, 128, 64, 2, 2, 4}, 2, 0.92, true},  {{64, 128, 64, 2, 1, 4}, 3, 0.70, true},
+    {{128, 64, 64, 2, 4, 4}, 3, 0.70, true},   {{128, 256, 64, 2, 2, 4}, 1, 0.90, true},
+    {{256, 128, 64, 2, 2, 4}, 1, 0.85, false}, {{128, 192, 64, 3, 2, 4}, 1, 0.80, false},
+    {{128, 128, 64, 4, 2, 4}, 1, 0.70, false}, {{256, 192, 32, 4, 2, 4}, 1, 0.85, false},
+    {{128, 192, 32, 4, 2, 4}, 2, 0.90, false}, {{128, 192, 64, 0, 2, 4}, 2, 1.00, false},
+    {{256, 192, 64, 0, 2, 4}, 1, 0.90, false}, {{256, 256, 64, 2, 2, 4}, 1, 0.85, false},
+    {{256, 256, 64, 2, 2, 8}, 1, 1.00, false}, {{256, 256, 64, 2, 4, 8}, 1, 1.00, false},
+    {{256, 128, 64, 2, 4, 8}, 1, 1.00, false}, {{128, 256, 64, 2, 2, 8}, 1, 1.00, false},
+    {{256, 256, 32, 4, 2, 8}, 1, 1.00, false}, {{128, 192, 32, 6, 2, 4}, 1, 1.00, false},
+    {{256, 192, 32, 5, 2, 4}, 1, 1.00, false}, {{128, 192, 64, 3, 4, 8}, 1, 1.00, false},
 };
 
-// FLINT_GEMM_CONFIG="bm,bn,bk,stages,waves_m" forces one of the instantiated
+// Workgroups of configuration c that share a CU.
+int occupancy(const Config& c) {
+    for (const Cand& k : kCands)
+        if (k.c.bm == c.bm && k.c.bn == c.bn && k.c.bk == c.bk && k.c.stages == c.stages &&
+            k.c.waves_m == c.waves_m && k.c.waves == c.waves)
+            return k.occ;
+    return 1;
+}
+
+// FLINT_GEMM_CONFIG="bm,bn,bk,stages,waves_m[,waves]" forces one of the instantiated
 // configurations (for tuning sweeps; read on every call so a sweep can change
 // it in-process); unset or unknown, the cost model below picks.
 bool forced_config(Config* out) {
     const char* e = std::getenv("FLINT_GEMM_CONFIG");
     if (e == nullptr) return false;
     Config c{};
-    if (std::sscanf(e, "%d,%d,%d,%d,%d", &c.bm, &c.bn, &c.bk, &c.stages, &c.waves_m) != 5) {
-        return false;
-    }
+    c.waves = 4;
+    const int got = std::sscanf(e, "%d,%d,%d,%d,%d,%d", &c.bm, &c.bn, &c.bk, &c.stages,
+                                &c.waves_m, &c.waves);
+    if (got != 5 && got != 6) return false;
     for (const Cand& k : kCands) {
         if (k.c.bm == c.bm && k.c.bn == c.bn && k.c.bk == c.bk && k.c.stages == c.stages &&
-            k.c.waves_m == c.waves_m) {
+            k.c.waves_m == c.waves_m && k.c.waves == c.waves) {
             *out = c;
             return true;
         }
@@ -598,9 +757,15 @@ bool forced_config(Config* out) {
 // minimises (rounds of tiles over CUs x occupancy) x (tile area x occupancy /
 // efficiency). Epilogue-heavy GELU output prefers the 256x192 tile (one
 // workgroup per CU), and TN's transposed loads the 128x256 one.
-Config pick_config(size_t m, size_t n, size_t slices, int cus, bool gelu, bool tn) {
+Config pick_config(size_t m, size_t n, size_t slices, int cus, bool gelu, bool tn,
+                   bool residual = false) {
     Config forced;
     if (forced_config(&forced)) return forced;
+    // The residual epilogue holds its prefetched residual and bias in
+    // registers, which leaves one 128x192 workgroup per CU: three stages then
+    // keep two k-steps of loads in flight (measured 17-20% faster at 8192 x
+    // 768 with k = 768 and 3,072).
+    if (residual && m % 128 == 0 && n % 192 == 0) return Config{128, 192, 64, 3, 2, 4};
     Config best = kCands[0].c;
     double best_cost = 1e300;
     for (const Cand& k : kCands) {
@@ -625,26 +790,35 @@ Config pick_config(size_t m, size_t n, size_t slices, int cus, bool gelu, bool t
 template <Layout L, Store S, bool CHECK>
 hipError_t dispatch(const Config& c, dim3 grid, const Operands& op, const TileArgs& ta,
                     hipStream_t stream) {
-#define FLINT_GEMM_CASE(BM_, BN_, BK_, ST_, WM_)                                          \
-    if (c.bm == BM_ && c.bn == BN_ && c.bk == BK_ && c.stages == ST_ && c.waves_m == WM_) { \
-        hipLaunchKernelGGL((gemm_kernel<BM_, BN_, BK_, ST_, WM_, L, S, CHECK>), grid,       \
-                           dim3(kThreads), 0, stream, op, ta);                               \
-        return hipGetLastError();                                                         \
+#define FLINT_GEMM_CASE(BM_, BN_, BK_, ST_, WM_, NW_)                                       \
+    if (c.bm == BM_ && c.bn == BN_ && c.bk == BK_ && c.stages == ST_ && c.waves_m == WM_ &&   \
+        c.waves == NW_) {                                                                     \
+        hipLaunchKernelGGL((gemm_kernel<BM_, BN_, BK_, ST_, WM_, NW_, L, S, CHECK>), grid,    \
+                           dim3(NW_ * 64), 0, stream, op, ta);                                \
+        return hipGetLastError();                                                             \
     }
-    FLINT_GEMM_CASE(128, 192, 64, 2, 2)
-    FLINT_GEMM_CASE(256, 192, 64, 2, 2)
-    FLINT_GEMM_CASE(128, 128, 64, 2, 2)
-    FLINT_GEMM_CASE(64, 128, 64, 2, 1)
-    FLINT_GEMM_CASE(128, 64, 64, 2, 4)
-    FLINT_GEMM_CASE(128, 256, 64, 2, 2)
-    FLINT_GEMM_CASE(256, 128, 64, 2, 2)
-    FLINT_GEMM_CASE(128, 192, 64, 3, 2)
-    FLINT_GEMM_CASE(128, 128, 64, 4, 2)
-    FLINT_GEMM_CASE(256, 192, 32, 4, 2)
-    FLINT_GEMM_CASE(128, 192, 32, 4, 2)
-    FLINT_GEMM_CASE(128, 192, 64, 0, 2)
-    FLINT_GEMM_CASE(256, 192, 64, 0, 2)
-    FLINT_GEMM_CASE(256, 256, 64, 2, 2)
+    FLINT_GEMM_CASE(128, 192, 64, 2, 2, 4)
+    FLINT_GEMM_CASE(256, 192, 64, 2, 2, 4)
+    FLINT_GEMM_CASE(128, 128, 64, 2, 2, 4)
+    FLINT_GEMM_CASE(64, 128, 64, 2, 1, 4)
+    FLINT_GEMM_CASE(128, 64, 64, 2, 4, 4)
+    FLINT_GEMM_CASE(128, 256, 64, 2, 2, 4)
+    FLINT_GEMM_CASE(256, 128, 64, 2, 2, 4)
+    FLINT_GEMM_CASE(128, 192, 64, 3, 2, 4)
+    FLINT_GEMM_CASE(128, 128, 64, 4, 2, 4)
+    FLINT_GEMM_CASE(256, 192, 32, 4, 2, 4)
+    FLINT_GEMM_CASE(128, 192, 32, 4, 2, 4)
+    FLINT_GEMM_CASE(128, 192, 64, 0, 2, 4)
+    FLINT_GEMM_CASE(256, 192, 64, 0, 2, 4)
+    FLINT_GEMM_CASE(256, 256, 64, 2, 2, 4)
+    FLINT_GEMM_CASE(256, 256, 64, 2, 2, 8)
+    FLINT_GEMM_CASE(256, 256, 64, 2, 4, 8)
+    FLINT_GEMM_CASE(256, 128, 64, 2, 4, 8)
+    FLINT_GEMM_CASE(128, 256, 64, 2, 2, 8)
+    FLINT_GEMM_CASE(256, 256, 32, 4, 2, 8)
+    FLINT_GEMM_CASE(128, 192, 32, 6, 2, 4)
+    FLINT_GEMM_CASE(256, 192, 32, 5, 2, 4)
+    FLINT_GEMM_CASE(128, 192, 64, 3, 4, 8)
 #undef FLINT_GEMM_CASE
     return hipErrorInvalidValue;
 }
@@ -656,7 +830,8 @@ hipError_t run(Operands op, size_t slices, int split_len, hipStream_t stream) {
     const bool split = S == Store::kTn && op.partials != nullptr;
     // A TN split's tile shape is the one gemm_tn_splits planned with.
     const Config c = pick_config(op.m, op.n, S == Store::kTn ? 1 : slices, cus,
-                                 S == Store::kBiasGelu, L == Layout::kTN);
+                                 S == Store::kBiasGelu, L == Layout::kTN,
+                                 S == Store::kBiasResidual);
     TileArgs ta;
     ta.tiles_m = (op.m + c.bm - 1) / c.bm;
     ta.tiles_n = (op.n + c.bn - 1) / c.bn;
@@ -664,10 +839,15 @@ hipError_t run(Operands op, size_t slices, int split_len, hipStream_t stream) {
     ta.slices = int(slices);
     ta.group_m = 8;
     ta.split_len = split_len;
+    // Persistent workgroups: as many as fit on the GPU at once (a multiple of
+    // 8, so a workgroup keeps its XCD's share of the tiles), each walking ids
+    // blockIdx.x, + gridDim.x, ...
     const size_t total = size_t(ta.tiles_per_slice) * slices;
-    const unsigned gx = unsigned(std::min<size_t>(total, size_t{1} << 20));
-    const unsigned gy = unsigned((total + gx - 1) / gx);
-    const dim3 grid(gx, gy);
+    size_t slots = size_t(cus) * size_t(occupancy(c));
+    if (const char* e = std::getenv("FLINT_GEMM_SLOTS")) slots = std::max(1, std::atoi(e));
+    size_t gx = std::min(total, slots);
+    if (gx >= 8) gx -= gx % 8;
+    const dim3 grid(static_cast<unsigned>(gx), 1, 1);
     // The unchecked kernel needs whole tiles and whole k-steps in every slice.
     const int k_piece = split ? split_len : op.k;
     const bool exact = op.m % c.bm == 0 && op.n % c.bn == 0 && k_piece % c.bk == 0 &&
