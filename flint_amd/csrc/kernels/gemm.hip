@@ -457,21 +457,28 @@ gemm_kernel(Operands op, TileArgs ta) {
     // Residual epilogue of the direct path: the tile's residual values and
     // bias go into registers when its k-loop starts (prefetch()), so their HBM
     // reads overlap the MFMAs instead of stalling the store stage.
+    // Bias epilogues of the direct path prefetch their bias the same way, so
+    // the store stage issues no loads: a load there would make the waves wait
+    // (in-order vmcnt) for the next tile's prefetched k-steps as well.
     constexpr bool kPrefetch = S == Store::kBiasResidual && kDirect;
+    constexpr bool kPrefetchBias =
+        kDirect && (S == Store::kBias || S == Store::kBiasGelu || S == Store::kBiasResidual);
     struct Prefetched {
         f32x4 res[kPrefetch ? FM : 1][kPrefetch ? FN : 1][4];
-        f32x4 bias[kPrefetch ? FN : 1][4];
+        f32x4 bias[kPrefetchBias ? FN : 1][4];
     } pre;
     auto prefetch = [&](const Geo& t) {
-        if constexpr (kPrefetch) {
-            const int col_lane = (lane >> 5) * 4;
-            const float* res = static_cast<const float*>(op.aux);
+        const int col_lane = (lane >> 5) * 4;
+        if constexpr (kPrefetchBias) {
 #pragma unroll
             for (int i = 0; i < FN; ++i)
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
                     pre.bias[i][g] = *reinterpret_cast<const f32x4*>(
                         op.bias + t.n0 + wn * WTN + i * 32 + g * 8 + col_lane);
+        }
+        if constexpr (kPrefetch) {
+            const float* res = static_cast<const float*>(op.aux);
 #pragma unroll
             for (int j = 0; j < FM; ++j) {
                 const int row = t.m0 + wm * WTM + j * 32 + frag_row;
@@ -524,8 +531,8 @@ gemm_kernel(Operands op, TileArgs ta) {
                         continue;
                     }
                     if (S == Store::kBias || S == Store::kBiasGelu || S == Store::kBiasResidual) {
-                        if constexpr (kPrefetch) {
-                            const f32x4 b = pre.bias[kPrefetch ? i : 0][g];
+                        if constexpr (kPrefetchBias) {
+                            const f32x4 b = pre.bias[kPrefetchBias ? i : 0][g];
                             v[0] += b[0]; v[1] += b[1]; v[2] += b[2]; v[3] += b[3];
                         } else if (whole) {
                             const f32x4 b = *reinterpret_cast<const f32x4*>(op.bias + col);
@@ -599,6 +606,14 @@ gemm_kernel(Operands op, TileArgs ta) {
         const unsigned n_tiles = (total - 1 - blockIdx.x) / gridDim.x + 1;
         const int total_steps = int(n_tiles) * steps;
         constexpr int kPer = LdsTile<BM, BK, kThreads>::kInstr + LdsTile<BN, BK, kThreads>::kInstr;
+        // Vector stores one store stage issues per lane.
+        constexpr int kStoreInstr = FM * FN * 4 * (S == Store::kBiasGelu ? 2 : 1);
+        constexpr int kAfterStore = (STAGES - 2) * kPer + kStoreInstr < 63
+                                        ? (STAGES - 2) * kPer + kStoreInstr : 63;
+        // Not with the residual prefetch: its extra branch led the compiler to
+        // drain vmcnt before every barrier (seen in the ISA), which costs more
+        // than the drained stores.
+        constexpr bool kWaitPastStores = !kPrefetch;
         Geo cur = geo(blockIdx.x);
         LdsTile<BM, BK, kThreads> tile_a;
         LdsTile<BN, BK, kThreads> tile_b;
@@ -626,8 +641,13 @@ gemm_kernel(Operands op, TileArgs ta) {
             if (t > 0) cur = geo(blockIdx.x + t * gridDim.x);
             prefetch(cur);
             for (int s = 0; s < steps; ++s, ++g) {
-                // Step g has landed once only the steps issued after it remain.
-                wait_tiles<kPer, STAGES - 2>(min(total_steps - 1 - g, STAGES - 2));
+                // Step g has landed once only the steps issued after it remain
+                // (and, right after a store stage, its stores: vmcnt retires in
+                // issue order, so the stores need not drain first).
+                if (kWaitPastStores && s == 0 && t > 0 && total_steps - 1 - g >= STAGES - 2)
+                    wait_vmcnt<kAfterStore>();
+                else
+                    wait_tiles<kPer, STAGES - 2>(min(total_steps - 1 - g, STAGES - 2));
                 __syncthreads();   // step g visible; stage (g - 1) % STAGES idle
                 if (g + STAGES - 1 < total_steps) issue(g + STAGES - 1);
                 compute_step(g % STAGES, [](int) {}, [](int) {});
@@ -838,6 +858,7 @@ hipError_t run(Operands op, size_t slices, int split_len, hipStream_t stream) {
     ta.tiles_per_slice = ta.tiles_m * ta.tiles_n;
     ta.slices = int(slices);
     ta.group_m = 8;
+    if (const char* e = std::getenv("FLINT_GEMM_GROUP_M")) ta.group_m = std::max(1, std::atoi(e));
     ta.split_len = split_len;
     // Persistent workgroups: as many as fit on the GPU at once (a multiple of
     // 8, so a workgroup keeps its XCD's share of the tiles), each walking ids
