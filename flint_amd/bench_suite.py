@@ -303,15 +303,21 @@ def run(f, torch, dev, path, only=None):
         # flint_copy over 824 MB: the practical read+write HBM rate of this part,
         # the ceiling the other bandwidth-bound kernels are read against.
         if want("flint_copy"):
-            nb = M * VP * 2
-            src = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(2)]
-            for t_ in src:
-                t_.fill_(1)
-            dst = torch.empty(nb, dtype=torch.uint8, device=dev)
-            ms = _time_gpu(torch, lambda st: f.copy(dst, src[st], nb), [0, 1], per_round=8)
-            record("flint_copy 824 MB", "red", 2 * nb, ms,
-                   note="read + write; the practical HBM ceiling for the kernels below")
-            del src, dst
+            # Copies of the traffic of the reductions above (LN forward, LN
+            # backward, softmax, cross-entropy): what a kernel moving that many
+            # bytes can reach on this part, launch and ramp included.
+            for traffic, label in ((37_748_736, "= LN forward"), (88_080_384, "= LN backward"),
+                                   (302_000_000, "= causal softmax forward"),
+                                   (2 * M * VP * 2, "= softmax + cross-entropy")):
+                nb = traffic // 2 // 16 * 16
+                n_ = max(2, -(-(600 << 20) // (2 * nb)))
+                src = [torch.ones(nb, dtype=torch.uint8, device=dev) for _ in range(n_)]
+                dst = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(n_)]
+                ms = _time_gpu(torch, lambda st: f.copy(dst[st], src[st], nb), list(range(n_)),
+                               per_round=max(8, n_))
+                record(f"flint_copy {2 * nb / 1e6:.0f} MB moved {label}", "red", 2 * nb, ms,
+                       note="read + write; the practical HBM ceiling at this size")
+                del src, dst
         if want("flint_fp32_to_fp16"):
             count = 124_475_904   # GPT-2 124M parameters, as synced each step
             xs = [normal((count,), 60 + r).to(dev) for r in range(2)]
@@ -355,6 +361,49 @@ def run(f, torch, dev, path, only=None):
             del wte, wpe, xs, dx, dwte, dwpe, ws
         torch.cuda.empty_cache()
 
+    def section_gpt2():
+        # A whole GPT-2 124M training step: 12 layers, width 768,
+        # 12 heads, 8 x 1024 tokens, padded vocabulary 50,304; forward through
+        # the loss and backward to every weight gradient, FP16 with loss scale
+        # 1024 (dlogits scale 1024 / 8192). 7.00 TFLOP by 2mnk over every GEMM.
+        from flint_amd.flint_lib import Gpt2
+
+        L_, S_, T_ = 12, 8, 1024
+        model = Gpt2(f, L_, H, C, T_, V, VP, S_, T_, backward=True)
+        g = torch.Generator().manual_seed(5)
+        for name, addr, rows, cols in model.parameters():
+            if name.endswith(("ln_1.weight", "ln_2.weight")) or name == "ln_f.weight":
+                t = torch.ones(rows, cols)
+            elif rows == 1:
+                t = torch.zeros(rows, cols)
+            else:
+                t = torch.randn(rows, cols, generator=g) * 0.02
+                if name == "wte.weight":
+                    t[V:] = 0
+            model.write(addr, t.to(dev))
+        model.sync_weights()
+        tok = torch.randint(0, V, (S_ * T_,), generator=g).to(torch.int32).to(torch.int16).to(dev)
+        tgt = torch.randint(0, V, (S_ * T_,), generator=g).to(torch.int32).to(torch.int16).to(dev)
+        scale = 1024.0 / (S_ * T_)
+
+        def step(_):
+            model.forward(tok, tgt, scale)
+            model.backward(tok)
+
+        ms = _time_gpu(torch, step, [0], rounds=5, per_round=5)
+        flops = 7.0013e12
+        entry = {"kernel": "gpt2_124m_train_step 8x1024 (forward + backward)", "ms": round(ms, 4),
+                 "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                 "frac_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_TF, 4),
+                 "tokens_per_s": round(S_ * T_ / (ms * 1e-3)), "cpu_threads": threads,
+                 "loss": round(model.mean_loss(), 4),
+                 "note": "7.00 TFLOP per step (2mnk over every GEMM, attention counted full); "
+                         "random-init weights, random tokens"}
+        out.append(entry)
+        print(json.dumps(entry), flush=True)
+        model.close()
+        torch.cuda.empty_cache()
+
     if any(want(x) for x in ("flint_gemm_nt_batched", "flint_gemm_nn_batched",
                              "flint_gemm_tn_batched")):
         section_batched()
@@ -365,6 +414,8 @@ def run(f, torch, dev, path, only=None):
         section_softmax()
     if want("flint_softmax_cross_entropy"):
         section_ce()
+    if want("gpt2_124m_train_step"):
+        section_gpt2()
     if any(want(x) for x in ("flint_copy", "flint_fp32_to_fp16", "flint_heads_split",
                              "flint_heads_merge", "flint_embedding")):
         section_support()

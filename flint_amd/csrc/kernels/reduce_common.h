@@ -74,6 +74,37 @@ __device__ __forceinline__ Comp comp_reduce(Comp a) {
     return a;
 }
 
+// DPP lane exchanges for wave-wide all-reductions (no LDS round trip):
+// quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror (lane i <-> 7 - i within
+// 8) and row_mirror (i <-> 15 - i within 16); then ds_swizzle xor 16 and one
+// bpermute for xor 32. After step k every lane holds the total of its group
+// of 2^k lanes.
+__device__ __forceinline__ float dpp_f(float v, int ctrl_sel) {
+    const int x = __builtin_bit_cast(int, v);
+    int r;
+    switch (ctrl_sel) {
+    case 0: r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false); break;
+    case 1: r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false); break;
+    case 2: r = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false); break;
+    case 3: r = __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false); break;
+    case 4: r = __builtin_amdgcn_ds_swizzle(x, 0x401F); break;
+    default: r = __shfl_xor(x, 32, 64); break;
+    }
+    return __builtin_bit_cast(float, r);
+}
+
+// Compensated all-reduce over the 64 lanes; every lane ends with the same
+// bits (comp_merge is symmetric). The order differs from comp_reduce<64>.
+__device__ __forceinline__ Comp comp_allreduce64(Comp a) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        const float s = dpp_f(a.sum, k);
+        const float e = dpp_f(a.error, k);
+        comp_merge(a, s, e);
+    }
+    return a;
+}
+
 template <int WIDTH>
 __device__ __forceinline__ float sum_reduce(float v) {
 #pragma unroll

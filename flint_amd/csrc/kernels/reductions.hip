@@ -39,67 +39,83 @@ constexpr size_t kMaxBlocks = size_t{1} << 22;
 constexpr int kLnRowsPerBlock = 4;
 
 // One wave per row; lane l holds float4 groups l, l + 64, ... (up to CPL of
-// them) for the whole kernel.
+// them). Waves stride over rows (the grid is sized to the GPU), load the next
+// row before reducing the current one, and keep gamma and beta in registers
+// for all their rows. The two compensated wave reductions use DPP exchanges.
 template <int CPL>
 __global__ void __launch_bounds__(256)
 layernorm_forward_regs(_Float16* __restrict__ y, float* __restrict__ mean,
                        float* __restrict__ rstd, const float* __restrict__ x,
                        const float* __restrict__ gamma, const float* __restrict__ beta,
                        size_t rows, int cols, float eps) {
-    for (size_t row = size_t(blockIdx.x) * kLnRowsPerBlock + (threadIdx.x >> 6); row < rows;
-         row += size_t(gridDim.x) * kLnRowsPerBlock) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
     const int lane = threadIdx.x & 63;
     const int groups = cols >> 2;
-    const f4* xr = reinterpret_cast<const f4*>(x + row * cols);
-    f4 v[CPL];
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        const int g = lane + i * 64;
-        v[i] = g < groups ? xr[g] : f4{};
-    }
-    Comp s;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        if (lane + i * 64 < groups) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) comp_add(s, v[i][j]);
-        }
-    }
-    s = comp_reduce<64>(s);
-    const float n = float(cols);
-    const float mu = __fdiv_rn(add_rn(s.sum, s.error), n);
-    Comp q;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        if (lane + i * 64 < groups) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) comp_add_square(q, sub_rn(v[i][j], mu));
-        }
-    }
-    q = comp_reduce<64>(q);
-    const float var = __fdiv_rn(add_rn(q.sum, q.error), n);
-    const float rs = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(var, eps)));
-    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-    h4* yr = reinterpret_cast<h4*>(y + row * cols);
+    const size_t stride = size_t(gridDim.x) * kLnRowsPerBlock;
     const f4* g4 = reinterpret_cast<const f4*>(gamma);
     const f4* b4 = reinterpret_cast<const f4*>(beta);
+    f4 ga[CPL], be[CPL];
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
         const int g = lane + i * 64;
-        if (g < groups) {
-            const f4 ga = g4[g];
-            const f4 be = b4[g];
-            h4 o;
+        ga[i] = g < groups ? g4[g] : f4{};
+        be[i] = g < groups ? b4[g] : f4{};
+    }
+    size_t row = size_t(blockIdx.x) * kLnRowsPerBlock + (threadIdx.x >> 6);
+    f4 v[CPL];
+    auto load_row = [&](size_t r, f4 (&dst)[CPL]) {
+        const f4* xr = reinterpret_cast<const f4*>(x + r * cols);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                o[j] = _Float16(__builtin_fmaf(mul_rn(sub_rn(v[i][j], mu), rs), ga[j], be[j]));
-            yr[g] = o;
+        for (int i = 0; i < CPL; ++i) {
+            const int g = lane + i * 64;
+            dst[i] = g < groups ? xr[g] : f4{};
         }
-    }
-    if (lane == 0) {
-        mean[row] = mu;
-        rstd[row] = rs;
-    }
+    };
+    if (row < rows) load_row(row, v);
+    for (; row < rows; row += stride) {
+        f4 nxt[CPL];
+        if (row + stride < rows) load_row(row + stride, nxt);
+        Comp s;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            if (lane + i * 64 < groups) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) comp_add(s, v[i][j]);
+            }
+        }
+        s = comp_allreduce64(s);
+        const float n = float(cols);
+        const float mu = __fdiv_rn(add_rn(s.sum, s.error), n);
+        Comp q;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            if (lane + i * 64 < groups) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) comp_add_square(q, sub_rn(v[i][j], mu));
+            }
+        }
+        q = comp_allreduce64(q);
+        const float var = __fdiv_rn(add_rn(q.sum, q.error), n);
+        const float rs = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(var, eps)));
+        h4* yr = reinterpret_cast<h4*>(y + row * cols);
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int g = lane + i * 64;
+            if (g < groups) {
+                h4 o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    o[j] = _Float16(__builtin_fmaf(mul_rn(sub_rn(v[i][j], mu), rs), ga[i][j],
+                                                   be[i][j]));
+                yr[g] = o;
+            }
+        }
+        if (lane == 0) {
+            mean[row] = mu;
+            rstd[row] = rs;
+        }
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) v[i] = nxt[i];
     }
 }
 
@@ -675,7 +691,14 @@ softmax_cross_entropy(h8* __restrict__ dlogits, float* __restrict__ row_loss,
 hipError_t launch_layernorm_forward(void* y, void* mean, void* rstd, const void* x,
                                     const void* gamma, const void* beta, size_t rows, size_t cols,
                                     float eps, hipStream_t stream) {
-    const unsigned blocks = unsigned(std::min<size_t>((rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock, kMaxBlocks));
+    // Register-resident rows: a grid the GPU holds at once (6 workgroups of 4
+    // waves per CU), each wave walking rows; the any-width kernel keeps the
+    // one-row-per-wave grid.
+    int cus = 256;
+    if (hipError_t e = device_cus(&cus); e != hipSuccess) return e;
+    const size_t row_blocks = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+    const unsigned blocks = unsigned(std::min<size_t>(row_blocks, kMaxBlocks));
+    const unsigned reg_blocks = unsigned(std::min<size_t>(row_blocks, size_t(cus) * 6));
     auto* yh = static_cast<_Float16*>(y);
     auto* mf = static_cast<float*>(mean);
     auto* rf = static_cast<float*>(rstd);
@@ -684,7 +707,7 @@ hipError_t launch_layernorm_forward(void* y, void* mean, void* rstd, const void*
     const auto* bf = static_cast<const float*>(beta);
     const int c = int(cols);
 #define FLINT_LN(CPL)                                                                       \
-    hipLaunchKernelGGL(layernorm_forward_regs<CPL>, dim3(blocks), dim3(256), 0, stream, yh, mf, \
+    hipLaunchKernelGGL(layernorm_forward_regs<CPL>, dim3(reg_blocks), dim3(256), 0, stream, yh, mf, \
                        rf, xf, gf, bf, rows, c, eps)
     const size_t groups = cols / 4;
     if (cols % 4 == 0 && groups <= 64) FLINT_LN(1);
