@@ -39,88 +39,10 @@
 
 #include "common/common.h"
 #include "kernels/kernels.h"
+#include "kernels/gemm_common.h"
 
 namespace flint {
 namespace {
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) _Float16 lds_half;
-
-
-enum class Layout { kNT, kNN, kTN };
-// What the kernel's store stage does. kTn writes FP32 (plain, accumulate or a
-// split's partial); kTnHalf is the batched TN's FP16 output.
-enum class Store { kNone, kBias, kBiasGelu, kBiasResidual, kDGelu, kScale, kTn, kTnHalf };
-
-// Position of 16-byte chunk `chunk` of LDS row `row` (BK / 8 chunks a row).
-// BK 64: 128-byte rows, key (row ^ row >> 3) & 7; BK 32: 64-byte rows, key
-// (row >> 1 ^ row >> 2) & 3. Either keeps the 8 / 16 rows that one LDS cycle
-// serves (32 / 64 banks) on distinct banks for a fragment read.
-template <int BK>
-__device__ __forceinline__ int swizzle(int row, int chunk) {
-    if constexpr (BK == 64) return chunk ^ ((row ^ (row >> 3)) & 7);
-    else return chunk ^ (((row >> 1) ^ (row >> 2)) & 3);
-}
-
-// GPT-2's tanh GELU. 0.5 s (1 + tanh u) equals s / (1 + exp(-2u)), which has
-// no cancellation for negative s; u = sqrt(2/pi) (s + 0.044715 s^3). The
-// exponential is 2^(s (c0 + c1 s^2)) on v_exp_f32 and the quotient one
-// v_rcp_f32 multiply: about 1e-6 relative error, far inside FP16's rounding.
-// +inf gives +inf, -inf gives NaN (as the tanh form does), large negative s -0.
-__device__ __forceinline__ float gelu(float s) {
-    constexpr float c0 = -2.3022082f;          // -2 sqrt(2/pi) log2(e)
-    constexpr float c1 = -0.10294324f;         // c0 * 0.044715
-    const float e = __builtin_amdgcn_exp2f(s * __builtin_fmaf(c1, s * s, c0));
-    return s * __builtin_amdgcn_rcpf(1.0f + e);
-}
-
-// d/ds [s sigma(2u)] = sigma + s sigma (1 - sigma) 2u', 2u' = 2 sqrt(2/pi)
-// (1 + 3 * 0.044715 s^2). 1 - sigma is taken as e sigma for s >= 0 (keeps
-// precision as sigma -> 1) and directly for s < 0 (e may overflow there).
-// Infinite s returns GELU's limits; NaN propagates.
-__device__ __forceinline__ float gelu_grad(float s) {
-    constexpr float c0 = -2.3022082f;
-    constexpr float c1 = -0.10294324f;
-    const float e = __builtin_amdgcn_exp2f(s * __builtin_fmaf(c1, s * s, c0));
-    const float sigma = __builtin_amdgcn_rcpf(1.0f + e);
-    const float one_minus = s < 0.0f ? 1.0f - sigma : e * sigma;
-    const float q = s * one_minus * __builtin_fmaf(0.21406444860866706f, s * s, 1.5957691216057308f);
-    const float g = __builtin_fmaf(sigma, q, sigma);
-    return __builtin_isinf(s) ? (s > 0.0f ? 1.0f : 0.0f) : g;
-}
-
-struct TileArgs {
-    int tiles_m, tiles_n;     // macro-tiles per batch / split
-    int tiles_per_slice;      // tiles_m * tiles_n
-    int slices;               // batches, or k splits for TN
-    int group_m;              // grouped ordering width (in m tiles)
-    int split_len;            // TN: k per split (multiple of 64)
-};
-
-// Maps logical tile id `id` (< tiles_per_slice * slices) to (slice, tile_m,
-// tile_n). Workgroups run persistently: workgroup b takes ids b, b + G, b + 2G,
-// ... (G = grid size, a multiple of 8 when there are at least 8 ids), so id % 8
-// is the XCD the workgroup runs on (XCDs take workgroups round-robin). The
-// remap gives XCD x the contiguous range [x * total/8, (x+1) * total/8) of
-// tiles when total is a multiple of 8; within a slice, tiles go in groups of
-// group_m rows of tiles, column by column, for L2 reuse.
-__device__ __forceinline__ void map_tile(const TileArgs& t, unsigned id, int* slice, int* tm,
-                                         int* tn) {
-    const unsigned total = unsigned(t.tiles_per_slice) * unsigned(t.slices);
-    if ((total & 7u) == 0) id = (id & 7u) * (total >> 3) + (id >> 3);
-    *slice = int(id / unsigned(t.tiles_per_slice));
-    const int in_slice = int(id % unsigned(t.tiles_per_slice));
-    const int per_group = t.group_m * t.tiles_n;
-    const int group = in_slice / per_group;
-    const int first_m = group * t.group_m;
-    const int rows = min(t.tiles_m - first_m, t.group_m);
-    const int in_group = in_slice - group * per_group;
-    *tm = first_m + in_group % rows;
-    *tn = in_group / rows;
-}
 
 // Streams a ROWS x BK tile of a k-contiguous matrix straight into LDS with
 // buffer_load_dwordx4 ... lds. The buffer resource covers the tile's rows (base
@@ -131,14 +53,6 @@ __device__ __forceinline__ void map_tile(const TileArgs& t, unsigned id, int* sl
 // loads the global chunk the swizzle puts there.
 // (Buffer rather than global addressing: on MI355X the global form stalled the
 // address unit on the L1 for a large share of the GEMM's cycles.)
-// A wave-uniform pointer held in scalar registers (buffer resources need one).
-__device__ __forceinline__ _Float16* uniform_ptr(const _Float16* p) {
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
-    return reinterpret_cast<_Float16*>((uint64_t(hi) << 32) | lo);
-}
-
 template <int ROWS, int BK, int THREADS>
 struct LdsTile {
     static constexpr int kWaves = THREADS / 64;
@@ -191,13 +105,7 @@ struct LdsTile {
     }
 };
 
-// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima), gfx9
-// encoding: vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
+
 
 // Waits until at most `tiles` tiles of PER loads each are outstanding.
 template <int PER, int MAX>
@@ -300,17 +208,6 @@ struct TransposedTile {
     }
 };
 
-struct Operands {
-    void* y;
-    const _Float16* x;
-    const _Float16* w;
-    const float* bias;     // bias (n FP32)
-    void* aux;             // pre (GELU out / dGELU in) or residual
-    float* partials;       // TN split partials, or null
-    float scale;
-    int accumulate;        // TN: y += instead of y =
-    int m, n, k;
-};
 
 // Registers a lane may hold: 512 (one wave per SIMD) when its accumulators
 // alone take 192 or more, else 256 (two waves per SIMD, or two workgroups).
@@ -648,7 +545,7 @@ gemm_kernel(Operands op, TileArgs ta) {
                     wait_vmcnt<kAfterStore>();
                 else
                     wait_tiles<kPer, STAGES - 2>(min(total_steps - 1 - g, STAGES - 2));
-                __syncthreads();   // step g visible; stage (g - 1) % STAGES idle
+                block_sync();   // step g visible; stage (g - 1) % STAGES idle
                 if (g + STAGES - 1 < total_steps) issue(g + STAGES - 1);
                 compute_step(g % STAGES, [](int) {}, [](int) {});
             }
@@ -675,7 +572,7 @@ gemm_kernel(Operands op, TileArgs ta) {
                 ta_regs.load(cur.a + a_step, a_ld, a_rows_valid, k_left, tid);
                 tb_regs.load(cur.b + b_step, b_ld, b_rows_valid, k_left, tid);
             }
-            __syncthreads();
+            block_sync();
             for (int s = 0; s < steps; ++s) {
                 const int c = s & 1;
                 compute_step(c, [&](int kk) {
@@ -691,7 +588,7 @@ gemm_kernel(Operands op, TileArgs ta) {
                         }
                     }
                 }, [](int) {});
-                __syncthreads();
+                block_sync();
             }
             store_tile(cur);
             zero_acc();
@@ -733,7 +630,11 @@ constexpr Cand kCands[] = {
     {{128, 192, 64, 2, 2, 4}, 2, 1.00, true},  {{256, 192, 64, 2, 2, 4}, 1, 0.93, true},
     {{128, 128, 64, 2, 2, 4}, 2, 0.92, true},  {{64, 128, 64, 2, 1, 4}, 3, 0.70, true},
     {{128, 64, 64, 2, 4, 4}, 3, 0.70, true},   {{128, 256, 64, 2, 2, 4}, 1, 0.90, true},
-    {{256, 128, 64, 2, 2, 4}, 1, 0.85, false}, {{128, 192, 64, 3, 2, 4}, 1, 0.80, false},
+    {{128, 192, 64, 3, 2, 4}, 1, 0.80, false},
+#ifdef FLINT_GEMM_SWEEP
+    // Tuning-sweep configurations (FLINT_GEMM_CONFIG only), built with
+    // -DFLINT_GEMM_SWEEP so the product library stays quick to compile.
+    {{256, 128, 64, 2, 2, 4}, 1, 0.85, false},
     {{128, 128, 64, 4, 2, 4}, 1, 0.70, false}, {{256, 192, 32, 4, 2, 4}, 1, 0.85, false},
     {{128, 192, 32, 4, 2, 4}, 2, 0.90, false}, {{128, 192, 64, 0, 2, 4}, 2, 1.00, false},
     {{256, 192, 64, 0, 2, 4}, 1, 0.90, false}, {{256, 256, 64, 2, 2, 4}, 1, 0.85, false},
@@ -741,6 +642,7 @@ constexpr Cand kCands[] = {
     {{256, 128, 64, 2, 4, 8}, 1, 1.00, false}, {{128, 256, 64, 2, 2, 8}, 1, 1.00, false},
     {{256, 256, 32, 4, 2, 8}, 1, 1.00, false}, {{128, 192, 32, 6, 2, 4}, 1, 1.00, false},
     {{256, 192, 32, 5, 2, 4}, 1, 1.00, false}, {{128, 192, 64, 3, 4, 8}, 1, 1.00, false},
+#endif
 };
 
 // Workgroups of configuration c that share a CU.
@@ -823,8 +725,9 @@ hipError_t dispatch(const Config& c, dim3 grid, const Operands& op, const TileAr
     FLINT_GEMM_CASE(64, 128, 64, 2, 1, 4)
     FLINT_GEMM_CASE(128, 64, 64, 2, 4, 4)
     FLINT_GEMM_CASE(128, 256, 64, 2, 2, 4)
-    FLINT_GEMM_CASE(256, 128, 64, 2, 2, 4)
     FLINT_GEMM_CASE(128, 192, 64, 3, 2, 4)
+#ifdef FLINT_GEMM_SWEEP
+    FLINT_GEMM_CASE(256, 128, 64, 2, 2, 4)
     FLINT_GEMM_CASE(128, 128, 64, 4, 2, 4)
     FLINT_GEMM_CASE(256, 192, 32, 4, 2, 4)
     FLINT_GEMM_CASE(128, 192, 32, 4, 2, 4)
@@ -839,6 +742,7 @@ hipError_t dispatch(const Config& c, dim3 grid, const Operands& op, const TileAr
     FLINT_GEMM_CASE(128, 192, 32, 6, 2, 4)
     FLINT_GEMM_CASE(256, 192, 32, 5, 2, 4)
     FLINT_GEMM_CASE(128, 192, 64, 3, 4, 8)
+#endif
 #undef FLINT_GEMM_CASE
     return hipErrorInvalidValue;
 }
@@ -935,6 +839,8 @@ hipError_t gemm_tn_workspace(size_t m, size_t n, size_t k, size_t* bytes) {
 
 hipError_t launch_gemm_nt(void* y, const void* x, const void* w, const void* bias, void* aux,
                           Epilogue e, size_t m, size_t n, size_t k, hipStream_t stream) {
+    if (gemm_nt_pipe_eligible(e, m, n, k))
+        return launch_gemm_nt_pipe(y, x, w, bias, aux, e, 1.0f, 1, m, n, k, stream);
     Operands op = make_ops(y, x, w, m, n, k);
     op.bias = static_cast<const float*>(bias);
     op.aux = aux;
@@ -978,6 +884,9 @@ hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_
 
 hipError_t launch_gemm_nt_batched(void* y, const void* x, const void* w, size_t batches,
                                   size_t m, size_t n, size_t k, float scale, hipStream_t stream) {
+    if (gemm_nt_pipe_eligible(Epilogue::kScale, m, n, k))
+        return launch_gemm_nt_pipe(y, x, w, nullptr, nullptr, Epilogue::kScale, scale, batches, m,
+                                   n, k, stream);
     Operands op = make_ops(y, x, w, m, n, k);
     op.scale = scale;
     return run<Layout::kNT, Store::kScale>(op, batches, 0, stream);
