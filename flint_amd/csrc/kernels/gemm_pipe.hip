@@ -58,10 +58,20 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 __device__ __forceinline__ int pipe_key(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 
 // Per-wave C staging of the epilogue: a wave turns one 32-row block of its
-// accumulators into [32][WTN + 8] halves (the pad moves consecutive rows by 16
-// bytes, 4 banks) and stores it back as whole 16-byte row chunks.
-template <int BN>
-constexpr int pipe_ldw() { return BN / 2 + 8; }
+// accumulators into [32][WTN + pad] elements (FP16, or FP32 for the residual
+// epilogue; the pad moves consecutive rows by 16 bytes, 4 banks) and stores it
+// back as whole 16-byte row chunks.
+template <int BN, bool F32>
+struct PipeStaging {
+    static constexpr int kWtn = BN / 2;
+    static constexpr int kElem = F32 ? 4 : 2;              // bytes per element
+    static constexpr int kPerChunk = 16 / kElem;           // elements per 16-byte chunk
+    static constexpr int kLdw = kWtn + kPerChunk;          // row stride (elements)
+    static constexpr int kHalves = 32 * kLdw * kElem / 2;  // one wave's block, in halves
+    static constexpr int kCpr = kWtn / kPerChunk;          // chunks per row
+    static constexpr int kPerLane = 32 * kCpr / 64;        // chunks per lane per block
+    static_assert(32 * kCpr % 64 == 0, "whole store instructions");
+};
 
 template <int BM, int BN, int S, Store ST>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -75,25 +85,24 @@ gemm_nt_pipe(Operands op, TileArgs ta) {
     constexpr int IA = BM / 64, IB = BN / 64;   // loads (16 rows each) per thread per step
     constexpr int PER = IA + IB;
     constexpr int HALF = PER / 2;
-    constexpr bool kBias = ST == Store::kBias || ST == Store::kBiasGelu;
-    constexpr int LDW = pipe_ldw<BN>();
+    constexpr bool kBias =
+        ST == Store::kBias || ST == Store::kBiasGelu || ST == Store::kBiasResidual;
+    constexpr bool kF32 = ST == Store::kBiasResidual;   // y = residual + (sum + bias), FP32
+    using C = PipeStaging<BN, kF32>;
     constexpr int kStageHalves = S * (BM + BN) * BK;
-    constexpr int kCHalves = 32 * LDW;   // one wave's staging block
+    constexpr int kCHalves = C::kHalves;   // one wave's staging block
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "whole 32 x 32 blocks per wave");
     static_assert((S - 2) * PER + PER < 64, "vmcnt range");
     static_assert(ST == Store::kNone || ST == Store::kBias || ST == Store::kBiasGelu ||
-                      ST == Store::kScale, "FP16 outputs only");
+                      ST == Store::kScale || ST == Store::kBiasResidual, "NT epilogues");
     // One LDS object for everything: with a second one, the compiler's LDS-DMA
     // alias tracking put a vmcnt(0) in front of every fragment read.
     __shared__ __attribute__((aligned(16))) _Float16 lds[kStageHalves + 4 * kCHalves];
     auto stage = [&](int st) { return lds + st * (BM + BN) * BK; };
-    // Epilogue: per 32-row block of a wave, CPR 16-byte chunks a row,
-    // PER_LANE stores a lane, per output (GELU writes two).
+    // Epilogue: per 32-row block of a wave, C::kPerLane stores a lane per
+    // output (GELU writes two).
     constexpr int kPasses = ST == Store::kBiasGelu ? 2 : 1;
-    constexpr int CPR = WTN / 8;
-    constexpr int PER_LANE = 32 * CPR / 64;
-    static_assert(32 * CPR % 64 == 0, "whole store instructions");
-    constexpr int kStores = FM * PER_LANE * kPasses;   // buffer stores per wave per tile
+    constexpr int kStores = FM * C::kPerLane * kPasses;   // buffer stores per wave per tile
     constexpr int kBiasLoads = kBias ? FN * 4 : 0;       // buffer loads per wave per tile
 
     const int tid = threadIdx.x;
@@ -286,9 +295,34 @@ gemm_nt_pipe(Operands op, TileArgs ta) {
         // while the next tile's k-loop runs on its prefetched steps.
         const int row_base = t.m0 + wm * WTM;
         const int col_base = t.n0 + wn * WTN;
-        const unsigned out_bytes = unsigned(m) * unsigned(n) * 2u;
+        const unsigned out_bytes = unsigned(m) * unsigned(n) * unsigned(C::kElem);
+        // Byte offset of chunk q of this lane in 32-row block j (past the end
+        // of the output when the chunk is outside it; n % 8 == 0 on this path,
+        // so a chunk is whole once it starts).
+        auto chunk_off = [&](int j, int q, int* r, int* cc) {
+            const int c = q * 64 + lane;
+            *r = c / C::kCpr;
+            *cc = c % C::kCpr;
+            const int gr = row_base + j * 32 + *r, gc = col_base + *cc * C::kPerChunk;
+            return gr < m && gc < n ? (unsigned(gr) * unsigned(n) + unsigned(gc)) * unsigned(C::kElem)
+                                    : 0xfffffff0u;
+        };
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
+            // Residual: this block's chunks are loaded first, so their latency
+            // overlaps the staging writes.
+            f32x4 res[kF32 ? C::kPerLane : 1];
+            if constexpr (kF32) {
+                const auto rres = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<float*>(static_cast<const float*>(op.aux) + t.y_batch), 0,
+                    out_bytes, 0x00020000);
+#pragma unroll
+                for (int q = 0; q < C::kPerLane; ++q) {
+                    int r, cc;
+                    res[q] = __builtin_bit_cast(
+                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(rres, chunk_off(j, q, &r, &cc), 0, 0));
+                }
+            }
 #pragma unroll
             for (int pass = 0; pass < kPasses; ++pass) {
                 // GELU: pass 0 writes pre = RN16(s), pass 1 y = RN16(gelu(s)).
@@ -301,30 +335,39 @@ gemm_nt_pipe(Operands op, TileArgs ta) {
                                    acc[ii][j][g4 * 4 + 2], acc[ii][j][g4 * 4 + 3]};
                         if constexpr (kBias) v += bias[ii][g4];
                         if constexpr (ST == Store::kScale) v *= op.scale;
-                        if (gelu_pass) {
+                        const int at = fr * C::kLdw + ii * 32 + g4 * 8 + fc * 4;
+                        if constexpr (kF32) {
+                            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(cst) + at) = v;
+                        } else {
+                            if (gelu_pass) {
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) v[e] = gelu(v[e]);
+                                for (int e = 0; e < 4; ++e) v[e] = gelu(v[e]);
+                            }
+                            const f16x4 h = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]),
+                                             _Float16(v[3])};
+                            *reinterpret_cast<f16x4*>(cst + at) = h;
                         }
-                        const f16x4 h = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]),
-                                         _Float16(v[3])};
-                        *reinterpret_cast<f16x4*>(cst + fr * LDW + ii * 32 + g4 * 8 + fc * 4) = h;
                     }
                 }
-                _Float16* out = static_cast<_Float16*>(ST == Store::kBiasGelu && pass == 0
-                                                           ? op.aux : op.y) + t.y_batch;
-                const auto rout = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(out), 0,
-                                                                    out_bytes, 0x00020000);
+                void* out = ST == Store::kBiasGelu && pass == 0 ? op.aux : op.y;
+                out = static_cast<char*>(out) + t.y_batch * C::kElem;
+                const auto rout = __builtin_amdgcn_make_buffer_rsrc(out, 0, out_bytes, 0x00020000);
 #pragma unroll
-                for (int q = 0; q < PER_LANE; ++q) {
-                    const int c = q * 64 + lane;
-                    const int r = c / CPR, cc = c % CPR;
-                    const f16x8 v = *reinterpret_cast<const f16x8*>(cst + r * LDW + cc * 8);
-                    const int gr = row_base + j * 32 + r, gc = col_base + cc * 8;
-                    // n % 8 == 0 on this path: a chunk is whole once it starts.
-                    const unsigned off = gr < m && gc < n ? (unsigned(gr) * unsigned(n) + unsigned(gc)) * 2u
-                                                          : 0xfffffff0u;
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), rout, off,
-                                                           0, 0);
+                for (int q = 0; q < C::kPerLane; ++q) {
+                    int r, cc;
+                    const unsigned off = chunk_off(j, q, &r, &cc);
+                    i32x4 v;
+                    if constexpr (kF32) {
+                        // y = residual + (sum + bias): one FP32 add, as the
+                        // unstaged epilogue does it.
+                        const f32x4 sb = *reinterpret_cast<const f32x4*>(
+                            reinterpret_cast<const float*>(cst) + r * C::kLdw + cc * 4);
+                        v = __builtin_bit_cast(i32x4, res[q] + sb);
+                    } else {
+                        v = __builtin_bit_cast(
+                            i32x4, *reinterpret_cast<const f16x8*>(cst + r * C::kLdw + cc * 8));
+                    }
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rout, off, 0, 0);
                 }
             }
         }
@@ -343,7 +386,7 @@ struct PipeConfig {
     int bm, bn, stages;
 };
 
-constexpr PipeConfig kPipeConfigs[] = {{256, 256, 3}, {256, 192, 4}};
+constexpr PipeConfig kPipeConfigs[] = {{256, 256, 3}, {256, 192, 4}, {128, 192, 4}};
 
 // FLINT_GEMM_PIPE: "0" routes every NT call to gemm.hip's kernels;
 // "bm,bn,stages" forces one of kPipeConfigs (tuning sweeps; read per call).
@@ -369,16 +412,24 @@ bool pipe_forced(PipeConfig* out, bool* disabled) {
 // The macro-tile: whole waves of tiles over the CUs weigh most (a K = 768
 // tile is short, so a partial last wave costs nearly a full one); among
 // equal wave counts the larger tile needs fewer bytes per FLOP.
-PipeConfig pick_pipe(size_t m, size_t n, size_t slices, int cus) {
+// LDS bytes of a configuration: its stages plus four per-wave staging blocks.
+constexpr size_t pipe_lds_bytes(int bm, int bn, int stages, bool f32) {
+    const int wtn = bn / 2, per_chunk = f32 ? 4 : 8;
+    return size_t(stages) * (bm + bn) * kPipeBK * 2 + 4 * 32 * size_t(wtn + per_chunk) * (f32 ? 4 : 2);
+}
+constexpr size_t kPipeMaxLds = 160 * 1024;
+
+PipeConfig pick_pipe(size_t m, size_t n, size_t slices, int cus, bool f32) {
     PipeConfig best = kPipeConfigs[0];
     double best_cost = 1e300;
     for (const PipeConfig& c : kPipeConfigs) {
+        if (pipe_lds_bytes(c.bm, c.bn, c.stages, f32) > kPipeMaxLds) continue;
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn) *
                              double(slices);
         const double rounds = std::ceil(tiles / cus);
         // Relative time of one tile: its area over its measured throughput per
         // unit area (256 x 256 as 1; the smaller tiles move more bytes per FLOP).
-        const double eff = c.bn == 256 ? 1.0 : 0.97;
+        const double eff = c.bm == 128 ? 0.80 : (c.bn == 256 ? 1.0 : 0.97);
         const double cost = rounds * double(c.bm) * double(c.bn) / eff;
         if (cost < best_cost * 0.999) {
             best_cost = cost;
@@ -405,13 +456,18 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     size_t gx = std::min(total, size_t(cus));
     if (gx >= 8) gx -= gx % 8;
     const dim3 grid(unsigned(gx), 1, 1);
+    constexpr bool kF32 = ST == Store::kBiasResidual;
 #define FLINT_PIPE_CASE(BM_, BN_, S_)                                                         \
-    if (c.bm == BM_ && c.bn == BN_ && c.stages == S_) {                                       \
-        hipLaunchKernelGGL((gemm_nt_pipe<BM_, BN_, S_, ST>), grid, dim3(256), 0, stream, op, ta); \
-        return hipGetLastError();                                                             \
+    if constexpr (pipe_lds_bytes(BM_, BN_, S_, kF32) <= kPipeMaxLds) {                        \
+        if (c.bm == BM_ && c.bn == BN_ && c.stages == S_) {                                   \
+            hipLaunchKernelGGL((gemm_nt_pipe<BM_, BN_, S_, ST>), grid, dim3(256), 0, stream, op, \
+                               ta);                                                           \
+            return hipGetLastError();                                                         \
+        }                                                                                     \
     }
     FLINT_PIPE_CASE(256, 256, 3)
     FLINT_PIPE_CASE(256, 192, 4)
+    FLINT_PIPE_CASE(128, 192, 4)
 #undef FLINT_PIPE_CASE
     return hipErrorInvalidValue;
 }
@@ -423,15 +479,17 @@ bool gemm_nt_pipe_eligible(Epilogue e, size_t m, size_t n, size_t k) {
     PipeConfig forced;
     const bool force = pipe_forced(&forced, &disabled);
     if (disabled || m == 0 || n == 0 || n % 8 != 0 || k % kPipeBK != 0 || k < kPipeBK) return false;
-    // The epilogue's buffer stores address one slice's output with 32-bit offsets.
-    if (m * n * 2 >= (size_t{1} << 31)) return false;
+    // The epilogue's buffer stores address one slice's output with 32-bit
+    // offsets (FP32 for the residual epilogue).
+    if (m * n * (e == Epilogue::kBiasResidual ? 4 : 2) >= (size_t{1} << 31)) return false;
     if (e != Epilogue::kNone && e != Epilogue::kBias && e != Epilogue::kBiasGelu &&
-        e != Epilogue::kScale) {
+        e != Epilogue::kScale && e != Epilogue::kBiasResidual) {
         return false;
     }
-    // Narrow outputs (n = 768 at 8,192 rows: 128 tiles of 256 x 192) leave
-    // half the CUs idle; gemm.hip's 128-row tiles fill them.
-    return force || n >= 1024;
+    // The residual outputs of GPT-2 are 768 wide: 128-row tiles are needed to
+    // fill the CUs there, and gemm.hip's 128 x 192 x 64 kernel with the
+    // residual prefetched into registers measured as fast as this one's.
+    return force || e != Epilogue::kBiasResidual || n >= 1024;
 }
 
 hipError_t launch_gemm_nt_pipe(void* y, const void* x, const void* w, const void* bias, void* aux,
@@ -451,12 +509,16 @@ hipError_t launch_gemm_nt_pipe(void* y, const void* x, const void* w, const void
     op.k = int(k);
     PipeConfig c;
     bool disabled = false;
-    if (!pipe_forced(&c, &disabled)) c = pick_pipe(m, n, slices, cus);
+    const bool f32 = e == Epilogue::kBiasResidual;
+    if (!pipe_forced(&c, &disabled) || pipe_lds_bytes(c.bm, c.bn, c.stages, f32) > kPipeMaxLds)
+        c = pick_pipe(m, n, slices, cus, f32);
     switch (e) {
     case Epilogue::kNone: return launch_pipe<Store::kNone>(c, op, slices, cus, stream);
     case Epilogue::kBias: return launch_pipe<Store::kBias>(c, op, slices, cus, stream);
     case Epilogue::kBiasGelu: return launch_pipe<Store::kBiasGelu>(c, op, slices, cus, stream);
     case Epilogue::kScale: return launch_pipe<Store::kScale>(c, op, slices, cus, stream);
+    case Epilogue::kBiasResidual:
+        return launch_pipe<Store::kBiasResidual>(c, op, slices, cus, stream);
     default: return hipErrorInvalidValue;
     }
 }

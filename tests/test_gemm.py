@@ -260,3 +260,60 @@ def test_deterministic(flint, cuda):
     flint.gemm_nt(b, x, w, m, n, k)
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+# Every configuration of the one-wave-per-SIMD NT pipeline (gemm_pipe.hip),
+# forced through FLINT_GEMM_PIPE, with every epilogue it serves: edge tiles in
+# m and n, fewer k-steps than stages, and more tiles than CUs (each workgroup
+# then walks several, the next one's loads streaming under this one's stores).
+PIPE_CONFIGS = ["256,256,3", "256,192,4", "128,192,4"]
+PIPE_SHAPES = [(300, 200, 64), (4315, 4600, 96)]
+
+
+@pytest.mark.parametrize("cfg", PIPE_CONFIGS)
+@pytest.mark.parametrize("m,n,k", PIPE_SHAPES)
+@pytest.mark.parametrize("epi", ["none", "bias", "gelu", "residual"])
+def test_nt_pipe_forced(flint, cuda, monkeypatch, cfg, m, n, k, epi):
+    monkeypatch.setenv("FLINT_GEMM_PIPE", cfg)
+    x = uniform((m, k), 40)
+    w = normal((n, k), 41, 0.05, torch.float16)
+    b = normal((n,), 42, 0.02)
+    s = ref_nt(x, w)
+    xd, wd, bd = x.to(cuda), w.to(cuda), b.to(cuda)
+    if epi == "none":
+        y = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
+        flint.gemm_nt(y, xd, wd, m, n, k)
+        torch.cuda.synchronize()
+        assert rel_err(y.cpu(), s) <= TOL
+    elif epi == "bias":
+        y = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
+        flint.gemm_nt_bias(y, xd, wd, bd, m, n, k)
+        torch.cuda.synchronize()
+        assert rel_err(y.cpu(), s + b) <= TOL
+    elif epi == "gelu":
+        y = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
+        pre = torch.full_like(y, float("nan"))
+        flint.gemm_nt_bias_gelu(y, pre, xd, wd, bd, m, n, k)
+        torch.cuda.synchronize()
+        assert rel_err(pre.cpu(), s + b) <= TOL
+        gelu = torch.nn.functional.gelu((s + b).double(), approximate="tanh")
+        assert rel_err(y.cpu(), gelu) <= TOL
+    else:
+        r = normal((m, n), 43)
+        y = torch.full((m, n), float("nan"), dtype=torch.float32, device=cuda)
+        flint.gemm_nt_bias_residual(y, xd, wd, bd, r.to(cuda), m, n, k)
+        torch.cuda.synchronize()
+        assert rel_err(y.cpu(), r + (s + b)) <= TOL
+
+
+@pytest.mark.parametrize("cfg", PIPE_CONFIGS)
+def test_nt_batched_pipe_forced(flint, cuda, monkeypatch, cfg):
+    monkeypatch.setenv("FLINT_GEMM_PIPE", cfg)
+    batches, m, n, k = 5, 264, 200, 64
+    x = uniform((batches, m, k), 44)
+    w = uniform((batches, n, k), 45)
+    y = torch.full((batches, m, n), float("nan"), dtype=torch.float16, device=cuda)
+    flint.gemm_nt_batched(y, x.to(cuda), w.to(cuda), batches, m, n, k, 0.125)
+    torch.cuda.synchronize()
+    ref = torch.bmm(x.float(), w.float().transpose(1, 2).contiguous()) * 0.125
+    assert rel_err(y.cpu(), ref) <= TOL
