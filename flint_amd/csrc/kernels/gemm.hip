@@ -839,8 +839,9 @@ hipError_t gemm_tn_workspace(size_t m, size_t n, size_t k, size_t* bytes) {
 
 hipError_t launch_gemm_nt(void* y, const void* x, const void* w, const void* bias, void* aux,
                           Epilogue e, size_t m, size_t n, size_t k, hipStream_t stream) {
-    if (gemm_nt_pipe_eligible(e, m, n, k))
-        return launch_gemm_nt_pipe(y, x, w, bias, aux, e, 1.0f, 1, m, n, k, stream);
+    if (gemm_pipe_eligible(GemmLayout::kNT, e, m, n, k))
+        return launch_gemm_pipe(GemmLayout::kNT, e, y, x, w, bias, aux, 1.0f, 1, m, n, k, false,
+                                nullptr, 0, stream);
     Operands op = make_ops(y, x, w, m, n, k);
     op.bias = static_cast<const float*>(bias);
     op.aux = aux;
@@ -855,6 +856,9 @@ hipError_t launch_gemm_nt(void* y, const void* x, const void* w, const void* bia
 
 hipError_t launch_gemm_nn(void* y, const void* x, const void* w, const void* aux, Epilogue e,
                           size_t m, size_t n, size_t k, hipStream_t stream) {
+    if (gemm_pipe_eligible(GemmLayout::kNN, e, m, n, k))
+        return launch_gemm_pipe(GemmLayout::kNN, e, y, x, w, nullptr, const_cast<void*>(aux), 1.0f,
+                                1, m, n, k, false, nullptr, 0, stream);
     Operands op = make_ops(y, x, w, m, n, k);
     op.aux = const_cast<void*>(aux);
     switch (e) {
@@ -871,10 +875,14 @@ hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_
     Operands op = make_ops(y, x, w, m, n, k);
     op.accumulate = accumulate ? 1 : 0;
     op.partials = splits > 1 ? static_cast<float*>(workspace) : nullptr;
-    if (hipError_t e = run<Layout::kTN, Store::kTn>(op, size_t(splits), len, stream);
-        e != hipSuccess || splits == 1) {
-        return e;
+    hipError_t err;
+    if (gemm_pipe_eligible(GemmLayout::kTN, kTnFloat, m, n, k)) {
+        err = launch_gemm_pipe(GemmLayout::kTN, kTnFloat, y, x, w, nullptr, nullptr, 1.0f,
+                               size_t(splits), m, n, k, accumulate, op.partials, len, stream);
+    } else {
+        err = run<Layout::kTN, Store::kTn>(op, size_t(splits), len, stream);
     }
+    if (err != hipSuccess || splits == 1) return err;
     const size_t quads = m * n / 4;
     const unsigned blocks = unsigned(std::clamp<size_t>((quads + 255) / 256, 1, 8192));
     hipLaunchKernelGGL(tn_reduce, dim3(blocks), dim3(256), 0, stream, static_cast<float*>(y),
@@ -884,9 +892,9 @@ hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_
 
 hipError_t launch_gemm_nt_batched(void* y, const void* x, const void* w, size_t batches,
                                   size_t m, size_t n, size_t k, float scale, hipStream_t stream) {
-    if (gemm_nt_pipe_eligible(Epilogue::kScale, m, n, k))
-        return launch_gemm_nt_pipe(y, x, w, nullptr, nullptr, Epilogue::kScale, scale, batches, m,
-                                   n, k, stream);
+    if (gemm_pipe_eligible(GemmLayout::kNT, Epilogue::kScale, m, n, k))
+        return launch_gemm_pipe(GemmLayout::kNT, Epilogue::kScale, y, x, w, nullptr, nullptr, scale,
+                                batches, m, n, k, false, nullptr, 0, stream);
     Operands op = make_ops(y, x, w, m, n, k);
     op.scale = scale;
     return run<Layout::kNT, Store::kScale>(op, batches, 0, stream);
@@ -894,12 +902,18 @@ hipError_t launch_gemm_nt_batched(void* y, const void* x, const void* w, size_t 
 
 hipError_t launch_gemm_nn_batched(void* y, const void* x, const void* w, size_t batches,
                                   size_t m, size_t n, size_t k, hipStream_t stream) {
+    if (gemm_pipe_eligible(GemmLayout::kNN, Epilogue::kNone, m, n, k))
+        return launch_gemm_pipe(GemmLayout::kNN, Epilogue::kNone, y, x, w, nullptr, nullptr, 1.0f,
+                                batches, m, n, k, false, nullptr, 0, stream);
     Operands op = make_ops(y, x, w, m, n, k);
     return run<Layout::kNN, Store::kNone>(op, batches, 0, stream);
 }
 
 hipError_t launch_gemm_tn_batched(void* y, const void* x, const void* w, size_t batches,
                                   size_t m, size_t n, size_t k, hipStream_t stream) {
+    if (gemm_pipe_eligible(GemmLayout::kTN, Epilogue::kNone, m, n, k))
+        return launch_gemm_pipe(GemmLayout::kTN, Epilogue::kNone, y, x, w, nullptr, nullptr, 1.0f,
+                                batches, m, n, k, false, nullptr, 0, stream);
     Operands op = make_ops(y, x, w, m, n, k);
     return run<Layout::kTN, Store::kTnHalf>(op, batches, 0, stream);
 }

@@ -1,8 +1,7 @@
-// NT GEMM on gfx950 with one wave per SIMD and large wave tiles: the path for
-// whole k-steps of 32 and rows of 16-byte multiples (n % 8 == 0, k % 32 == 0),
-// which covers every NT shape of GPT-2 (forward linear layers, logits, and the
-// batched QK^T). Other NT shapes, and the NN / TN layouts, run gemm.hip's
-// kernels.
+// The GEMM pipeline on gfx950 with one wave per SIMD and large wave tiles,
+// for all three layouts (NT, NN, TN, and their batched forms) whenever k is a
+// multiple of 32 and the output rows are 16-byte multiples. Other shapes run
+// gemm.hip's kernels.
 //
 // Why this shape of kernel (measured on MI355X):
 //  * A CU pulls about 110 GB/s (~45 B/clk) from L2 through the vector memory
@@ -12,20 +11,34 @@
 //    128 x 96 or 128 x 128 accumulators per wave (192 / 256 AGPRs), so one
 //    wave runs per SIMD and overlap has to come from the instruction stream,
 //    not from other waves.
-//  * The k-loop takes k-steps of 32 through S = 4 LDS stages (256 x 256: 32 KB
-//    a stage). The loads of step g + 3 are issued half during the first and
-//    half during the second k16 sub-step of the steps before it, one
-//    buffer_load ... lds after every second MFMA, and the fragment reads of the
-//    next sub-step one after every MFMA: no burst of loads stalls the wave, and
-//    three steps of latency are covered. One barrier per step sits between the
-//    two sub-steps, after the last fragment read of the step.
-//  * The epilogue stages the tile through LDS (the stages are free by then) so
-//    that every global store instruction writes whole rows: 64 lanes x 16 B.
-//    Stores straight from the MFMA layout cover 32 rows x 16 B each and ran the
-//    output at under 2 TB/s; the staged form more than doubles that.
-//  * Edge tiles need no separate path: each operand's buffer resource ends at
-//    the last valid row, so loads past it read zeros (and a row of A or B only
-//    ever meets its own output row or column), and the stores are masked.
+//  * The k-loop takes k-steps of 32 through S LDS stages. The loads of step
+//    g + S - 1 are issued half during the first and half during the second k16
+//    sub-step of the steps before it, one buffer_load ... lds after every
+//    second MFMA, and the fragment reads of the next sub-step one after every
+//    MFMA: no burst of loads stalls the wave, and S - 1 steps of latency are
+//    covered. One barrier per step sits between the two sub-steps, after the
+//    last fragment read of the step.
+//  * Operands whose rows run along k (NT's x and w, NN's x) sit in LDS as
+//    [rows][32 k]. Operands stored k-major (NN's and TN's w, TN's x) are
+//    loaded as they lie, [32 k][rows], and their MFMA fragments come from
+//    ds_read_b64_tr_b16: within 16 lanes, lane j addresses 4 halves of row
+//    k0 + j / 4 at column c0 + 4 (j % 4), and lane i receives column c0 + i of
+//    rows k0 .. k0 + 3, so two such reads give a lane its 8 consecutive k.
+//    Either way a load instruction fills 1 KB of LDS in one piece, and 16-byte
+//    chunks are XOR-swizzled per row against bank conflicts.
+//  * Workgroups are persistent and walk their tiles as one stream of k-steps,
+//    so the next tile's first steps load under this tile's epilogue.
+//  * The epilogue stages each wave's accumulators through LDS, 32 rows (FP16
+//    outputs) or 16 rows (FP32 values) at a time, so that every global store
+//    instruction writes whole rows: 64 lanes x 16 B. Stores straight from the
+//    MFMA layout cover 32 rows x 16 B each and ran the output at under 2 TB/s.
+//    They are buffer stores: a chunk outside the output gets an offset past
+//    the resource's end and is dropped, so every wave issues the same count,
+//    which the k-loop's waits rely on to let them drain under the next tile.
+//  * Edge tiles need no separate path: loads past an operand's end read zeros
+//    (or, for a k-major operand's last columns, the next row's first values),
+//    a row of either operand only ever meets its own output row or column, and
+//    the stores are masked.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -42,6 +55,7 @@ namespace {
 constexpr int kPipeBK = 32;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int cap63(int n) { return n < 63 ? n : 63; }
 
@@ -52,138 +66,186 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
-// Key of the 64-byte LDS rows (4 chunks of 16 B): rows r and r + 4 differ, so
-// the 16 lanes a ds_read_b128 serves per cycle (16 rows, one chunk) cover all
-// four chunk positions four times and no 16-byte bank group twice in a row of 4.
-__device__ __forceinline__ int pipe_key(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+// Key of the [rows][32 k] layout (64-byte rows, 4 chunks): the 16 lanes a
+// ds_read_b128 serves per cycle (16 rows, one chunk) cover every chunk
+// position four times and no 16-byte bank group twice in a row of 4.
+__device__ __forceinline__ int row_key(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+// Key of the [32 k][rows] layout: rows k .. k + 3, which one transposing read
+// of 16 lanes touches (2 chunks each), land on 8 distinct chunk positions of an
+// aligned group of 8 (the XOR stays inside the group, hence inside the row).
+__host__ __device__ constexpr int kmajor_key(int k) { return 2 * (k & 3); }
 
-// Per-wave C staging of the epilogue: a wave turns one 32-row block of its
-// accumulators into [32][WTN + pad] elements (FP16, or FP32 for the residual
-// epilogue; the pad moves consecutive rows by 16 bytes, 4 banks) and stores it
-// back as whole 16-byte row chunks.
-template <int BN, bool F32>
-struct PipeStaging {
+// What the epilogue stages per wave and writes per 16-byte chunk.
+template <int BN, Store ST>
+struct PipeEpi {
+    // FP32 values are staged when the output is FP32 (residual, TN) or when
+    // the rounding needs a value that only the store pass reads (dGELU's pre).
+    static constexpr bool kF32 =
+        ST == Store::kBiasResidual || ST == Store::kTn || ST == Store::kDGelu;
+    static constexpr int kOutElem = ST == Store::kBiasResidual || ST == Store::kTn ? 4 : 2;
     static constexpr int kWtn = BN / 2;
-    static constexpr int kElem = F32 ? 4 : 2;              // bytes per element
-    static constexpr int kPerChunk = 16 / kElem;           // elements per 16-byte chunk
-    static constexpr int kLdw = kWtn + kPerChunk;          // row stride (elements)
-    static constexpr int kHalves = 32 * kLdw * kElem / 2;  // one wave's block, in halves
-    static constexpr int kCpr = kWtn / kPerChunk;          // chunks per row
-    static constexpr int kPerLane = 32 * kCpr / 64;        // chunks per lane per block
-    static_assert(32 * kCpr % 64 == 0, "whole store instructions");
+    static constexpr int kPerChunk = kF32 ? 4 : 8;            // values per staged chunk
+    static constexpr int kRows = kF32 ? 16 : 32;              // rows staged at a time
+    static constexpr int kLdw = kWtn + kPerChunk;             // staged row stride (values)
+    static constexpr int kHalves = kRows * kLdw * (kF32 ? 2 : 1);   // per wave, in halves
+    static constexpr int kCpr = kWtn / kPerChunk;             // chunks per staged row
+    static constexpr int kPerLane = kRows * kCpr / 64;        // chunks per lane per block
+    static_assert(kRows * kCpr % 64 == 0, "whole store instructions");
+    static constexpr int kPasses = ST == Store::kBiasGelu ? 2 : 1;
+    static constexpr int kSubs = 32 / kRows;                  // staged blocks per 32 rows
 };
 
-template <int BM, int BN, int S, Store ST>
+template <int BM, int BN, int S, Layout L, Store ST>
+constexpr size_t pipe_lds_bytes() {
+    using E = PipeEpi<BN, ST>;
+    return size_t(S) * (BM + BN) * kPipeBK * 2 + 4 * size_t(E::kHalves) * 2;
+}
+constexpr size_t kPipeMaxLds = 160 * 1024;
+
+template <int BM, int BN, int S, Layout L, Store ST>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-gemm_nt_pipe(Operands op, TileArgs ta) {
+gemm_pipe(Operands op, TileArgs ta) {
     // The host pass only needs a kernel to emit a launch stub for; the buffer
     // resource builtins below exist on the device side only.
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int BK = kPipeBK;
     constexpr int WTM = BM / 2, WTN = BN / 2;   // 2 x 2 waves
     constexpr int FM = WTM / 32, FN = WTN / 32;
-    constexpr int IA = BM / 64, IB = BN / 64;   // loads (16 rows each) per thread per step
+    constexpr int IA = BM / 64, IB = BN / 64;   // 1 KB loads per thread per step
     constexpr int PER = IA + IB;
     constexpr int HALF = PER / 2;
+    // x side (rows m, the MFMA's B operand) and w side (rows n, its A operand)
+    // are k-major ([32 k][rows] in LDS) or row-major ([rows][32 k]).
+    constexpr bool kXM = L == Layout::kTN;
+    constexpr bool kWM = L != Layout::kNT;
     constexpr bool kBias =
         ST == Store::kBias || ST == Store::kBiasGelu || ST == Store::kBiasResidual;
-    constexpr bool kF32 = ST == Store::kBiasResidual;   // y = residual + (sum + bias), FP32
-    using C = PipeStaging<BN, kF32>;
+    using E = PipeEpi<BN, ST>;
     constexpr int kStageHalves = S * (BM + BN) * BK;
-    constexpr int kCHalves = C::kHalves;   // one wave's staging block
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "whole 32 x 32 blocks per wave");
+    static_assert(pipe_lds_bytes<BM, BN, S, L, ST>() <= kPipeMaxLds, "LDS");
     static_assert((S - 2) * PER + PER < 64, "vmcnt range");
-    static_assert(ST == Store::kNone || ST == Store::kBias || ST == Store::kBiasGelu ||
-                      ST == Store::kScale || ST == Store::kBiasResidual, "NT epilogues");
+    // Buffer stores per wave per tile, bias loads per wave per tile.
+    constexpr int kStores = FM * E::kSubs * E::kPerLane * E::kPasses;
+    constexpr int kBiasLoads = kBias ? FN * 4 : 0;
     // One LDS object for everything: with a second one, the compiler's LDS-DMA
     // alias tracking put a vmcnt(0) in front of every fragment read.
-    __shared__ __attribute__((aligned(16))) _Float16 lds[kStageHalves + 4 * kCHalves];
+    __shared__ __attribute__((aligned(16))) _Float16 lds[kStageHalves + 4 * E::kHalves];
     auto stage = [&](int st) { return lds + st * (BM + BN) * BK; };
-    // Epilogue: per 32-row block of a wave, C::kPerLane stores a lane per
-    // output (GELU writes two).
-    constexpr int kPasses = ST == Store::kBiasGelu ? 2 : 1;
-    constexpr int kStores = FM * C::kPerLane * kPasses;   // buffer stores per wave per tile
-    constexpr int kBiasLoads = kBias ? FN * 4 : 0;       // buffer loads per wave per tile
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int m = op.m, n = op.n, K = op.k;
-    _Float16* const cst = lds + kStageHalves + wave * kCHalves;
+    const bool split = ST == Store::kTn && op.partials != nullptr;
+    _Float16* const cst = lds + kStageHalves + wave * E::kHalves;
 
     // This workgroup's tiles: ids blockIdx.x, + gridDim.x, ... (gridDim.x is a
     // multiple of 8 when there are 8 or more tiles, so they stay on one XCD).
     const unsigned total = unsigned(ta.tiles_per_slice) * unsigned(ta.slices);
     const int n_tiles = int((total - 1 - blockIdx.x) / gridDim.x) + 1;
-    const int steps = K / BK;
     struct Tile {
-        int m0, n0;
-        size_t y_batch;
-        const _Float16* a;
+        int m0, n0, k_begin, k_end, slice;
+        size_t y_off;                 // output elements before this tile's slice
+        const _Float16* a;            // x side: the tile's first row (k-contiguous) or column
         const _Float16* b;
-        unsigned a_bytes, b_bytes;
+        unsigned a_bytes, b_bytes;    // each operand's resource length
     };
     auto tile = [&](int i) {
         Tile t;
-        int slice, tm, tn;
-        map_tile(ta, blockIdx.x + unsigned(i) * gridDim.x, &slice, &tm, &tn);
+        int tm, tn;
+        map_tile(ta, blockIdx.x + unsigned(i) * gridDim.x, &t.slice, &tm, &tn);
         t.m0 = tm * BM;
         t.n0 = tn * BN;
-        t.a = op.x;
-        t.b = op.w;
-        t.y_batch = 0;
-        if (ta.slices > 1) {
-            t.a += size_t(slice) * m * K;
-            t.b += size_t(slice) * n * K;
-            t.y_batch = size_t(slice) * m * n;
+        t.k_begin = 0;
+        t.k_end = K;
+        t.y_off = 0;
+        const _Float16* xs = op.x;
+        const _Float16* ws = op.w;
+        if (split) {
+            t.k_begin = t.slice * ta.split_len;
+            t.k_end = min(K, t.k_begin + ta.split_len);
+            t.y_off = size_t(t.slice) * m * n;
+        } else if (ta.slices > 1) {
+            xs += size_t(t.slice) * m * K;
+            ws += size_t(t.slice) * n * K;
+            t.y_off = size_t(t.slice) * m * n;
         }
-        t.a += size_t(t.m0) * K;
-        t.b += size_t(t.n0) * K;
-        // Each operand's resource ends at its last valid row of the tile.
-        t.a_bytes = unsigned(min(BM, m - t.m0)) * unsigned(K) * 2u;
-        t.b_bytes = unsigned(min(BN, n - t.n0)) * unsigned(K) * 2u;
+        // Row-major operands: the resource ends at the tile's last valid row.
+        // k-major ones: at the end of the slice's matrix.
+        if (kXM) {
+            t.a = xs + t.m0;
+            t.a_bytes = unsigned((size_t(K) * m - t.m0) * 2);
+        } else {
+            t.a = xs + size_t(t.m0) * K;
+            t.a_bytes = unsigned(min(BM, m - t.m0)) * unsigned(K) * 2u;
+        }
+        if (kWM) {
+            t.b = ws + t.n0;
+            t.b_bytes = unsigned((size_t(K) * n - t.n0) * 2);
+        } else {
+            t.b = ws + size_t(t.n0) * K;
+            t.b_bytes = unsigned(min(BN, n - t.n0)) * unsigned(K) * 2u;
+        }
         return t;
     };
 
-    // Load instruction q of a step: 16 rows x 64 bytes; lane l fills LDS row
-    // l / 4 of the group, slot l % 4, with the global chunk the key puts there.
-    const int lrow = lane >> 2;
-    const unsigned lane_off = unsigned((lrow * K + ((lane & 3) ^ pipe_key(lrow)) * 8) * 2);
+    // Instruction u = q * 4 + wave of an operand fills LDS bytes
+    // [u KB, u KB + 1 KB) of its region; lane l writes bytes l * 16 .. + 16.
+    // voff: the lane's byte offset in the global operand for k = 0 (the
+    // k-step goes in the scalar offset).
+    const int a_ld = kXM ? m : K;
+    const int b_ld = kWM ? n : K;
+    auto lane_voff = [&](int q, int rows, bool kmajor, int ld) {
+        const int u = q * 4 + wave;
+        if (kmajor) {
+            const int p = u * 1024 + lane * 16;       // byte in the [32][rows] tile
+            const int r = p / (rows * 2);             // k within the step
+            const int pos = (p % (rows * 2)) / 16;    // chunk position in the row
+            const int c = pos ^ kmajor_key(r);
+            return unsigned((r * ld + c * 8) * 2);
+        }
+        const int row = u * 16 + (lane >> 2);
+        return unsigned((row * ld + ((lane & 3) ^ row_key(lane >> 2)) * 8) * 2);
+    };
     unsigned voff[PER];
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
-        const int row0 = ((q < IA ? q : q - IA) * 4 + wave) * 16;
-        voff[q] = lane_off + unsigned(row0 * K * 2);
-    }
+    for (int q = 0; q < PER; ++q)
+        voff[q] = q < IA ? lane_voff(q, BM, kXM, a_ld) : lane_voff(q - IA, BN, kWM, b_ld);
+
     // The issue side walks one stream of k-steps over all of the workgroup's
     // tiles, S steps ahead of the MFMAs; past the last one it reloads the last
     // step (into a stage nobody reads), so every wait counts the same loads.
     struct Issue {
-        int tile, k0, st;
+        int tile, k0, k_end, st;
         __amdgpu_buffer_rsrc_t ra, rb;
     };
     auto rsrc_of = [&](Issue& is) {
         const Tile t = tile(is.tile);
+        is.k0 = t.k_begin;
+        is.k_end = t.k_end;
         is.ra = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(t.a), 0, t.a_bytes, 0x00020000);
         is.rb = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(t.b), 0, t.b_bytes, 0x00020000);
     };
     auto advance = [&](Issue& is) {
         is.st = is.st + 1 == S ? 0 : is.st + 1;
-        if (is.k0 + BK < K) {
+        if (is.k0 + BK < is.k_end) {
             is.k0 += BK;
         } else if (is.tile + 1 < n_tiles) {
-            is.k0 = 0;
             ++is.tile;
             rsrc_of(is);
         }
     };
     auto issue_q = [&](const Issue& is, int q) {
-        const int row0 = ((q < IA ? q : q - IA) * 4 + wave) * 16;
-        lds_half* dst = (lds_half*)(stage(is.st) + (q < IA ? 0 : BM * BK) + row0 * BK);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(q < IA ? is.ra : is.rb,
+        const bool xq = q < IA;
+        const int u = (xq ? q : q - IA) * 4 + wave;
+        lds_half* dst = (lds_half*)(stage(is.st) + (xq ? 0 : BM * BK) + u * 512);
+        // Row-major: k0 halves into every row. k-major: k0 rows down.
+        const unsigned soff = unsigned(is.k0) * 2u * unsigned(xq ? (kXM ? a_ld : 1) : (kWM ? b_ld : 1));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xq ? is.ra : is.rb,
                                                  (__attribute__((address_space(3))) void*)dst, 16,
-                                                 voff[q], unsigned(is.k0) * 2u, 0, 0);
+                                                 voff[q], soff, 0, 0);
     };
 
     f32x16 acc[FN][FM];
@@ -193,15 +255,53 @@ gemm_nt_pipe(Operands op, TileArgs ta) {
         for (int j = 0; j < FM; ++j) acc[i][j] = f32x16{};
 
     const int fr = lane & 31, fc = lane >> 5;
-    auto frag = [&](int row, int kk) { return row * BK + (((kk * 2 + fc) ^ pipe_key(row)) * 8); };
+    // Fragment of operand rows r0 .. r0 + 31, k16 sub-step kk, from an LDS
+    // region of `rows` rows: lane l gets row r0 + l % 32, k 8 (l / 32) .. + 8.
+    auto frag_rowmajor = [&](const _Float16* region, int r0, int kk) {
+        const int row = r0 + fr;
+        return *reinterpret_cast<const f16x8*>(region + row * BK +
+                                               (((kk * 2 + fc) ^ row_key(row)) * 8));
+    };
+    // Lane j of a 16-lane group addresses row k0 + j / 4, columns
+    // c0 + 4 (j % 4) .. + 3; the read hands lane i column c0 + i of rows
+    // k0 .. k0 + 3. k0 = 16 kk + 8 (l / 32) + 4 t, c0 = r0 + 16 ((l / 16) % 2).
+    // The reads are inline asm: the compiler's LDS-DMA alias tracking put a
+    // vmcnt(0) in front of every ds_read_b64_tr_b16 builtin (it cannot tell
+    // them from the stage being loaded), which serialised the pipeline. The
+    // asm results are unknown to its waitcnt pass, so the k-loop waits for
+    // lgkmcnt(0) itself before the sub-step that uses them.
+    auto frag_kmajor = [&](const _Float16* region, int rows, int r0, int kk) {
+        const int j = lane & 15;
+        const int col = r0 + 16 * ((lane >> 4) & 1) + 4 * (j & 3);
+        const int key = kmajor_key(j >> 2);
+        const int chunk = ((col >> 3) ^ key) * 8 + (col & 4);   // halves into the row
+        const int k = kk * 16 + 8 * fc + (j >> 2);
+        const unsigned a0 = unsigned(reinterpret_cast<uintptr_t>(
+            (lds_half*)(region + k * rows + chunk)));
+        i32x2 lo, hi;
+        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo) : "v"(a0));
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(hi) : "v"(a0), "i"(4 * rows * 2));
+        return __builtin_shufflevector(__builtin_bit_cast(f16x4, lo), __builtin_bit_cast(f16x4, hi),
+                                       0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    // lgkmcnt(0) before a sub-step whose fragments include asm reads.
+    auto wait_frags = [&]() {
+        if constexpr (kXM || kWM) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     // Fragment read idx (< FM: an x fragment, else a w fragment) of sub-step kk.
     auto read_one = [&](int st, int kk, int idx, f16x8 (&xf)[FM], f16x8 (&wf)[FN]) {
         const _Float16* s0 = stage(st);
         if (idx < FM) {
-            xf[idx] = *reinterpret_cast<const f16x8*>(s0 + frag(wm * WTM + idx * 32 + fr, kk));
+            const int r0 = wm * WTM + idx * 32;
+            xf[idx] = kXM ? frag_kmajor(s0, BM, r0, kk) : frag_rowmajor(s0, r0, kk);
         } else {
-            const int i = idx - FM;
-            wf[i] = *reinterpret_cast<const f16x8*>(s0 + BM * BK + frag(wn * WTN + i * 32 + fr, kk));
+            const int r0 = wn * WTN + (idx - FM) * 32;
+            wf[idx - FM] = kWM ? frag_kmajor(s0 + BM * BK, BN, r0, kk)
+                               : frag_rowmajor(s0 + BM * BK, r0, kk);
         }
     };
     // The MFMAs of one k16 sub-step, with `between(q)` after MFMA q; the
@@ -220,7 +320,6 @@ gemm_nt_pipe(Operands op, TileArgs ta) {
     // Prologue: stream steps 0 .. S-2 and the first half of step S-1.
     Issue cur;
     cur.tile = 0;
-    cur.k0 = 0;
     cur.st = 0;
     rsrc_of(cur);
 #pragma unroll
@@ -241,9 +340,8 @@ gemm_nt_pipe(Operands op, TileArgs ta) {
     // `cur` is the step whose second half goes out in the next sub-step 0.
     for (int i = 0; i < n_tiles; ++i) {
         const Tile t = tile(i);
-        // Bias of this lane's columns, for the epilogue (48 or 64 VGPRs). Buffer
-        // loads with the resource ending at n: columns past it read 0, and
-        // every wave issues exactly FN * 4 of them (the waits below count them).
+        // Bias of this lane's columns, for the epilogue: buffer loads with the
+        // resource ending at n (columns past it read 0), FN * 4 of them per wave.
         f32x4 bias[kBias ? FN : 1][4];
         if constexpr (kBias) {
             const auto rbias = __builtin_amdgcn_make_buffer_rsrc(
@@ -257,9 +355,11 @@ gemm_nt_pipe(Operands op, TileArgs ta) {
                         f32x4, __builtin_amdgcn_raw_buffer_load_b128(rbias, unsigned(c) * 4u, 0, 0));
                 }
         }
+        const int steps = (t.k_end - t.k_begin) / BK;
         for (int s = 0; s < steps; ++s) {
             Issue nxt = cur;
             advance(nxt);
+            wait_frags();
             // Sub-step 0: reads of sub-step 1, second half of step `cur`.
             mfmas(xf[0], wf[0], [&](int q) {
                 if (q < FM + FN) read_one(st, 1, q, xf[1], wf[1]);
@@ -288,86 +388,130 @@ gemm_nt_pipe(Operands op, TileArgs ta) {
             cur = nxt;
         }
 
-        // ---- epilogue: per 32-row block, registers -> this wave's staging
-        // block -> whole 16-byte row chunks to HBM. Buffer stores: a chunk
-        // outside the output gets an offset past the resource's end and is
-        // dropped, so every wave issues exactly kStores of them. They drain
-        // while the next tile's k-loop runs on its prefetched steps.
+        // ---- epilogue: per staged block of a wave, registers -> staging ->
+        // whole 16-byte row chunks to HBM.
         const int row_base = t.m0 + wm * WTM;
         const int col_base = t.n0 + wn * WTN;
-        const unsigned out_bytes = unsigned(m) * unsigned(n) * unsigned(C::kElem);
-        // Byte offset of chunk q of this lane in 32-row block j (past the end
-        // of the output when the chunk is outside it; n % 8 == 0 on this path,
-        // so a chunk is whole once it starts).
-        auto chunk_off = [&](int j, int q, int* r, int* cc) {
+        const unsigned out_bytes = unsigned(size_t(m) * n * E::kOutElem);
+        // Byte offset (elements of `elem` bytes) of chunk q of this lane in the
+        // staged block (j, h), or past the end when the chunk is outside the
+        // output (n % 8 == 0 here, so a chunk is whole once it starts).
+        auto chunk_at = [&](int j, int h, int q, int elem, int* r, int* cc) {
             const int c = q * 64 + lane;
-            *r = c / C::kCpr;
-            *cc = c % C::kCpr;
-            const int gr = row_base + j * 32 + *r, gc = col_base + *cc * C::kPerChunk;
-            return gr < m && gc < n ? (unsigned(gr) * unsigned(n) + unsigned(gc)) * unsigned(C::kElem)
+            *r = c / E::kCpr;
+            *cc = c % E::kCpr;
+            const int gr = row_base + j * 32 + h * E::kRows + *r;
+            const int gc = col_base + *cc * E::kPerChunk;
+            return gr < m && gc < n ? (unsigned(gr) * unsigned(n) + unsigned(gc)) * unsigned(elem)
                                     : 0xfffffff0u;
         };
+        const bool accumulate = ST == Store::kTn && !split && op.accumulate;
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
-            // Residual: this block's chunks are loaded first, so their latency
-            // overlaps the staging writes.
-            f32x4 res[kF32 ? C::kPerLane : 1];
-            if constexpr (kF32) {
-                const auto rres = __builtin_amdgcn_make_buffer_rsrc(
-                    const_cast<float*>(static_cast<const float*>(op.aux) + t.y_batch), 0,
-                    out_bytes, 0x00020000);
 #pragma unroll
-                for (int q = 0; q < C::kPerLane; ++q) {
-                    int r, cc;
-                    res[q] = __builtin_bit_cast(
-                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(rres, chunk_off(j, q, &r, &cc), 0, 0));
-                }
-            }
+            for (int h = 0; h < E::kSubs; ++h) {
+                // Values the store pass reads back, loaded first so that their
+                // latency overlaps the staging writes: the residual, the old y
+                // of an accumulating TN, dGELU's pre.
+                constexpr bool kReads = ST == Store::kBiasResidual || ST == Store::kDGelu ||
+                                        ST == Store::kTn;
+                f32x4 rd[kReads ? E::kPerLane : 1];
+                if constexpr (ST == Store::kBiasResidual || ST == Store::kTn) {
+                    const float* src = ST == Store::kTn ? static_cast<const float*>(op.y)
+                                                        : static_cast<const float*>(op.aux);
+                    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+                        const_cast<float*>(src + t.y_off), 0, out_bytes, 0x00020000);
 #pragma unroll
-            for (int pass = 0; pass < kPasses; ++pass) {
-                // GELU: pass 0 writes pre = RN16(s), pass 1 y = RN16(gelu(s)).
-                const bool gelu_pass = ST == Store::kBiasGelu && pass == 1;
-#pragma unroll
-                for (int ii = 0; ii < FN; ++ii) {
-#pragma unroll
-                    for (int g4 = 0; g4 < 4; ++g4) {
-                        f32x4 v = {acc[ii][j][g4 * 4 + 0], acc[ii][j][g4 * 4 + 1],
-                                   acc[ii][j][g4 * 4 + 2], acc[ii][j][g4 * 4 + 3]};
-                        if constexpr (kBias) v += bias[ii][g4];
-                        if constexpr (ST == Store::kScale) v *= op.scale;
-                        const int at = fr * C::kLdw + ii * 32 + g4 * 8 + fc * 4;
-                        if constexpr (kF32) {
-                            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(cst) + at) = v;
+                    for (int q = 0; q < E::kPerLane; ++q) {
+                        int r, cc;
+                        if (ST == Store::kTn && !accumulate) {
+                            rd[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                         } else {
-                            if (gelu_pass) {
-#pragma unroll
-                                for (int e = 0; e < 4; ++e) v[e] = gelu(v[e]);
-                            }
-                            const f16x4 h = {_Float16(v[0]), _Float16(v[1]), _Float16(v[2]),
-                                             _Float16(v[3])};
-                            *reinterpret_cast<f16x4*>(cst + at) = h;
+                            rd[q] = __builtin_bit_cast(
+                                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rs, chunk_at(j, h, q, 4, &r, &cc), 0, 0));
                         }
                     }
                 }
-                void* out = ST == Store::kBiasGelu && pass == 0 ? op.aux : op.y;
-                out = static_cast<char*>(out) + t.y_batch * C::kElem;
-                const auto rout = __builtin_amdgcn_make_buffer_rsrc(out, 0, out_bytes, 0x00020000);
+                if constexpr (ST == Store::kDGelu) {
+                    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+                        const_cast<void*>(static_cast<const void*>(
+                            static_cast<const _Float16*>(op.aux) + t.y_off)),
+                        0, out_bytes, 0x00020000);
 #pragma unroll
-                for (int q = 0; q < C::kPerLane; ++q) {
-                    int r, cc;
-                    const unsigned off = chunk_off(j, q, &r, &cc);
-                    i32x4 v;
-                    if constexpr (kF32) {
-                        // y = residual + (sum + bias): one FP32 add, as the
-                        // unstaged epilogue does it.
-                        const f32x4 sb = *reinterpret_cast<const f32x4*>(
-                            reinterpret_cast<const float*>(cst) + r * C::kLdw + cc * 4);
-                        v = __builtin_bit_cast(i32x4, res[q] + sb);
-                    } else {
-                        v = __builtin_bit_cast(
-                            i32x4, *reinterpret_cast<const f16x8*>(cst + r * C::kLdw + cc * 8));
+                    for (int q = 0; q < E::kPerLane; ++q) {
+                        int r, cc;
+                        const i32x2 p = __builtin_amdgcn_raw_buffer_load_b64(
+                            rs, chunk_at(j, h, q, 2, &r, &cc), 0, 0);
+                        const f16x4 ph = __builtin_bit_cast(f16x4, p);
+                        rd[q] = f32x4{float(ph[0]), float(ph[1]), float(ph[2]), float(ph[3])};
                     }
-                    __builtin_amdgcn_raw_buffer_store_b128(v, rout, off, 0, 0);
+                }
+#pragma unroll
+                for (int pass = 0; pass < E::kPasses; ++pass) {
+                    // GELU: pass 0 writes pre = RN16(s), pass 1 y = RN16(gelu(s)).
+                    const bool gelu_pass = ST == Store::kBiasGelu && pass == 1;
+                    const bool mine = !E::kF32 || (fr >> 4) == h;   // FP32: 16 of the 32 rows
+                    if (mine) {
+                        const int srow = E::kF32 ? (fr & 15) : fr;
+#pragma unroll
+                        for (int ii = 0; ii < FN; ++ii) {
+#pragma unroll
+                            for (int g4 = 0; g4 < 4; ++g4) {
+                                f32x4 v = {acc[ii][j][g4 * 4 + 0], acc[ii][j][g4 * 4 + 1],
+                                           acc[ii][j][g4 * 4 + 2], acc[ii][j][g4 * 4 + 3]};
+                                if constexpr (kBias) v += bias[ii][g4];
+                                if constexpr (ST == Store::kScale) v *= op.scale;
+                                const int at = srow * E::kLdw + ii * 32 + g4 * 8 + fc * 4;
+                                if constexpr (E::kF32) {
+                                    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(cst) + at) = v;
+                                } else {
+                                    if (gelu_pass) {
+#pragma unroll
+                                        for (int e = 0; e < 4; ++e) v[e] = gelu(v[e]);
+                                    }
+                                    const f16x4 hv = {_Float16(v[0]), _Float16(v[1]),
+                                                      _Float16(v[2]), _Float16(v[3])};
+                                    *reinterpret_cast<f16x4*>(cst + at) = hv;
+                                }
+                            }
+                        }
+                    }
+                    void* out = ST == Store::kBiasGelu && pass == 0 ? op.aux : op.y;
+                    if (split) out = op.partials;
+                    out = static_cast<char*>(out) + t.y_off * E::kOutElem;
+                    const auto rout = __builtin_amdgcn_make_buffer_rsrc(out, 0, out_bytes,
+                                                                        0x00020000);
+#pragma unroll
+                    for (int q = 0; q < E::kPerLane; ++q) {
+                        int r, cc;
+                        if constexpr (ST == Store::kDGelu) {
+                            // y = RN16(sum * GELU'(pre)), 4 outputs = 8 bytes.
+                            const unsigned off = chunk_at(j, h, q, 2, &r, &cc);
+                            const f32x4 sv = *reinterpret_cast<const f32x4*>(
+                                reinterpret_cast<const float*>(cst) + r * E::kLdw + cc * 4);
+                            f16x4 o;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) o[e] = _Float16(sv[e] * gelu_grad(rd[q][e]));
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, o), rout,
+                                                                  off, 0, 0);
+                        } else if constexpr (E::kF32) {
+                            // Residual: y = residual + (sum + bias). TN: y = sum,
+                            // y = old + sum, or a split's partial.
+                            const unsigned off = chunk_at(j, h, q, 4, &r, &cc);
+                            const f32x4 sv = *reinterpret_cast<const f32x4*>(
+                                reinterpret_cast<const float*>(cst) + r * E::kLdw + cc * 4);
+                            f32x4 o = sv;
+                            if (ST == Store::kBiasResidual || accumulate) o = rd[q] + sv;
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, o), rout,
+                                                                   off, 0, 0);
+                        } else {
+                            const unsigned off = chunk_at(j, h, q, 2, &r, &cc);
+                            const f16x8 v = *reinterpret_cast<const f16x8*>(cst + r * E::kLdw + cc * 8);
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), rout,
+                                                                   off, 0, 0);
+                        }
+                    }
                 }
             }
         }
@@ -388,8 +532,8 @@ struct PipeConfig {
 
 constexpr PipeConfig kPipeConfigs[] = {{256, 256, 3}, {256, 192, 4}, {128, 192, 4}};
 
-// FLINT_GEMM_PIPE: "0" routes every NT call to gemm.hip's kernels;
-// "bm,bn,stages" forces one of kPipeConfigs (tuning sweeps; read per call).
+// FLINT_GEMM_PIPE: "0" routes every call to gemm.hip's kernels; "bm,bn,stages"
+// forces one of kPipeConfigs (tuning sweeps and tests; read per call).
 bool pipe_forced(PipeConfig* out, bool* disabled) {
     *disabled = false;
     const char* e = std::getenv("FLINT_GEMM_PIPE");
@@ -409,21 +553,23 @@ bool pipe_forced(PipeConfig* out, bool* disabled) {
     return false;
 }
 
-// The macro-tile: whole waves of tiles over the CUs weigh most (a K = 768
-// tile is short, so a partial last wave costs nearly a full one); among
-// equal wave counts the larger tile needs fewer bytes per FLOP.
-// LDS bytes of a configuration: its stages plus four per-wave staging blocks.
-constexpr size_t pipe_lds_bytes(int bm, int bn, int stages, bool f32) {
-    const int wtn = bn / 2, per_chunk = f32 ? 4 : 8;
-    return size_t(stages) * (bm + bn) * kPipeBK * 2 + 4 * 32 * size_t(wtn + per_chunk) * (f32 ? 4 : 2);
+// LDS bytes of a configuration at run time (the kernel's own static_assert
+// checks the same sum).
+size_t lds_bytes(const PipeConfig& c, Store st) {
+    const bool f32 = st == Store::kBiasResidual || st == Store::kTn || st == Store::kDGelu;
+    const int wtn = c.bn / 2, per = f32 ? 4 : 8, rows = f32 ? 16 : 32;
+    return size_t(c.stages) * (c.bm + c.bn) * kPipeBK * 2 +
+           4 * size_t(rows) * (wtn + per) * (f32 ? 4 : 2);
 }
-constexpr size_t kPipeMaxLds = 160 * 1024;
 
-PipeConfig pick_pipe(size_t m, size_t n, size_t slices, int cus, bool f32) {
+// The macro-tile: whole waves of tiles over the CUs weigh most (a K = 768
+// tile is short, so a partial last wave costs nearly a full one); among equal
+// wave counts the larger tile needs fewer bytes per FLOP.
+PipeConfig pick_pipe(size_t m, size_t n, size_t slices, int cus, Store st) {
     PipeConfig best = kPipeConfigs[0];
     double best_cost = 1e300;
     for (const PipeConfig& c : kPipeConfigs) {
-        if (pipe_lds_bytes(c.bm, c.bn, c.stages, f32) > kPipeMaxLds) continue;
+        if (lds_bytes(c, st) > kPipeMaxLds) continue;
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn) *
                              double(slices);
         const double rounds = std::ceil(tiles / cus);
@@ -439,16 +585,16 @@ PipeConfig pick_pipe(size_t m, size_t n, size_t slices, int cus, bool f32) {
     return best;
 }
 
-template <Store ST>
-hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, int cus,
-                       hipStream_t stream) {
+template <Layout L, Store ST>
+hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, int split_len,
+                       int cus, hipStream_t stream) {
     TileArgs ta{};
     ta.tiles_m = (op.m + c.bm - 1) / c.bm;
     ta.tiles_n = (op.n + c.bn - 1) / c.bn;
     ta.tiles_per_slice = ta.tiles_m * ta.tiles_n;
     ta.slices = int(slices);
     ta.group_m = 8;
-    ta.split_len = 0;
+    ta.split_len = split_len;
     const size_t total = size_t(ta.tiles_per_slice) * slices;
     if (total == 0 || total > 0x7fffffffu) return hipErrorInvalidValue;
     // Persistent: one workgroup per CU (a multiple of 8, so each keeps its
@@ -456,14 +602,13 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     size_t gx = std::min(total, size_t(cus));
     if (gx >= 8) gx -= gx % 8;
     const dim3 grid(unsigned(gx), 1, 1);
-    constexpr bool kF32 = ST == Store::kBiasResidual;
-#define FLINT_PIPE_CASE(BM_, BN_, S_)                                                         \
-    if constexpr (pipe_lds_bytes(BM_, BN_, S_, kF32) <= kPipeMaxLds) {                        \
-        if (c.bm == BM_ && c.bn == BN_ && c.stages == S_) {                                   \
-            hipLaunchKernelGGL((gemm_nt_pipe<BM_, BN_, S_, ST>), grid, dim3(256), 0, stream, op, \
-                               ta);                                                           \
-            return hipGetLastError();                                                         \
-        }                                                                                     \
+#define FLINT_PIPE_CASE(BM_, BN_, S_)                                                          \
+    if constexpr (pipe_lds_bytes<BM_, BN_, S_, L, ST>() <= kPipeMaxLds) {                      \
+        if (c.bm == BM_ && c.bn == BN_ && c.stages == S_) {                                    \
+            hipLaunchKernelGGL((gemm_pipe<BM_, BN_, S_, L, ST>), grid, dim3(256), 0, stream, op, \
+                               ta);                                                            \
+            return hipGetLastError();                                                          \
+        }                                                                                      \
     }
     FLINT_PIPE_CASE(256, 256, 3)
     FLINT_PIPE_CASE(256, 192, 4)
@@ -472,29 +617,94 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     return hipErrorInvalidValue;
 }
 
+Store store_of(Epilogue e, Layout l) {
+    if (e == kTnFloat) return Store::kTn;
+    switch (e) {
+    case Epilogue::kNone: return l == Layout::kTN ? Store::kTnHalf : Store::kNone;
+    case Epilogue::kBias: return Store::kBias;
+    case Epilogue::kBiasGelu: return Store::kBiasGelu;
+    case Epilogue::kBiasResidual: return Store::kBiasResidual;
+    case Epilogue::kDGelu: return Store::kDGelu;
+    case Epilogue::kScale: return Store::kScale;
+    }
+    return Store::kNone;
+}
+
+Layout layout_of(GemmLayout l) {
+    return l == GemmLayout::kNT ? Layout::kNT : (l == GemmLayout::kNN ? Layout::kNN : Layout::kTN);
+}
+
+template <Layout L>
+hipError_t dispatch_pipe(const PipeConfig& c, Store st, const Operands& op, size_t slices,
+                         int split_len, int cus, hipStream_t stream) {
+    if constexpr (L == Layout::kNT) {
+        switch (st) {
+        case Store::kNone: return launch_pipe<L, Store::kNone>(c, op, slices, split_len, cus, stream);
+        case Store::kBias: return launch_pipe<L, Store::kBias>(c, op, slices, split_len, cus, stream);
+        case Store::kBiasGelu:
+            return launch_pipe<L, Store::kBiasGelu>(c, op, slices, split_len, cus, stream);
+        case Store::kBiasResidual:
+            return launch_pipe<L, Store::kBiasResidual>(c, op, slices, split_len, cus, stream);
+        case Store::kScale:
+            return launch_pipe<L, Store::kScale>(c, op, slices, split_len, cus, stream);
+        default: break;
+        }
+    } else if constexpr (L == Layout::kNN) {
+        switch (st) {
+        case Store::kNone: return launch_pipe<L, Store::kNone>(c, op, slices, split_len, cus, stream);
+        case Store::kDGelu:
+            return launch_pipe<L, Store::kDGelu>(c, op, slices, split_len, cus, stream);
+        default: break;
+        }
+    } else {
+        switch (st) {
+        case Store::kTn: return launch_pipe<L, Store::kTn>(c, op, slices, split_len, cus, stream);
+        case Store::kTnHalf:
+            return launch_pipe<L, Store::kTnHalf>(c, op, slices, split_len, cus, stream);
+        default: break;
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
 }  // namespace
 
-bool gemm_nt_pipe_eligible(Epilogue e, size_t m, size_t n, size_t k) {
+bool gemm_pipe_eligible(GemmLayout gl, Epilogue e, size_t m, size_t n, size_t k) {
     bool disabled = false;
     PipeConfig forced;
     const bool force = pipe_forced(&forced, &disabled);
     if (disabled || m == 0 || n == 0 || n % 8 != 0 || k % kPipeBK != 0 || k < kPipeBK) return false;
-    // The epilogue's buffer stores address one slice's output with 32-bit
-    // offsets (FP32 for the residual epilogue).
-    if (m * n * (e == Epilogue::kBiasResidual ? 4 : 2) >= (size_t{1} << 31)) return false;
-    if (e != Epilogue::kNone && e != Epilogue::kBias && e != Epilogue::kBiasGelu &&
-        e != Epilogue::kScale && e != Epilogue::kBiasResidual) {
+    const Layout l = layout_of(gl);
+    const Store st = store_of(e, l);
+    // Only the epilogues each layout serves.
+    const bool served = l == Layout::kNT ? (st == Store::kNone || st == Store::kBias ||
+                                            st == Store::kBiasGelu || st == Store::kBiasResidual ||
+                                            st == Store::kScale)
+                        : l == Layout::kNN ? (st == Store::kNone || st == Store::kDGelu)
+                                           : (st == Store::kTn || st == Store::kTnHalf);
+    if (!served) return false;
+    // k-major operands come in 16-byte chunks of their columns.
+    if (l == Layout::kTN && m % 8 != 0) return false;
+    // Buffer offsets are 32-bit: one slice's output and each operand.
+    const size_t out_elem = st == Store::kBiasResidual || st == Store::kTn ? 4 : 2;
+    if (m * n * out_elem >= (size_t{1} << 31) || m * k * 2 >= (size_t{1} << 31) ||
+        n * k * 2 >= (size_t{1} << 31)) {
         return false;
     }
+    if (force) return true;
+    // Outputs narrower than a tile (the attention GEMMs' 64 columns) would
+    // leave most of each tile idle; gemm.hip's 64-wide tiles serve them.
+    if (n < 128) return false;
     // The residual outputs of GPT-2 are 768 wide: 128-row tiles are needed to
     // fill the CUs there, and gemm.hip's 128 x 192 x 64 kernel with the
     // residual prefetched into registers measured as fast as this one's.
-    return force || e != Epilogue::kBiasResidual || n >= 1024;
+    return st != Store::kBiasResidual || n >= 1024;
 }
 
-hipError_t launch_gemm_nt_pipe(void* y, const void* x, const void* w, const void* bias, void* aux,
-                               Epilogue e, float scale, size_t slices, size_t m, size_t n,
-                               size_t k, hipStream_t stream) {
+hipError_t launch_gemm_pipe(GemmLayout gl, Epilogue e, void* y, const void* x, const void* w,
+                            const void* bias, void* aux, float scale, size_t slices, size_t m,
+                            size_t n, size_t k, bool accumulate, void* partials, int split_len,
+                            hipStream_t stream) {
     int cus = 256;
     if (hipError_t err = device_cus(&cus); err != hipSuccess) return err;
     Operands op{};
@@ -503,24 +713,24 @@ hipError_t launch_gemm_nt_pipe(void* y, const void* x, const void* w, const void
     op.w = static_cast<const _Float16*>(w);
     op.bias = static_cast<const float*>(bias);
     op.aux = aux;
+    op.partials = static_cast<float*>(partials);
     op.scale = scale;
+    op.accumulate = accumulate ? 1 : 0;
     op.m = int(m);
     op.n = int(n);
     op.k = int(k);
+    const Layout l = layout_of(gl);
+    const Store st = store_of(e, l);
     PipeConfig c;
     bool disabled = false;
-    const bool f32 = e == Epilogue::kBiasResidual;
-    if (!pipe_forced(&c, &disabled) || pipe_lds_bytes(c.bm, c.bn, c.stages, f32) > kPipeMaxLds)
-        c = pick_pipe(m, n, slices, cus, f32);
-    switch (e) {
-    case Epilogue::kNone: return launch_pipe<Store::kNone>(c, op, slices, cus, stream);
-    case Epilogue::kBias: return launch_pipe<Store::kBias>(c, op, slices, cus, stream);
-    case Epilogue::kBiasGelu: return launch_pipe<Store::kBiasGelu>(c, op, slices, cus, stream);
-    case Epilogue::kScale: return launch_pipe<Store::kScale>(c, op, slices, cus, stream);
-    case Epilogue::kBiasResidual:
-        return launch_pipe<Store::kBiasResidual>(c, op, slices, cus, stream);
-    default: return hipErrorInvalidValue;
+    if (!pipe_forced(&c, &disabled) || lds_bytes(c, st) > kPipeMaxLds)
+        c = pick_pipe(m, n, slices, cus, st);
+    switch (l) {
+    case Layout::kNT: return dispatch_pipe<Layout::kNT>(c, st, op, slices, split_len, cus, stream);
+    case Layout::kNN: return dispatch_pipe<Layout::kNN>(c, st, op, slices, split_len, cus, stream);
+    case Layout::kTN: return dispatch_pipe<Layout::kTN>(c, st, op, slices, split_len, cus, stream);
     }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace flint

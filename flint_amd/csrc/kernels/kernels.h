@@ -21,13 +21,18 @@ enum class Epilogue { kNone, kBias, kBiasGelu, kBiasResidual, kDGelu, kScale };
 hipError_t launch_gemm_nt(void* y, const void* x, const void* w, const void* bias,
                           void* aux, Epilogue e, size_t m, size_t n, size_t k,
                           hipStream_t stream);
-// The one-wave-per-SIMD NT pipeline (gemm_pipe.hip) for n % 8 == 0 and
-// k % 32 == 0; launch_gemm_nt and launch_gemm_nt_batched route there when
-// eligible (FLINT_GEMM_PIPE=0 turns it off).
-bool gemm_nt_pipe_eligible(Epilogue e, size_t m, size_t n, size_t k);
-hipError_t launch_gemm_nt_pipe(void* y, const void* x, const void* w, const void* bias, void* aux,
-                               Epilogue e, float scale, size_t slices, size_t m, size_t n,
-                               size_t k, hipStream_t stream);
+// The one-wave-per-SIMD GEMM pipeline (gemm_pipe.hip), for k % 32 == 0 and
+// n % 8 == 0 (and m % 8 == 0 for TN). The launchers below route there when
+// gemm_pipe_eligible says so (FLINT_GEMM_PIPE=0 turns it off).
+enum class GemmLayout { kNT, kNN, kTN };
+// kTnFloat: TN's FP32 output (y = sum, y += sum, or a split's partial);
+// kNone with TN is the batched FP16 output.
+constexpr Epilogue kTnFloat = Epilogue(100);
+bool gemm_pipe_eligible(GemmLayout l, Epilogue e, size_t m, size_t n, size_t k);
+hipError_t launch_gemm_pipe(GemmLayout l, Epilogue e, void* y, const void* x, const void* w,
+                            const void* bias, void* aux, float scale, size_t slices, size_t m,
+                            size_t n, size_t k, bool accumulate, void* partials, int split_len,
+                            hipStream_t stream);
 hipError_t launch_gemm_nn(void* y, const void* x, const void* w, const void* aux, Epilogue e,
                           size_t m, size_t n, size_t k, hipStream_t stream);
 // Number of k splits TN uses for m x n x k on this device (1 = none).

@@ -317,3 +317,63 @@ def test_nt_batched_pipe_forced(flint, cuda, monkeypatch, cfg):
     torch.cuda.synchronize()
     ref = torch.bmm(x.float(), w.float().transpose(1, 2).contiguous()) * 0.125
     assert rel_err(y.cpu(), ref) <= TOL
+
+
+# The pipeline's k-major operand paths (NN's w, TN's x and w through the
+# transposing LDS reads), forced per configuration: edge tiles, a k-range
+# shorter than the stages, splits of TN (whose workspace plan is the ABI's).
+@pytest.mark.parametrize("cfg", PIPE_CONFIGS)
+@pytest.mark.parametrize("m,n,k", [(300, 200, 64), (1100, 1096, 320)])
+def test_nn_pipe_forced(flint, cuda, monkeypatch, cfg, m, n, k):
+    monkeypatch.setenv("FLINT_GEMM_PIPE", cfg)
+    x = uniform((m, k), 46)
+    w = normal((k, n), 47, 0.05, torch.float16)
+    y = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
+    flint.gemm_nn(y, x.to(cuda), w.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu(), ref_nn(x, w)) <= TOL
+    pre = normal((m, n), 48, 1.0, torch.float16)
+    flint.gemm_nn_dgelu(y, x.to(cuda), w.to(cuda), pre.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    from oracle.oracle import gelu_grad64
+
+    dg = torch.from_numpy(gelu_grad64(pre.float().numpy()))
+    assert rel_err(y.cpu(), ref_nn(x, w).double() * dg) <= TOL
+
+
+@pytest.mark.parametrize("cfg", PIPE_CONFIGS)
+@pytest.mark.parametrize("m,n,k", [(296, 200, 2048), (1032, 264, 4096), (768, 768, 8192)])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_tn_pipe_forced(flint, cuda, monkeypatch, cfg, m, n, k, accumulate):
+    monkeypatch.setenv("FLINT_GEMM_PIPE", cfg)
+    x = normal((k, m), 49, 1e-2, torch.float16)
+    w = uniform((k, n), 50)
+    y0 = normal((m, n), 51)
+    y = y0.clone().to(cuda)
+    flint.gemm_tn(y, x.to(cuda), w.to(cuda), m, n, k, accumulate=accumulate)
+    torch.cuda.synchronize()
+    ref = ref_tn(x, w) + (y0 if accumulate else 0)
+    assert rel_err(y.cpu(), ref) <= TOL
+    if accumulate:
+        plain = torch.empty((m, n), device=cuda)
+        flint.gemm_tn(plain, x.to(cuda), w.to(cuda), m, n, k, accumulate=False)
+        torch.cuda.synchronize()
+        assert torch.equal(y.cpu(), y0 + plain.cpu())
+
+
+@pytest.mark.parametrize("cfg", PIPE_CONFIGS)
+def test_batched_nn_tn_pipe_forced(flint, cuda, monkeypatch, cfg):
+    monkeypatch.setenv("FLINT_GEMM_PIPE", cfg)
+    batches, m, n, k = 5, 264, 72, 96
+    x = uniform((batches, m, k), 52)
+    w = uniform((batches, k, n), 53)
+    y = torch.full((batches, m, n), float("nan"), dtype=torch.float16, device=cuda)
+    flint.gemm_nn_batched(y, x.to(cuda), w.to(cuda), batches, m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu(), torch.bmm(x.float(), w.float())) <= TOL
+    xt = uniform((batches, k, m), 54)
+    y2 = torch.full((batches, m, n), float("nan"), dtype=torch.float16, device=cuda)
+    flint.gemm_tn_batched(y2, xt.to(cuda), w.to(cuda), batches, m, n, k)
+    torch.cuda.synchronize()
+    ref = torch.bmm(xt.float().transpose(1, 2).contiguous(), w.float())
+    assert rel_err(y2.cpu(), ref) <= TOL
