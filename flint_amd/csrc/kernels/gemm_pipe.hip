@@ -14,7 +14,7 @@
 //  * The k-loop takes k-steps of 32 through S LDS stages. The loads of step
 //    g + S - 1 are issued half during the first and half during the second k16
 //    sub-step of the steps before it, one buffer_load ... lds after every
-//    second MFMA, and the fragment reads of the next sub-step one after every
+//    second MFMA (every MFMA for 64-wide tiles), and the fragment reads of the next sub-step one after every
 //    MFMA: no burst of loads stalls the wave, and S - 1 steps of latency are
 //    covered. One barrier per step sits between the two sub-steps, after the
 //    last fragment read of the step.
@@ -75,15 +75,18 @@ __device__ __forceinline__ int row_key(int row) { return ((row >> 1) ^ (row >> 2
 // aligned group of 8 (the XOR stays inside the group, hence inside the row).
 __host__ __device__ constexpr int kmajor_key(int k) { return 2 * (k & 3); }
 
-// What the epilogue stages per wave and writes per 16-byte chunk.
-template <int BN, Store ST>
+// Waves of a workgroup along n: 2 x 2 waves, or 4 x 1 for 64-wide tiles.
+__host__ __device__ constexpr int pipe_waves_n(int bn) { return bn >= 128 ? 2 : 1; }
+
+// What the epilogue stages per wave (WTN columns) and writes per 16-byte chunk.
+template <int WTN, Store ST>
 struct PipeEpi {
     // FP32 values are staged when the output is FP32 (residual, TN) or when
     // the rounding needs a value that only the store pass reads (dGELU's pre).
     static constexpr bool kF32 =
         ST == Store::kBiasResidual || ST == Store::kTn || ST == Store::kDGelu;
     static constexpr int kOutElem = ST == Store::kBiasResidual || ST == Store::kTn ? 4 : 2;
-    static constexpr int kWtn = BN / 2;
+    static constexpr int kWtn = WTN;
     static constexpr int kPerChunk = kF32 ? 4 : 8;            // values per staged chunk
     static constexpr int kRows = kF32 ? 16 : 32;              // rows staged at a time
     static constexpr int kLdw = kWtn + kPerChunk;             // staged row stride (values)
@@ -97,7 +100,7 @@ struct PipeEpi {
 
 template <int BM, int BN, int S, Layout L, Store ST>
 constexpr size_t pipe_lds_bytes() {
-    using E = PipeEpi<BN, ST>;
+    using E = PipeEpi<BN / pipe_waves_n(BN), ST>;
     return size_t(S) * (BM + BN) * kPipeBK * 2 + 4 * size_t(E::kHalves) * 2;
 }
 constexpr size_t kPipeMaxLds = 160 * 1024;
@@ -109,18 +112,24 @@ gemm_pipe(Operands op, TileArgs ta) {
     // resource builtins below exist on the device side only.
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int BK = kPipeBK;
-    constexpr int WTM = BM / 2, WTN = BN / 2;   // 2 x 2 waves
+    constexpr int WAVES_N = pipe_waves_n(BN);
+    constexpr int WTM = BM / (4 / WAVES_N), WTN = BN / WAVES_N;
     constexpr int FM = WTM / 32, FN = WTN / 32;
     constexpr int IA = BM / 64, IB = BN / 64;   // 1 KB loads per thread per step
     constexpr int PER = IA + IB;
     constexpr int HALF = PER / 2;
+    // A sub-step's loads go out after every second MFMA, or after every one
+    // when the sub-step has too few MFMAs for that (64-wide tiles); every load
+    // must get a slot, or the waits below would count loads never issued.
+    constexpr int kLoadEvery = FM * FN >= 2 * (PER - HALF) ? 2 : 1;
+    static_assert(FM * FN >= (PER - HALF) * kLoadEvery, "a slot for every load");
     // x side (rows m, the MFMA's B operand) and w side (rows n, its A operand)
     // are k-major ([32 k][rows] in LDS) or row-major ([rows][32 k]).
     constexpr bool kXM = L == Layout::kTN;
     constexpr bool kWM = L != Layout::kNT;
     constexpr bool kBias =
         ST == Store::kBias || ST == Store::kBiasGelu || ST == Store::kBiasResidual;
-    using E = PipeEpi<BN, ST>;
+    using E = PipeEpi<WTN, ST>;
     constexpr int kStageHalves = S * (BM + BN) * BK;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "whole 32 x 32 blocks per wave");
     static_assert(pipe_lds_bytes<BM, BN, S, L, ST>() <= kPipeMaxLds, "LDS");
@@ -136,7 +145,7 @@ gemm_pipe(Operands op, TileArgs ta) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int m = op.m, n = op.n, K = op.k;
     const bool split = ST == Store::kTn && op.partials != nullptr;
     _Float16* const cst = lds + kStageHalves + wave * E::kHalves;
@@ -363,7 +372,8 @@ gemm_pipe(Operands op, TileArgs ta) {
             // Sub-step 0: reads of sub-step 1, second half of step `cur`.
             mfmas(xf[0], wf[0], [&](int q) {
                 if (q < FM + FN) read_one(st, 1, q, xf[1], wf[1]);
-                if ((q & 1) && HALF + q / 2 < PER) issue_q(cur, HALF + q / 2);
+                if (q % kLoadEvery == kLoadEvery - 1 && HALF + q / kLoadEvery < PER)
+                    issue_q(cur, HALF + q / kLoadEvery);
             });
             // The next step has landed once only the loads of the S - 2 steps
             // after it remain outstanding. For the first S - 2 steps of a tile
@@ -382,7 +392,8 @@ gemm_pipe(Operands op, TileArgs ta) {
             // Sub-step 1: reads of the next step's sub-step 0, first half of `nxt`.
             mfmas(xf[1], wf[1], [&](int q) {
                 if (q < FM + FN) read_one(st_next, 0, q, xf[0], wf[0]);
-                if ((q & 1) && q / 2 < HALF) issue_q(nxt, q / 2);
+                if (q % kLoadEvery == kLoadEvery - 1 && q / kLoadEvery < HALF)
+                    issue_q(nxt, q / kLoadEvery);
             });
             st = st_next;
             cur = nxt;
@@ -530,7 +541,7 @@ struct PipeConfig {
     int bm, bn, stages;
 };
 
-constexpr PipeConfig kPipeConfigs[] = {{256, 256, 3}, {256, 192, 4}, {128, 192, 4}};
+constexpr PipeConfig kPipeConfigs[] = {{256, 256, 3}, {256, 192, 4}, {128, 192, 4}, {256, 64, 4}};
 
 // FLINT_GEMM_PIPE: "0" routes every call to gemm.hip's kernels; "bm,bn,stages"
 // forces one of kPipeConfigs (tuning sweeps and tests; read per call).
@@ -557,7 +568,7 @@ bool pipe_forced(PipeConfig* out, bool* disabled) {
 // checks the same sum).
 size_t lds_bytes(const PipeConfig& c, Store st) {
     const bool f32 = st == Store::kBiasResidual || st == Store::kTn || st == Store::kDGelu;
-    const int wtn = c.bn / 2, per = f32 ? 4 : 8, rows = f32 ? 16 : 32;
+    const int wtn = c.bn / pipe_waves_n(c.bn), per = f32 ? 4 : 8, rows = f32 ? 16 : 32;
     return size_t(c.stages) * (c.bm + c.bn) * kPipeBK * 2 +
            4 * size_t(rows) * (wtn + per) * (f32 ? 4 : 2);
 }
@@ -575,7 +586,8 @@ PipeConfig pick_pipe(size_t m, size_t n, size_t slices, int cus, Store st) {
         const double rounds = std::ceil(tiles / cus);
         // Relative time of one tile: its area over its measured throughput per
         // unit area (256 x 256 as 1; the smaller tiles move more bytes per FLOP).
-        const double eff = c.bm == 128 ? 0.80 : (c.bn == 256 ? 1.0 : 0.97);
+        // (256 x 64: 51 FLOP per loaded byte, worth it only where n <= 64.)
+        const double eff = c.bn == 64 ? 0.55 : c.bm == 128 ? 0.80 : (c.bn == 256 ? 1.0 : 0.97);
         const double cost = rounds * double(c.bm) * double(c.bn) / eff;
         if (cost < best_cost * 0.999) {
             best_cost = cost;
@@ -613,6 +625,7 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     FLINT_PIPE_CASE(256, 256, 3)
     FLINT_PIPE_CASE(256, 192, 4)
     FLINT_PIPE_CASE(128, 192, 4)
+    FLINT_PIPE_CASE(256, 64, 4)
 #undef FLINT_PIPE_CASE
     return hipErrorInvalidValue;
 }
@@ -692,9 +705,6 @@ bool gemm_pipe_eligible(GemmLayout gl, Epilogue e, size_t m, size_t n, size_t k)
         return false;
     }
     if (force) return true;
-    // Outputs narrower than a tile (the attention GEMMs' 64 columns) would
-    // leave most of each tile idle; gemm.hip's 64-wide tiles serve them.
-    if (n < 128) return false;
     // The residual outputs of GPT-2 are 768 wide: 128-row tiles are needed to
     // fill the CUs there, and gemm.hip's 128 x 192 x 64 kernel with the
     // residual prefetched into registers measured as fast as this one's.
