@@ -877,8 +877,10 @@ hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_
     op.partials = splits > 1 ? static_cast<float*>(workspace) : nullptr;
     hipError_t err;
     if (gemm_pipe_eligible(GemmLayout::kTN, kTnFloat, m, n, k)) {
-        err = launch_gemm_pipe(GemmLayout::kTN, kTnFloat, y, x, w, nullptr, nullptr, 1.0f,
-                               size_t(splits), m, n, k, accumulate, op.partials, len, stream);
+        // The pipeline picks its own split count, at most the plan's.
+        int used = 1;
+        err = launch_gemm_pipe_tn(y, x, w, m, n, k, accumulate, op.partials, splits, &used, stream);
+        splits = used;
     } else {
         err = run<Layout::kTN, Store::kTn>(op, size_t(splits), len, stream);
     }

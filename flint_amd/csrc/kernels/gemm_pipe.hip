@@ -597,6 +597,42 @@ PipeConfig pick_pipe(size_t m, size_t n, size_t slices, int cus, Store st) {
     return best;
 }
 
+// TN's tile and split count together. The ABI plan (gemm_tn_splits, which the
+// workspace size follows) caps the split count; any count up to it fits the
+// caller's workspace. Cost: rounds of (tile, split) units over the CUs times a
+// unit's work, plus the partials' reduce pass when there is more than one
+// split ((splits + 1 or 2) * m * n * 4 bytes at ~5 TB/s, and a launch).
+void plan_tn(size_t m, size_t n, size_t k, int max_splits, int cus, bool accumulate,
+             PipeConfig* best_c, int* best_s) {
+    const Store st = Store::kTn;
+    double best = 1e300;
+    *best_c = pick_pipe(m, n, 1, cus, st);
+    *best_s = 1;
+    for (const PipeConfig& c : kPipeConfigs) {
+        if (lds_bytes(c, st) > kPipeMaxLds) continue;
+        const double eff = c.bn == 64 ? 0.55 : c.bm == 128 ? 0.80 : (c.bn == 256 ? 1.0 : 0.97);
+        const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn);
+        for (int sp = 1; sp <= max_splits; ++sp) {
+            const size_t len = (k + sp - 1) / sp;
+            const size_t len32 = (len + kPipeBK - 1) / kPipeBK * kPipeBK;
+            if (size_t(sp - 1) * len32 >= k) continue;   // the last split would be empty
+            const double rounds = std::ceil(tiles * sp / cus);
+            // One 256 x 256 x 32 step of a unit is ~0.5 us at the pipeline's rate.
+            const double t_compute = rounds * double(c.bm) * double(c.bn) * double(len32) /
+                                     (256.0 * 256.0 * 32.0) * 0.5e-6 / eff;
+            const double t_reduce = sp > 1 ? double(sp + 1 + (accumulate ? 1 : 0)) * double(m) *
+                                                 double(n) * 4.0 / 5e12 + 3e-6
+                                           : 0.0;
+            const double t = t_compute + t_reduce;
+            if (t < best * 0.999) {
+                best = t;
+                *best_c = c;
+                *best_s = sp;
+            }
+        }
+    }
+}
+
 template <Layout L, Store ST>
 hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, int split_len,
                        int cus, hipStream_t stream) {
@@ -681,6 +717,33 @@ hipError_t dispatch_pipe(const PipeConfig& c, Store st, const Operands& op, size
 }
 
 }  // namespace
+
+hipError_t launch_gemm_pipe_tn(void* y, const void* x, const void* w, size_t m, size_t n,
+                               size_t k, bool accumulate, void* workspace, int max_splits,
+                               int* splits, hipStream_t stream) {
+    int cus = 256;
+    if (hipError_t err = device_cus(&cus); err != hipSuccess) return err;
+    PipeConfig c;
+    int sp = 1;
+    bool disabled = false;
+    plan_tn(m, n, k, workspace != nullptr ? max_splits : 1, cus, accumulate, &c, &sp);
+    PipeConfig forced;
+    if (pipe_forced(&forced, &disabled) && lds_bytes(forced, Store::kTn) <= kPipeMaxLds)
+        c = forced;
+    const size_t len = ((k + sp - 1) / sp + kPipeBK - 1) / kPipeBK * kPipeBK;
+    Operands op{};
+    op.y = y;
+    op.x = static_cast<const _Float16*>(x);
+    op.w = static_cast<const _Float16*>(w);
+    op.partials = sp > 1 ? static_cast<float*>(workspace) : nullptr;
+    op.accumulate = accumulate ? 1 : 0;
+    op.scale = 1.0f;
+    op.m = int(m);
+    op.n = int(n);
+    op.k = int(k);
+    *splits = sp;
+    return launch_pipe<Layout::kTN, Store::kTn>(c, op, size_t(sp), int(len), cus, stream);
+}
 
 bool gemm_pipe_eligible(GemmLayout gl, Epilogue e, size_t m, size_t n, size_t k) {
     bool disabled = false;

@@ -29,6 +29,12 @@ enum class GemmLayout { kNT, kNN, kTN };
 // kNone with TN is the batched FP16 output.
 constexpr Epilogue kTnFloat = Epilogue(100);
 bool gemm_pipe_eligible(GemmLayout l, Epilogue e, size_t m, size_t n, size_t k);
+// TN's FP32 output through the pipeline, choosing its own tile and split count
+// up to max_splits (the ABI plan the workspace was sized for); the count used
+// comes back in *splits (1: no partials, y written directly).
+hipError_t launch_gemm_pipe_tn(void* y, const void* x, const void* w, size_t m, size_t n,
+                               size_t k, bool accumulate, void* workspace, int max_splits,
+                               int* splits, hipStream_t stream);
 hipError_t launch_gemm_pipe(GemmLayout l, Epilogue e, void* y, const void* x, const void* w,
                             const void* bias, void* aux, float scale, size_t slices, size_t m,
                             size_t n, size_t k, bool accumulate, void* partials, int split_len,
