@@ -66,10 +66,18 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
-// Key of the [rows][32 k] layout (64-byte rows, 4 chunks): the 16 lanes a
-// ds_read_b128 serves per cycle (16 rows, one chunk) cover every chunk
-// position four times and no 16-byte bank group twice in a row of 4.
-__device__ __forceinline__ int row_key(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+// Key of the [rows][BK] layouts, XORed into a row's 16-byte chunk index. The
+// 16 lanes a ds_read_b128 serves per cycle read one chunk of 16 consecutive
+// rows, which must land on 16 distinct 16-byte bank groups (64 banks):
+//  * BK = 32 (64-byte rows, 4 chunks): rows r, r + 4, r + 8, r + 12 share
+//    bank groups before the XOR; ((row >> 1) ^ (row >> 2)) & 3 tells them apart.
+//  * BK = 64 (128-byte rows, 8 chunks): the 8 even (odd) rows share 8 bank
+//    groups; (row >> 1) & 7 gives each its own.
+template <int BK>
+__device__ __forceinline__ int row_key(int row) {
+    if constexpr (BK == 32) return ((row >> 1) ^ (row >> 2)) & 3;
+    else return (row >> 1) & 7;
+}
 // Key of the [32 k][rows] layout: rows k .. k + 3, which one transposing read
 // of 16 lanes touches (2 chunks each), land on 8 distinct chunk positions of an
 // aligned group of 8 (the XOR stays inside the group, hence inside the row).
@@ -79,7 +87,9 @@ __host__ __device__ constexpr int kmajor_key(int k) { return 2 * (k & 3); }
 __host__ __device__ constexpr int pipe_waves_n(int bn) { return bn >= 128 ? 2 : 1; }
 
 // What the epilogue stages per wave (WTN columns) and writes per 16-byte chunk.
-template <int WTN, Store ST>
+// COMPACT halves the rows staged at a time, for tiles whose stages leave too
+// little LDS for the full staging.
+template <int WTN, Store ST, bool COMPACT = false>
 struct PipeEpi {
     // FP32 values are staged when the output is FP32 (residual, TN) or when
     // the rounding needs a value that only the store pass reads (dGELU's pre).
@@ -88,7 +98,7 @@ struct PipeEpi {
     static constexpr int kOutElem = ST == Store::kBiasResidual || ST == Store::kTn ? 4 : 2;
     static constexpr int kWtn = WTN;
     static constexpr int kPerChunk = kF32 ? 4 : 8;            // values per staged chunk
-    static constexpr int kRows = kF32 ? 16 : 32;              // rows staged at a time
+    static constexpr int kRows = (kF32 ? 16 : 32) / (COMPACT ? 2 : 1);   // rows staged at a time
     static constexpr int kLdw = kWtn + kPerChunk;             // staged row stride (values)
     static constexpr int kHalves = kRows * kLdw * (kF32 ? 2 : 1);   // per wave, in halves
     static constexpr int kCpr = kWtn / kPerChunk;             // chunks per staged row
@@ -98,45 +108,61 @@ struct PipeEpi {
     static constexpr int kSubs = 32 / kRows;                  // staged blocks per 32 rows
 };
 
-template <int BM, int BN, int S, Layout L, Store ST>
-constexpr size_t pipe_lds_bytes() {
-    using E = PipeEpi<BN / pipe_waves_n(BN), ST>;
-    return size_t(S) * (BM + BN) * kPipeBK * 2 + 4 * size_t(E::kHalves) * 2;
-}
 constexpr size_t kPipeMaxLds = 160 * 1024;
+// Whether a configuration stages its epilogue compactly (see PipeEpi).
+template <int BM, int BN, int S, int BK, Store ST>
+constexpr bool pipe_compact() {
+    using E = PipeEpi<BN / pipe_waves_n(BN), ST>;
+    return size_t(S) * (BM + BN) * BK * 2 + 4 * size_t(E::kHalves) * 2 > kPipeMaxLds;
+}
+template <int BM, int BN, int S, int BK, Layout L, Store ST>
+constexpr size_t pipe_lds_bytes() {
+    using E = PipeEpi<BN / pipe_waves_n(BN), ST, pipe_compact<BM, BN, S, BK, ST>()>;
+    return size_t(S) * (BM + BN) * BK * 2 + 4 * size_t(E::kHalves) * 2;
+}
 
-template <int BM, int BN, int S, Layout L, Store ST>
+template <int BM, int BN, int S, int BK, Layout L, Store ST>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_pipe(Operands op, TileArgs ta) {
     // The host pass only needs a kernel to emit a launch stub for; the buffer
     // resource builtins below exist on the device side only.
 #if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int BK = kPipeBK;
+    static_assert(BK == 32 || BK == 64, "k-step");
+    constexpr int NS = BK / 16;                 // k16 sub-steps per k-step
     constexpr int WAVES_N = pipe_waves_n(BN);
     constexpr int WTM = BM / (4 / WAVES_N), WTN = BN / WAVES_N;
     constexpr int FM = WTM / 32, FN = WTN / 32;
-    constexpr int IA = BM / 64, IB = BN / 64;   // 1 KB loads per thread per step
+    constexpr int IA = BM * BK / 2048, IB = BN * BK / 2048;   // 1 KB loads per thread per step
     constexpr int PER = IA + IB;
-    constexpr int HALF = PER / 2;
+    // A step's loads: POST of them in the sub-step after the barrier, the rest
+    // PRE at a time in the NS - 1 sub-steps before the next one.
+    constexpr int POST = PER / NS;
+    constexpr int PRE = (PER - POST + NS - 2) / (NS - 1);
+    constexpr int kMaxLoads = POST > PRE ? POST : PRE;
     // A sub-step's loads go out after every second MFMA, or after every one
     // when the sub-step has too few MFMAs for that (64-wide tiles); every load
     // must get a slot, or the waits below would count loads never issued.
-    constexpr int kLoadEvery = FM * FN >= 2 * (PER - HALF) ? 2 : 1;
-    static_assert(FM * FN >= (PER - HALF) * kLoadEvery, "a slot for every load");
+    constexpr int kLoadEvery = FM * FN >= 2 * kMaxLoads ? 2 : 1;
+    static_assert(FM * FN >= kMaxLoads * kLoadEvery, "a slot for every load");
     // x side (rows m, the MFMA's B operand) and w side (rows n, its A operand)
     // are k-major ([32 k][rows] in LDS) or row-major ([rows][32 k]).
     constexpr bool kXM = L == Layout::kTN;
     constexpr bool kWM = L != Layout::kNT;
     constexpr bool kBias =
         ST == Store::kBias || ST == Store::kBiasGelu || ST == Store::kBiasResidual;
-    using E = PipeEpi<WTN, ST>;
+    using E = PipeEpi<WTN, ST, pipe_compact<BM, BN, S, BK, ST>()>;
     constexpr int kStageHalves = S * (BM + BN) * BK;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "whole 32 x 32 blocks per wave");
-    static_assert(pipe_lds_bytes<BM, BN, S, L, ST>() <= kPipeMaxLds, "LDS");
+    static_assert(pipe_lds_bytes<BM, BN, S, BK, L, ST>() <= kPipeMaxLds, "LDS");
     static_assert((S - 2) * PER + PER < 64, "vmcnt range");
     // Buffer stores per wave per tile, bias loads per wave per tile.
     constexpr int kStores = FM * E::kSubs * E::kPerLane * E::kPasses;
     constexpr int kBiasLoads = kBias ? FN * 4 : 0;
+    // The residual is loaded into registers at tile start where it fits in
+    // 128 VGPRs (128 x 192: 96), so that its latency hides under the k-loop.
+    constexpr int kResAll = FM * E::kSubs * E::kPerLane;
+    constexpr bool kResEarly = ST == Store::kBiasResidual && kResAll <= 32;
+    constexpr int kEarlyLoads = kBiasLoads + (kResEarly ? kResAll : 0);
     // One LDS object for everything: with a second one, the compiler's LDS-DMA
     // alias tracking put a vmcnt(0) in front of every fragment read.
     __shared__ __attribute__((aligned(16))) _Float16 lds[kStageHalves + 4 * E::kHalves];
@@ -215,8 +241,9 @@ gemm_pipe(Operands op, TileArgs ta) {
             const int c = pos ^ kmajor_key(r);
             return unsigned((r * ld + c * 8) * 2);
         }
-        const int row = u * 16 + (lane >> 2);
-        return unsigned((row * ld + ((lane & 3) ^ row_key(lane >> 2)) * 8) * 2);
+        constexpr int kCpr = BK / 8;              // 16-byte chunks per row
+        const int row = u * (64 / kCpr) + lane / kCpr;
+        return unsigned((row * ld + ((lane % kCpr) ^ row_key<BK>(row)) * 8) * 2);
     };
     unsigned voff[PER];
 #pragma unroll
@@ -269,7 +296,7 @@ gemm_pipe(Operands op, TileArgs ta) {
     auto frag_rowmajor = [&](const _Float16* region, int r0, int kk) {
         const int row = r0 + fr;
         return *reinterpret_cast<const f16x8*>(region + row * BK +
-                                               (((kk * 2 + fc) ^ row_key(row)) * 8));
+                                               (((kk * 2 + fc) ^ row_key<BK>(row)) * 8));
     };
     // Lane j of a 16-lane group addresses row k0 + j / 4, columns
     // c0 + 4 (j % 4) .. + 3; the read hands lane i column c0 + i of rows
@@ -326,7 +353,7 @@ gemm_pipe(Operands op, TileArgs ta) {
         }
     };
 
-    // Prologue: stream steps 0 .. S-2 and the first half of step S-1.
+    // Prologue: stream steps 0 .. S-2 and the post-barrier share of step S-1.
     Issue cur;
     cur.tile = 0;
     cur.st = 0;
@@ -338,15 +365,16 @@ gemm_pipe(Operands op, TileArgs ta) {
         advance(cur);
     }
 #pragma unroll
-    for (int q = 0; q < HALF; ++q) issue_q(cur, q);
-    wait_vm_lgkm0<(S - 2) * PER + HALF>();
+    for (int q = 0; q < POST; ++q) issue_q(cur, q);
+    wait_vm_lgkm0<(S - 2) * PER + POST>();
     block_sync();
 
     f16x8 xf[2][FM], wf[2][FN];
 #pragma unroll
     for (int q = 0; q < FM + FN; ++q) read_one(0, 0, q, xf[0], wf[0]);
     int st = 0;
-    // `cur` is the step whose second half goes out in the next sub-step 0.
+    // `cur` is the step whose remaining loads go out in the next sub-steps
+    // 0 .. NS - 2.
     for (int i = 0; i < n_tiles; ++i) {
         const Tile t = tile(i);
         // Bias of this lane's columns, for the epilogue: buffer loads with the
@@ -364,49 +392,13 @@ gemm_pipe(Operands op, TileArgs ta) {
                         f32x4, __builtin_amdgcn_raw_buffer_load_b128(rbias, unsigned(c) * 4u, 0, 0));
                 }
         }
-        const int steps = (t.k_end - t.k_begin) / BK;
-        for (int s = 0; s < steps; ++s) {
-            Issue nxt = cur;
-            advance(nxt);
-            wait_frags();
-            // Sub-step 0: reads of sub-step 1, second half of step `cur`.
-            mfmas(xf[0], wf[0], [&](int q) {
-                if (q < FM + FN) read_one(st, 1, q, xf[1], wf[1]);
-                if (q % kLoadEvery == kLoadEvery - 1 && HALF + q / kLoadEvery < PER)
-                    issue_q(cur, HALF + q / kLoadEvery);
-            });
-            // The next step has landed once only the loads of the S - 2 steps
-            // after it remain outstanding. For the first S - 2 steps of a tile
-            // the previous tile's stores and this tile's bias loads went out
-            // after the step as well (vmcnt retires in issue order), so they may
-            // stay in flight too: the stores drain while the MFMAs run. After
-            // the barrier nobody reads stage st any more.
-            if (s <= S - 3) {
-                if (i == 0) wait_vm_lgkm0<cap63((S - 2) * PER + kBiasLoads)>();
-                else wait_vm_lgkm0<cap63((S - 2) * PER + kBiasLoads + kStores)>();
-            } else {
-                wait_vm_lgkm0<(S - 2) * PER>();
-            }
-            block_sync();
-            const int st_next = st + 1 == S ? 0 : st + 1;
-            // Sub-step 1: reads of the next step's sub-step 0, first half of `nxt`.
-            mfmas(xf[1], wf[1], [&](int q) {
-                if (q < FM + FN) read_one(st_next, 0, q, xf[0], wf[0]);
-                if (q % kLoadEvery == kLoadEvery - 1 && q / kLoadEvery < HALF)
-                    issue_q(nxt, q / kLoadEvery);
-            });
-            st = st_next;
-            cur = nxt;
-        }
-
-        // ---- epilogue: per staged block of a wave, registers -> staging ->
-        // whole 16-byte row chunks to HBM.
+        // The epilogue's chunk addressing: byte offset (elements of `elem`
+        // bytes) of chunk q of this lane in the staged block (j, h), or past
+        // the end when the chunk is outside the output (n % 8 == 0 here, so a
+        // chunk is whole once it starts).
         const int row_base = t.m0 + wm * WTM;
         const int col_base = t.n0 + wn * WTN;
         const unsigned out_bytes = unsigned(size_t(m) * n * E::kOutElem);
-        // Byte offset (elements of `elem` bytes) of chunk q of this lane in the
-        // staged block (j, h), or past the end when the chunk is outside the
-        // output (n % 8 == 0 here, so a chunk is whole once it starts).
         auto chunk_at = [&](int j, int h, int q, int elem, int* r, int* cc) {
             const int c = q * 64 + lane;
             *r = c / E::kCpr;
@@ -416,6 +408,67 @@ gemm_pipe(Operands op, TileArgs ta) {
             return gr < m && gc < n ? (unsigned(gr) * unsigned(n) + unsigned(gc)) * unsigned(elem)
                                     : 0xfffffff0u;
         };
+        f32x4 res_all[kResEarly ? FM : 1][kResEarly ? E::kSubs : 1][kResEarly ? E::kPerLane : 1];
+        if constexpr (kResEarly) {
+            const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(static_cast<const float*>(op.aux) + t.y_off), 0, out_bytes,
+                0x00020000);
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+#pragma unroll
+                for (int h = 0; h < E::kSubs; ++h)
+#pragma unroll
+                    for (int q = 0; q < E::kPerLane; ++q) {
+                        int r, cc;
+                        res_all[j][h][q] = __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                       rs, chunk_at(j, h, q, 4, &r, &cc), 0, 0));
+                    }
+        }
+        const int steps = (t.k_end - t.k_begin) / BK;
+        for (int s = 0; s < steps; ++s) {
+            Issue nxt = cur;
+            advance(nxt);
+            // Sub-steps 0 .. NS - 2: reads of the sub-step after, the rest of
+            // step `cur`'s loads.
+#pragma unroll
+            for (int kk = 0; kk < NS - 1; ++kk) {
+                wait_frags();
+                mfmas(xf[kk & 1], wf[kk & 1], [&](int q) {
+                    if (q < FM + FN) read_one(st, kk + 1, q, xf[(kk + 1) & 1], wf[(kk + 1) & 1]);
+                    const int li = POST + kk * PRE + q / kLoadEvery;
+                    if (q % kLoadEvery == kLoadEvery - 1 && q / kLoadEvery < PRE && li < PER)
+                        issue_q(cur, li);
+                });
+            }
+            // The next step has landed once only the loads of the S - 2 steps
+            // after it remain outstanding. For the first S - 2 steps of a tile
+            // the previous tile's stores and this tile's bias (and residual)
+            // loads went out
+            // after the step as well (vmcnt retires in issue order), so they may
+            // stay in flight too: the stores drain while the MFMAs run. After
+            // the barrier nobody reads stage st any more.
+            if (s <= S - 3) {
+                if (i == 0) wait_vm_lgkm0<cap63((S - 2) * PER + kEarlyLoads)>();
+                else wait_vm_lgkm0<cap63((S - 2) * PER + kEarlyLoads + kStores)>();
+            } else {
+                wait_vm_lgkm0<(S - 2) * PER>();
+            }
+            block_sync();
+            const int st_next = st + 1 == S ? 0 : st + 1;
+            // Sub-step NS - 1: reads of the next step's sub-step 0, the first
+            // POST loads of `nxt` (into stage st, free since the barrier).
+            mfmas(xf[1], wf[1], [&](int q) {
+                if (q < FM + FN) read_one(st_next, 0, q, xf[0], wf[0]);
+                if (q % kLoadEvery == kLoadEvery - 1 && q / kLoadEvery < POST)
+                    issue_q(nxt, q / kLoadEvery);
+            });
+            st = st_next;
+            cur = nxt;
+        }
+
+        // ---- epilogue: per staged block of a wave, registers -> staging ->
+        // whole 16-byte row chunks to HBM.
         const bool accumulate = ST == Store::kTn && !split && op.accumulate;
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
@@ -427,7 +480,10 @@ gemm_pipe(Operands op, TileArgs ta) {
                 constexpr bool kReads = ST == Store::kBiasResidual || ST == Store::kDGelu ||
                                         ST == Store::kTn;
                 f32x4 rd[kReads ? E::kPerLane : 1];
-                if constexpr (ST == Store::kBiasResidual || ST == Store::kTn) {
+                if constexpr (kResEarly) {
+#pragma unroll
+                    for (int q = 0; q < E::kPerLane; ++q) rd[q] = res_all[j][h][q];
+                } else if constexpr (ST == Store::kBiasResidual || ST == Store::kTn) {
                     const float* src = ST == Store::kTn ? static_cast<const float*>(op.y)
                                                         : static_cast<const float*>(op.aux);
                     const auto rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -462,9 +518,10 @@ gemm_pipe(Operands op, TileArgs ta) {
                 for (int pass = 0; pass < E::kPasses; ++pass) {
                     // GELU: pass 0 writes pre = RN16(s), pass 1 y = RN16(gelu(s)).
                     const bool gelu_pass = ST == Store::kBiasGelu && pass == 1;
-                    const bool mine = !E::kF32 || (fr >> 4) == h;   // FP32: 16 of the 32 rows
+                    // The lanes holding the block's rows (each lane holds one row).
+                    const bool mine = E::kRows == 32 || fr / E::kRows == h;
                     if (mine) {
-                        const int srow = E::kF32 ? (fr & 15) : fr;
+                        const int srow = fr % E::kRows;
 #pragma unroll
                         for (int ii = 0; ii < FN; ++ii) {
 #pragma unroll
@@ -538,13 +595,16 @@ gemm_pipe(Operands op, TileArgs ta) {
 }
 
 struct PipeConfig {
-    int bm, bn, stages;
+    int bm, bn, stages, bk;
 };
 
-constexpr PipeConfig kPipeConfigs[] = {{256, 256, 3}, {256, 192, 4}, {128, 192, 4}, {256, 64, 4}};
+constexpr PipeConfig kPipeConfigs[] = {
+    {256, 256, 3, 32}, {256, 192, 4, 32}, {128, 192, 4, 32}, {256, 64, 4, 32},
+    {128, 192, 3, 64}, {256, 128, 3, 64}};
 
-// FLINT_GEMM_PIPE: "0" routes every call to gemm.hip's kernels; "bm,bn,stages"
-// forces one of kPipeConfigs (tuning sweeps and tests; read per call).
+// FLINT_GEMM_PIPE: "0" routes every call to gemm.hip's kernels;
+// "bm,bn,stages[,bk]" forces one of kPipeConfigs (tuning sweeps and tests;
+// read per call; bk defaults to 32).
 bool pipe_forced(PipeConfig* out, bool* disabled) {
     *disabled = false;
     const char* e = std::getenv("FLINT_GEMM_PIPE");
@@ -554,9 +614,11 @@ bool pipe_forced(PipeConfig* out, bool* disabled) {
         return false;
     }
     PipeConfig c{};
-    if (std::sscanf(e, "%d,%d,%d", &c.bm, &c.bn, &c.stages) != 3) return false;
+    c.bk = 32;
+    const int got = std::sscanf(e, "%d,%d,%d,%d", &c.bm, &c.bn, &c.stages, &c.bk);
+    if (got != 3 && got != 4) return false;
     for (const PipeConfig& k : kPipeConfigs) {
-        if (k.bm == c.bm && k.bn == c.bn && k.stages == c.stages) {
+        if (k.bm == c.bm && k.bn == c.bn && k.stages == c.stages && k.bk == c.bk) {
             *out = c;
             return true;
         }
@@ -569,26 +631,42 @@ bool pipe_forced(PipeConfig* out, bool* disabled) {
 size_t lds_bytes(const PipeConfig& c, Store st) {
     const bool f32 = st == Store::kBiasResidual || st == Store::kTn || st == Store::kDGelu;
     const int wtn = c.bn / pipe_waves_n(c.bn), per = f32 ? 4 : 8, rows = f32 ? 16 : 32;
-    return size_t(c.stages) * (c.bm + c.bn) * kPipeBK * 2 +
-           4 * size_t(rows) * (wtn + per) * (f32 ? 4 : 2);
+    const size_t stages = size_t(c.stages) * (c.bm + c.bn) * c.bk * 2;
+    const size_t staging = 4 * size_t(rows) * (wtn + per) * (f32 ? 4 : 2);
+    return stages + staging <= kPipeMaxLds ? stages + staging : stages + staging / 2;
+}
+
+// Whether a configuration can run an epilogue over k: it fits in LDS, k is
+// whole k-steps, and the 64-deep steps serve NT and NN only (TN's operands
+// are k-major, whole 128-byte lines at either depth).
+bool usable(const PipeConfig& c, Store st, size_t k) {
+    if (lds_bytes(c, st) > kPipeMaxLds || k % size_t(c.bk) != 0) return false;
+    return c.bk == 32 || (st != Store::kTn && st != Store::kTnHalf);
+}
+
+// Relative throughput per unit of tile area, measured on the GPT-2 shapes at
+// many tiles per CU (256 x 256 x 32 as 1). Larger tiles load fewer bytes per
+// FLOP; 64-deep k-steps load whole 128-byte lines of row-major operands, which
+// the vector memory path delivers at twice the rate of 64-byte pieces.
+// (256 x 64: 51 FLOP per loaded byte, worth it only where n <= 64.)
+double pipe_eff(const PipeConfig& c) {
+    if (c.bn == 64) return 0.55;
+    if (c.bk == 64) return c.bm == 128 ? 0.84 : 0.94;
+    return c.bm == 128 ? 0.80 : (c.bn == 256 ? 1.0 : 0.97);
 }
 
 // The macro-tile: whole waves of tiles over the CUs weigh most (a K = 768
 // tile is short, so a partial last wave costs nearly a full one); among equal
 // wave counts the larger tile needs fewer bytes per FLOP.
-PipeConfig pick_pipe(size_t m, size_t n, size_t slices, int cus, Store st) {
+PipeConfig pick_pipe(size_t m, size_t n, size_t k, size_t slices, int cus, Store st) {
     PipeConfig best = kPipeConfigs[0];
     double best_cost = 1e300;
     for (const PipeConfig& c : kPipeConfigs) {
-        if (lds_bytes(c, st) > kPipeMaxLds) continue;
+        if (!usable(c, st, k)) continue;
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn) *
                              double(slices);
         const double rounds = std::ceil(tiles / cus);
-        // Relative time of one tile: its area over its measured throughput per
-        // unit area (256 x 256 as 1; the smaller tiles move more bytes per FLOP).
-        // (256 x 64: 51 FLOP per loaded byte, worth it only where n <= 64.)
-        const double eff = c.bn == 64 ? 0.55 : c.bm == 128 ? 0.80 : (c.bn == 256 ? 1.0 : 0.97);
-        const double cost = rounds * double(c.bm) * double(c.bn) / eff;
+        const double cost = rounds * double(c.bm) * double(c.bn) / pipe_eff(c);
         if (cost < best_cost * 0.999) {
             best_cost = cost;
             best = c;
@@ -606,11 +684,11 @@ void plan_tn(size_t m, size_t n, size_t k, int max_splits, int cus, bool accumul
              PipeConfig* best_c, int* best_s) {
     const Store st = Store::kTn;
     double best = 1e300;
-    *best_c = pick_pipe(m, n, 1, cus, st);
+    *best_c = pick_pipe(m, n, k, 1, cus, st);
     *best_s = 1;
     for (const PipeConfig& c : kPipeConfigs) {
-        if (lds_bytes(c, st) > kPipeMaxLds) continue;
-        const double eff = c.bn == 64 ? 0.55 : c.bm == 128 ? 0.80 : (c.bn == 256 ? 1.0 : 0.97);
+        if (c.bk != kPipeBK || !usable(c, st, kPipeBK)) continue;
+        const double eff = pipe_eff(c);
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn);
         for (int sp = 1; sp <= max_splits; ++sp) {
             const size_t len = (k + sp - 1) / sp;
@@ -650,18 +728,21 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     size_t gx = std::min(total, size_t(cus));
     if (gx >= 8) gx -= gx % 8;
     const dim3 grid(unsigned(gx), 1, 1);
-#define FLINT_PIPE_CASE(BM_, BN_, S_)                                                          \
-    if constexpr (pipe_lds_bytes<BM_, BN_, S_, L, ST>() <= kPipeMaxLds) {                      \
-        if (c.bm == BM_ && c.bn == BN_ && c.stages == S_) {                                    \
-            hipLaunchKernelGGL((gemm_pipe<BM_, BN_, S_, L, ST>), grid, dim3(256), 0, stream, op, \
-                               ta);                                                            \
+#define FLINT_PIPE_CASE(BM_, BN_, S_, BK_)                                                     \
+    if constexpr (pipe_lds_bytes<BM_, BN_, S_, BK_, L, ST>() <= kPipeMaxLds &&                 \
+                  (BK_ == 32 || (ST != Store::kTn && ST != Store::kTnHalf))) {                 \
+        if (c.bm == BM_ && c.bn == BN_ && c.stages == S_ && c.bk == BK_) {                     \
+            hipLaunchKernelGGL((gemm_pipe<BM_, BN_, S_, BK_, L, ST>), grid, dim3(256), 0,      \
+                               stream, op, ta);                                                \
             return hipGetLastError();                                                          \
         }                                                                                      \
     }
-    FLINT_PIPE_CASE(256, 256, 3)
-    FLINT_PIPE_CASE(256, 192, 4)
-    FLINT_PIPE_CASE(128, 192, 4)
-    FLINT_PIPE_CASE(256, 64, 4)
+    FLINT_PIPE_CASE(256, 256, 3, 32)
+    FLINT_PIPE_CASE(256, 192, 4, 32)
+    FLINT_PIPE_CASE(128, 192, 4, 32)
+    FLINT_PIPE_CASE(256, 64, 4, 32)
+    FLINT_PIPE_CASE(128, 192, 3, 64)
+    FLINT_PIPE_CASE(256, 128, 3, 64)
 #undef FLINT_PIPE_CASE
     return hipErrorInvalidValue;
 }
@@ -728,7 +809,8 @@ hipError_t launch_gemm_pipe_tn(void* y, const void* x, const void* w, size_t m, 
     bool disabled = false;
     plan_tn(m, n, k, workspace != nullptr ? max_splits : 1, cus, accumulate, &c, &sp);
     PipeConfig forced;
-    if (pipe_forced(&forced, &disabled) && lds_bytes(forced, Store::kTn) <= kPipeMaxLds)
+    if (pipe_forced(&forced, &disabled) && forced.bk == kPipeBK &&
+        usable(forced, Store::kTn, kPipeBK))
         c = forced;
     const size_t len = ((k + sp - 1) / sp + kPipeBK - 1) / kPipeBK * kPipeBK;
     Operands op{};
@@ -748,7 +830,7 @@ hipError_t launch_gemm_pipe_tn(void* y, const void* x, const void* w, size_t m, 
 bool gemm_pipe_eligible(GemmLayout gl, Epilogue e, size_t m, size_t n, size_t k) {
     bool disabled = false;
     PipeConfig forced;
-    const bool force = pipe_forced(&forced, &disabled);
+    pipe_forced(&forced, &disabled);
     if (disabled || m == 0 || n == 0 || n % 8 != 0 || k % kPipeBK != 0 || k < kPipeBK) return false;
     const Layout l = layout_of(gl);
     const Store st = store_of(e, l);
@@ -767,11 +849,7 @@ bool gemm_pipe_eligible(GemmLayout gl, Epilogue e, size_t m, size_t n, size_t k)
         n * k * 2 >= (size_t{1} << 31)) {
         return false;
     }
-    if (force) return true;
-    // The residual outputs of GPT-2 are 768 wide: 128-row tiles are needed to
-    // fill the CUs there, and gemm.hip's 128 x 192 x 64 kernel with the
-    // residual prefetched into registers measured as fast as this one's.
-    return st != Store::kBiasResidual || n >= 1024;
+    return true;
 }
 
 hipError_t launch_gemm_pipe(GemmLayout gl, Epilogue e, void* y, const void* x, const void* w,
@@ -796,8 +874,7 @@ hipError_t launch_gemm_pipe(GemmLayout gl, Epilogue e, void* y, const void* x, c
     const Store st = store_of(e, l);
     PipeConfig c;
     bool disabled = false;
-    if (!pipe_forced(&c, &disabled) || lds_bytes(c, st) > kPipeMaxLds)
-        c = pick_pipe(m, n, slices, cus, st);
+    if (!pipe_forced(&c, &disabled) || !usable(c, st, k)) c = pick_pipe(m, n, k, slices, cus, st);
     switch (l) {
     case Layout::kNT: return dispatch_pipe<Layout::kNT>(c, st, op, slices, split_len, cus, stream);
     case Layout::kNN: return dispatch_pipe<Layout::kNN>(c, st, op, slices, split_len, cus, stream);
