@@ -642,22 +642,26 @@ size_t lds_bytes(const PipeConfig& c, Store st) {
     return stages + staging <= kPipeMaxLds ? stages + staging : stages + staging / 2;
 }
 
-// Whether a configuration can run an epilogue over k: it fits in LDS, k is
-// whole k-steps, and the 64-deep steps serve NT and NN only (TN's operands
-// are k-major, whole 128-byte lines at either depth).
+// Whether a configuration can run an epilogue over k: it fits in LDS and k is
+// whole k-steps.
 bool usable(const PipeConfig& c, Store st, size_t k) {
-    if (lds_bytes(c, st) > kPipeMaxLds || k % size_t(c.bk) != 0) return false;
-    return c.bk == 32 || (st != Store::kTn && st != Store::kTnHalf);
+    return lds_bytes(c, st) <= kPipeMaxLds && k % size_t(c.bk) == 0;
 }
 
 // Relative throughput per unit of tile area, measured on the GPT-2 shapes at
 // many tiles per CU (256 x 256 x 32 as 1). Larger tiles load fewer bytes per
 // FLOP; 64-deep k-steps load whole 128-byte lines of row-major operands, which
 // the vector memory path delivers at twice the rate of 64-byte pieces.
-// (256 x 64: 51 FLOP per loaded byte, worth it only where n <= 64.)
-double pipe_eff(const PipeConfig& c) {
+// (256 x 64: 51 FLOP per loaded byte, worth it only where n <= 64.) TN's
+// operands are k-major, whole lines at either depth; there the 64-deep steps
+// gain from half the barriers, most in 128 x 192 tiles.
+double pipe_eff(const PipeConfig& c, Store st) {
     if (c.bn == 64) return 0.55;
-    if (c.bk == 64) return c.bm == 128 ? 0.84 : 0.94;
+    if (st == Store::kTn || st == Store::kTnHalf) {
+        if (c.bk == 64) return c.bm == 128 ? 0.88 : 0.80;
+    } else if (c.bk == 64) {
+        return c.bm == 128 ? 0.84 : 0.94;
+    }
     return c.bm == 128 ? 0.80 : (c.bn == 256 ? 1.0 : 0.97);
 }
 
@@ -672,7 +676,7 @@ PipeConfig pick_pipe(size_t m, size_t n, size_t k, size_t slices, int cus, Store
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn) *
                              double(slices);
         const double rounds = std::ceil(tiles / cus);
-        const double cost = rounds * double(c.bm) * double(c.bn) / pipe_eff(c);
+        const double cost = rounds * double(c.bm) * double(c.bn) / pipe_eff(c, st);
         if (cost < best_cost * 0.999) {
             best_cost = cost;
             best = c;
@@ -686,19 +690,23 @@ PipeConfig pick_pipe(size_t m, size_t n, size_t k, size_t slices, int cus, Store
 // caller's workspace. Cost: rounds of (tile, split) units over the CUs times a
 // unit's work, plus the partials' reduce pass when there is more than one
 // split ((splits + 1 or 2) * m * n * 4 bytes at ~5 TB/s, and a launch).
+// `only`, when given, is the one configuration considered.
 void plan_tn(size_t m, size_t n, size_t k, int max_splits, int cus, bool accumulate,
-             PipeConfig* best_c, int* best_s) {
+             const PipeConfig* only, PipeConfig* best_c, int* best_s) {
     const Store st = Store::kTn;
     double best = 1e300;
-    *best_c = pick_pipe(m, n, k, 1, cus, st);
+    *best_c = only != nullptr ? *only : pick_pipe(m, n, k, 1, cus, st);
     *best_s = 1;
     for (const PipeConfig& c : kPipeConfigs) {
-        if (c.bk != kPipeBK || !usable(c, st, kPipeBK)) continue;
-        const double eff = pipe_eff(c);
+        if (!usable(c, st, k)) continue;
+        if (only != nullptr && (c.bm != only->bm || c.bn != only->bn ||
+                                c.stages != only->stages || c.bk != only->bk))
+            continue;
+        const double eff = pipe_eff(c, st);
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn);
         for (int sp = 1; sp <= max_splits; ++sp) {
             const size_t len = (k + sp - 1) / sp;
-            const size_t len32 = (len + kPipeBK - 1) / kPipeBK * kPipeBK;
+            const size_t len32 = (len + c.bk - 1) / c.bk * c.bk;
             if (size_t(sp - 1) * len32 >= k) continue;   // the last split would be empty
             const double rounds = std::ceil(tiles * sp / cus);
             // One 256 x 256 x 32 step of a unit is ~0.5 us at the pipeline's rate.
@@ -735,8 +743,7 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     if (gx >= 8) gx -= gx % 8;
     const dim3 grid(unsigned(gx), 1, 1);
 #define FLINT_PIPE_CASE(BM_, BN_, S_, BK_)                                                     \
-    if constexpr (pipe_lds_bytes<BM_, BN_, S_, BK_, L, ST>() <= kPipeMaxLds &&                 \
-                  (BK_ == 32 || (ST != Store::kTn && ST != Store::kTnHalf))) {                 \
+    if constexpr (pipe_lds_bytes<BM_, BN_, S_, BK_, L, ST>() <= kPipeMaxLds) {                 \
         if (c.bm == BM_ && c.bn == BN_ && c.stages == S_ && c.bk == BK_) {                     \
             hipLaunchKernelGGL((gemm_pipe<BM_, BN_, S_, BK_, L, ST>), grid, dim3(256), 0,      \
                                stream, op, ta);                                                \
@@ -813,12 +820,11 @@ hipError_t launch_gemm_pipe_tn(void* y, const void* x, const void* w, size_t m, 
     PipeConfig c;
     int sp = 1;
     bool disabled = false;
-    plan_tn(m, n, k, workspace != nullptr ? max_splits : 1, cus, accumulate, &c, &sp);
     PipeConfig forced;
-    if (pipe_forced(&forced, &disabled) && forced.bk == kPipeBK &&
-        usable(forced, Store::kTn, kPipeBK))
-        c = forced;
-    const size_t len = ((k + sp - 1) / sp + kPipeBK - 1) / kPipeBK * kPipeBK;
+    const bool force = pipe_forced(&forced, &disabled) && usable(forced, Store::kTn, k);
+    plan_tn(m, n, k, workspace != nullptr ? max_splits : 1, cus, accumulate,
+            force ? &forced : nullptr, &c, &sp);
+    const size_t len = ((k + sp - 1) / sp + c.bk - 1) / c.bk * c.bk;
     Operands op{};
     op.y = y;
     op.x = static_cast<const _Float16*>(x);
