@@ -658,7 +658,7 @@ bool usable(const PipeConfig& c, Store st, size_t k) {
 double pipe_eff(const PipeConfig& c, Store st) {
     if (c.bn == 64) return 0.55;
     if (st == Store::kTn || st == Store::kTnHalf) {
-        if (c.bk == 64) return c.bm == 128 ? 0.88 : 0.80;
+        if (c.bk == 64) return c.bm == 128 ? 0.86 : 0.80;
     } else if (c.bk == 64) {
         return c.bm == 128 ? 0.84 : 0.94;
     }
