@@ -141,15 +141,21 @@ gemm_pipe(Operands op, TileArgs ta) {
     constexpr int IA = BM * BK / 2048, IB = BN * BK / 2048;   // 1 KB loads per thread per step
     constexpr int PER = IA + IB;
     // A step's loads: POST of them in the sub-step after the barrier, the rest
-    // PRE at a time in the NS - 1 sub-steps before the next one.
-    constexpr int POST = PER / NS;
-    constexpr int PRE = (PER - POST + NS - 2) / (NS - 1);
+    // PRE at a time in the NS - 1 sub-steps before the next one. With two
+    // stages all of them go out after the barrier (the stage is free from
+    // there on, and the step after is all the lead there is).
+    static_assert(S >= 2 && (S > 2 || BK == 64), "stages");
+    constexpr bool kAllPost = S == 2;
+    constexpr int POST = kAllPost ? PER : PER / NS;
+    constexpr int PRE = kAllPost ? 0 : (PER - POST + NS - 2) / (NS - 1);
     constexpr int kMaxLoads = POST > PRE ? POST : PRE;
     // A sub-step's loads go out after every second MFMA, or after every one
-    // when the sub-step has too few MFMAs for that (64-wide tiles); every load
-    // must get a slot, or the waits below would count loads never issued.
+    // when the sub-step has too few MFMAs for that (64-wide tiles, two-stage
+    // tiles); every load must get a slot, or the waits below would count
+    // loads never issued. Two-stage tiles issue what has no slot right after
+    // the sub-step's MFMAs.
     constexpr int kLoadEvery = FM * FN >= 2 * kMaxLoads ? 2 : 1;
-    static_assert(FM * FN >= kMaxLoads * kLoadEvery, "a slot for every load");
+    static_assert(kAllPost || FM * FN >= kMaxLoads * kLoadEvery, "a slot for every load");
     // x side (rows m, the MFMA's B operand) and w side (rows n, its A operand)
     // are k-major ([32 k][rows] in LDS) or row-major ([rows][32 k]).
     constexpr bool kXM = L == Layout::kTN;
@@ -449,12 +455,13 @@ gemm_pipe(Operands op, TileArgs ta) {
             }
             // The next step has landed once only the loads of the S - 2 steps
             // after it remain outstanding. For the first S - 2 steps of a tile
-            // the previous tile's stores and this tile's bias (and residual)
-            // loads went out
-            // after the step as well (vmcnt retires in issue order), so they may
-            // stay in flight too: the stores drain while the MFMAs run. After
-            // the barrier nobody reads stage st any more.
-            if (s <= S - 3) {
+            // (S - 1 with kAllPost, where no loads follow the stores before
+            // the step after) the previous tile's stores and this tile's bias
+            // (and residual) loads went out after the step as well (vmcnt
+            // retires in issue order), so they may stay in flight too: the
+            // stores drain while the MFMAs run. After the barrier nobody reads
+            // stage st any more.
+            if (s <= S - (kAllPost ? 2 : 3)) {
                 if (i == 0) wait_vm_lgkm0<cap63((S - 2) * PER + kEarlyLoads)>();
                 else wait_vm_lgkm0<cap63((S - 2) * PER + kEarlyLoads + kStores)>();
             } else {
@@ -469,6 +476,10 @@ gemm_pipe(Operands op, TileArgs ta) {
                 if (q % kLoadEvery == kLoadEvery - 1 && q / kLoadEvery < POST)
                     issue_q(nxt, q / kLoadEvery);
             });
+            if constexpr (kAllPost) {
+#pragma unroll
+                for (int q = FM * FN / kLoadEvery; q < POST; ++q) issue_q(nxt, q);
+            }
             st = st_next;
             cur = nxt;
         }
@@ -606,7 +617,7 @@ struct PipeConfig {
 
 constexpr PipeConfig kPipeConfigs[] = {
     {256, 256, 3, 32}, {256, 192, 4, 32}, {128, 192, 4, 32}, {256, 64, 4, 32},
-    {128, 192, 3, 64}, {256, 128, 3, 64}};
+    {128, 192, 3, 64}, {256, 128, 3, 64}, {256, 256, 2, 64}, {256, 192, 2, 64}};
 
 // FLINT_GEMM_PIPE: "0" routes every call to gemm.hip's kernels;
 // "bm,bn,stages[,bk]" forces one of kPipeConfigs (tuning sweeps and tests;
@@ -657,6 +668,10 @@ bool usable(const PipeConfig& c, Store st, size_t k) {
 // gain from half the barriers, most in 128 x 192 tiles.
 double pipe_eff(const PipeConfig& c, Store st) {
     if (c.bn == 64) return 0.55;
+    // Two stages: worth it for 256 x 192 outside TN (MLP up 59 -> 56 us,
+    // dGELU 77 -> 74 us); 256 x 256 measured no better than at 32-deep steps.
+    if (c.stages == 2)
+        return c.bn == 192 && st != Store::kTn && st != Store::kTnHalf ? 1.0 : 0.5;
     if (st == Store::kTn || st == Store::kTnHalf) {
         if (c.bk == 64) return c.bm == 128 ? 0.86 : 0.80;
     } else if (c.bk == 64) {
@@ -756,6 +771,8 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     FLINT_PIPE_CASE(256, 64, 4, 32)
     FLINT_PIPE_CASE(128, 192, 3, 64)
     FLINT_PIPE_CASE(256, 128, 3, 64)
+    FLINT_PIPE_CASE(256, 256, 2, 64)
+    FLINT_PIPE_CASE(256, 192, 2, 64)
 #undef FLINT_PIPE_CASE
     return hipErrorInvalidValue;
 }
