@@ -8,11 +8,13 @@
 // backward, :721-813 for the passes), so the order of the calls and their
 // precisions match it. Everything else is this library's own: one bump-pointer
 // allocation sized once (HBM holds every layer's activations at GPT-2 124M
-// sizes many times over), every launch through the checked entry points, and
+// sizes many times over), every launch through the checked entry points but
+// the attention products (the batched GEMMs' causal variants, below), and
 // the one zero-fill the backward pass needs done by a kernel rather than a
 // memset, so the pass can be captured in a HIP graph.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <deque>
 #include <iterator>
@@ -374,6 +376,38 @@ flint_status allocate(flint_gpt2& m) {
 
 float score_scale(size_t head_width) { return 1.0f / std::sqrt(float(head_width)); }
 
+// The six attention products go to the batched GEMMs' causal variants: the
+// scores and their gradient are read only at or below the diagonal (the
+// causal softmax passes read the visible chunks alone), and P and dS are zero
+// above it, so the pipeline skips those tiles and k-ranges. The skipped
+// products are exact zeros, so no value that is read changes.
+// FLINT_ATTN_CAUSAL=0 computes everything (the tests compare the two).
+bool attn_causal() {
+    const char* e = std::getenv("FLINT_ATTN_CAUSAL");
+    return e == nullptr || !(e[0] == '0' && e[1] == '\0');
+}
+
+flint_status attn_nt(void* y, const void* x, const void* w, size_t batches, size_t m, size_t n,
+                     size_t k, float scale, flint_stream st) {
+    FLINT_HIP_CHECK(flint::launch_gemm_nt_batched(y, x, w, batches, m, n, k, scale,
+                                                  flint::to_hip(st), attn_causal()));
+    return FLINT_OK;
+}
+
+flint_status attn_nn(void* y, const void* x, const void* w, size_t batches, size_t m, size_t n,
+                     size_t k, flint_stream st) {
+    FLINT_HIP_CHECK(flint::launch_gemm_nn_batched(y, x, w, batches, m, n, k, flint::to_hip(st),
+                                                  attn_causal()));
+    return FLINT_OK;
+}
+
+flint_status attn_tn(void* y, const void* x, const void* w, size_t batches, size_t m, size_t n,
+                     size_t k, flint_stream st) {
+    FLINT_HIP_CHECK(flint::launch_gemm_tn_batched(y, x, w, batches, m, n, k, flint::to_hip(st),
+                                                  attn_causal()));
+    return FLINT_OK;
+}
+
 flint_status layer_norm(const flint_gpt2& m, const Norm& n, const void* x, void* y, void* mean,
                         void* rstd, flint_stream st) {
     return flint_layernorm_forward(y, mean, rstd, x, n.w->data, n.b->data, m.rows, m.cfg.width,
@@ -393,11 +427,10 @@ flint_status forward_layer(const flint_gpt2& m, const Layer& L, flint_stream st)
         FLINT_TRY(flint_heads_split(qkv_parts[i], m.qkv, c.sequences, c.length, c.heads, hw,
                                     3 * w, i * w, st));
     }
-    FLINT_TRY(flint_gemm_nt_batched(m.scores, s.q, s.k, m.head_batches, c.length, c.length, hw,
-                                    score_scale(hw), st));
+    FLINT_TRY(attn_nt(m.scores, s.q, s.k, m.head_batches, c.length, c.length, hw, score_scale(hw),
+                      st));
     FLINT_TRY(flint_causal_softmax_forward(s.p, m.scores, m.head_batches, c.length, st));
-    FLINT_TRY(flint_gemm_nn_batched(m.heads_out, s.p, s.v, m.head_batches, c.length, hw, c.length,
-                                    st));
+    FLINT_TRY(attn_nn(m.heads_out, s.p, s.v, m.head_batches, c.length, hw, c.length, st));
     FLINT_TRY(flint_heads_merge(s.attn_out, m.heads_out, c.sequences, c.length, c.heads, hw, w, 0,
                                 st));
     FLINT_TRY(flint_gemm_nt_bias_residual(s.x_mid, s.attn_out, L.attn_proj.half,
@@ -449,11 +482,11 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
     FLINT_TRY(bias_grad(m, *L.attn_proj.b, m.dres_half, acc, st));
     FLINT_TRY(flint_gemm_nn(m.dh, m.dres_half, L.attn_proj.half, rows, w, w, st));
     FLINT_TRY(flint_heads_split(m.heads_out, m.dh, c.sequences, len, c.heads, hw, w, 0, st));
-    FLINT_TRY(flint_gemm_tn_batched(m.dv, s.p, m.heads_out, nb, len, hw, len, st));
-    FLINT_TRY(flint_gemm_nt_batched(m.scores, m.heads_out, s.v, nb, len, len, hw, 1.0f, st));
+    FLINT_TRY(attn_tn(m.dv, s.p, m.heads_out, nb, len, hw, len, st));
+    FLINT_TRY(attn_nt(m.scores, m.heads_out, s.v, nb, len, len, hw, 1.0f, st));
     FLINT_TRY(flint_causal_softmax_backward(m.scores, s.p, m.scores, nb, len, score_scale(hw), st));
-    FLINT_TRY(flint_gemm_nn_batched(m.dq, m.scores, s.k, nb, len, hw, len, st));
-    FLINT_TRY(flint_gemm_tn_batched(m.dk, m.scores, s.q, nb, len, hw, len, st));
+    FLINT_TRY(attn_nn(m.dq, m.scores, s.k, nb, len, hw, len, st));
+    FLINT_TRY(attn_tn(m.dk, m.scores, s.q, nb, len, hw, len, st));
     const void* const parts[] = {m.dq, m.dk, m.dv};
     for (size_t i = 0; i < 3; ++i) {
         FLINT_TRY(flint_heads_merge(m.qkv, parts[i], c.sequences, len, c.heads, hw, 3 * w, i * w,

@@ -756,7 +756,7 @@ hipError_t run(Operands op, size_t slices, int split_len, hipStream_t stream) {
     const Config c = pick_config(op.m, op.n, S == Store::kTn ? 1 : slices, cus,
                                  S == Store::kBiasGelu, L == Layout::kTN,
                                  S == Store::kBiasResidual);
-    TileArgs ta;
+    TileArgs ta{};
     ta.tiles_m = (op.m + c.bm - 1) / c.bm;
     ta.tiles_n = (op.n + c.bn - 1) / c.bn;
     ta.tiles_per_slice = ta.tiles_m * ta.tiles_n;
@@ -893,29 +893,30 @@ hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_
 }
 
 hipError_t launch_gemm_nt_batched(void* y, const void* x, const void* w, size_t batches,
-                                  size_t m, size_t n, size_t k, float scale, hipStream_t stream) {
+                                  size_t m, size_t n, size_t k, float scale, hipStream_t stream,
+                                  bool causal) {
     if (gemm_pipe_eligible(GemmLayout::kNT, Epilogue::kScale, m, n, k))
         return launch_gemm_pipe(GemmLayout::kNT, Epilogue::kScale, y, x, w, nullptr, nullptr, scale,
-                                batches, m, n, k, false, nullptr, 0, stream);
+                                batches, m, n, k, false, nullptr, 0, stream, causal && m == n);
     Operands op = make_ops(y, x, w, m, n, k);
     op.scale = scale;
     return run<Layout::kNT, Store::kScale>(op, batches, 0, stream);
 }
 
 hipError_t launch_gemm_nn_batched(void* y, const void* x, const void* w, size_t batches,
-                                  size_t m, size_t n, size_t k, hipStream_t stream) {
+                                  size_t m, size_t n, size_t k, hipStream_t stream, bool causal) {
     if (gemm_pipe_eligible(GemmLayout::kNN, Epilogue::kNone, m, n, k))
         return launch_gemm_pipe(GemmLayout::kNN, Epilogue::kNone, y, x, w, nullptr, nullptr, 1.0f,
-                                batches, m, n, k, false, nullptr, 0, stream);
+                                batches, m, n, k, false, nullptr, 0, stream, causal && m == k);
     Operands op = make_ops(y, x, w, m, n, k);
     return run<Layout::kNN, Store::kNone>(op, batches, 0, stream);
 }
 
 hipError_t launch_gemm_tn_batched(void* y, const void* x, const void* w, size_t batches,
-                                  size_t m, size_t n, size_t k, hipStream_t stream) {
+                                  size_t m, size_t n, size_t k, hipStream_t stream, bool causal) {
     if (gemm_pipe_eligible(GemmLayout::kTN, Epilogue::kNone, m, n, k))
         return launch_gemm_pipe(GemmLayout::kTN, Epilogue::kNone, y, x, w, nullptr, nullptr, 1.0f,
-                                batches, m, n, k, false, nullptr, 0, stream);
+                                batches, m, n, k, false, nullptr, 0, stream, causal && m == k);
     Operands op = make_ops(y, x, w, m, n, k);
     return run<Layout::kTN, Store::kTnHalf>(op, batches, 0, stream);
 }

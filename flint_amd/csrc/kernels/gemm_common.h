@@ -133,6 +133,9 @@ struct Operands {
     float scale;
     int accumulate;        // TN: y += instead of y =
     int m, n, k;
+    int causal;            // attention (pipeline only): the per-slice m x m
+                           // operand (NT's y, NN's and TN's x) is zero, or
+                           // not wanted, above its diagonal
 };
 
 }  // namespace

@@ -127,6 +127,32 @@ constexpr size_t pipe_lds_bytes() {
     return size_t(S) * (BM + BN) * BK * 2 + 4 * size_t(E::kHalves) * 2;
 }
 
+// Tiles of one slice at or below the diagonal of a causal NT output: row
+// block tm needs column blocks tn with tn * BN < (tm + 1) * BM.
+__host__ __device__ inline int causal_row_tiles(int tm, int bm, int bn, int tiles_n) {
+    const int c = ((tm + 1) * bm + bn - 1) / bn;
+    return c < tiles_n ? c : tiles_n;
+}
+
+// map_tile for a causal NT output: the same XCD remap, then row block by row
+// block through the tiles at or below the diagonal (tiles_m is small here:
+// attention rows are at most a sequence).
+__device__ inline void map_tile_causal(const TileArgs& t, unsigned id, int bm, int bn, int* slice,
+                                       int* tm, int* tn) {
+    const unsigned total = unsigned(t.tiles_per_slice) * unsigned(t.slices);
+    if ((total & 7u) == 0) id = (id & 7u) * (total >> 3) + (id >> 3);
+    *slice = int(id / unsigned(t.tiles_per_slice));
+    int rest = int(id % unsigned(t.tiles_per_slice));
+    int r = 0;
+    for (; r + 1 < t.tiles_m; ++r) {
+        const int c = causal_row_tiles(r, bm, bn, t.tiles_n);
+        if (rest < c) break;
+        rest -= c;
+    }
+    *tm = r;
+    *tn = rest;
+}
+
 template <int BM, int BN, int S, int BK, Layout L, Store ST>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_pipe(Operands op, TileArgs ta) {
@@ -202,11 +228,20 @@ gemm_pipe(Operands op, TileArgs ta) {
     auto tile = [&](int i) {
         Tile t;
         int tm, tn;
-        map_tile(ta, blockIdx.x + unsigned(i) * gridDim.x, &t.slice, &tm, &tn);
+        if (L == Layout::kNT && op.causal)
+            map_tile_causal(ta, blockIdx.x + unsigned(i) * gridDim.x, BM, BN, &t.slice, &tm, &tn);
+        else
+            map_tile(ta, blockIdx.x + unsigned(i) * gridDim.x, &t.slice, &tm, &tn);
         t.m0 = tm * BM;
         t.n0 = tn * BN;
         t.k_begin = 0;
         t.k_end = K;
+        // Causal NN / TN: x's row (NN) or column (TN) r is zero past r, so an
+        // output row block [m0, m0 + BM) needs k < m0 + BM (NN: keys up to
+        // the block's last query) or k >= m0 (TN: queries from the block's
+        // first key on), in whole k-steps.
+        if (L == Layout::kNN && op.causal) t.k_end = min(K, (t.m0 + BM + BK - 1) / BK * BK);
+        if (L == Layout::kTN && op.causal) t.k_begin = t.m0 / BK * BK;
         t.y_off = 0;
         const _Float16* xs = op.x;
         const _Float16* ws = op.w;
@@ -747,6 +782,11 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     ta.tiles_m = (op.m + c.bm - 1) / c.bm;
     ta.tiles_n = (op.n + c.bn - 1) / c.bn;
     ta.tiles_per_slice = ta.tiles_m * ta.tiles_n;
+    if (L == Layout::kNT && op.causal) {
+        ta.tiles_per_slice = 0;
+        for (int r = 0; r < ta.tiles_m; ++r)
+            ta.tiles_per_slice += causal_row_tiles(r, c.bm, c.bn, ta.tiles_n);
+    }
     ta.slices = int(slices);
     ta.group_m = 8;
     ta.split_len = split_len;
@@ -884,7 +924,7 @@ bool gemm_pipe_eligible(GemmLayout gl, Epilogue e, size_t m, size_t n, size_t k)
 hipError_t launch_gemm_pipe(GemmLayout gl, Epilogue e, void* y, const void* x, const void* w,
                             const void* bias, void* aux, float scale, size_t slices, size_t m,
                             size_t n, size_t k, bool accumulate, void* partials, int split_len,
-                            hipStream_t stream) {
+                            hipStream_t stream, bool causal) {
     int cus = 256;
     if (hipError_t err = device_cus(&cus); err != hipSuccess) return err;
     Operands op{};
@@ -900,6 +940,9 @@ hipError_t launch_gemm_pipe(GemmLayout gl, Epilogue e, void* y, const void* x, c
     op.n = int(n);
     op.k = int(k);
     const Layout l = layout_of(gl);
+    // Causal needs the square operand, and no TN split (k-ranges of its own).
+    op.causal = causal && split_len == 0 &&
+                        (l == Layout::kNT ? m == n : m == k) ? 1 : 0;
     const Store st = store_of(e, l);
     PipeConfig c;
     bool disabled = false;

@@ -35,10 +35,13 @@ bool gemm_pipe_eligible(GemmLayout l, Epilogue e, size_t m, size_t n, size_t k);
 hipError_t launch_gemm_pipe_tn(void* y, const void* x, const void* w, size_t m, size_t n,
                                size_t k, bool accumulate, void* workspace, int max_splits,
                                int* splits, hipStream_t stream);
+// causal: the per-slice m x m operand is zero above its diagonal (NT: only the
+// output's tiles at or below it are computed; NN / TN: each tile's k-range is
+// cut to where that operand can be nonzero). Requires m == n (NT) or m == k.
 hipError_t launch_gemm_pipe(GemmLayout l, Epilogue e, void* y, const void* x, const void* w,
                             const void* bias, void* aux, float scale, size_t slices, size_t m,
                             size_t n, size_t k, bool accumulate, void* partials, int split_len,
-                            hipStream_t stream);
+                            hipStream_t stream, bool causal = false);
 hipError_t launch_gemm_nn(void* y, const void* x, const void* w, const void* aux, Epilogue e,
                           size_t m, size_t n, size_t k, hipStream_t stream);
 // Number of k splits TN uses for m x n x k on this device (1 = none).
@@ -46,12 +49,20 @@ hipError_t gemm_tn_splits(size_t m, size_t n, size_t k, int* splits, int* split_
 hipError_t gemm_tn_workspace(size_t m, size_t n, size_t k, size_t* bytes);
 hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_t n, size_t k,
                           bool accumulate, void* workspace, hipStream_t stream);
+// The batched GEMMs. causal (attention inside the GPT-2 model only): x (NN,
+// TN) is zero above its diagonal per slice, or (NT) only y's entries at or
+// below the diagonal are wanted; the pipeline then skips the rest, which
+// changes no wanted value (the skipped products are exact zeros). Shapes the
+// pipeline does not take compute everything.
 hipError_t launch_gemm_nt_batched(void* y, const void* x, const void* w, size_t batches,
-                                  size_t m, size_t n, size_t k, float scale, hipStream_t stream);
+                                  size_t m, size_t n, size_t k, float scale, hipStream_t stream,
+                                  bool causal = false);
 hipError_t launch_gemm_nn_batched(void* y, const void* x, const void* w, size_t batches,
-                                  size_t m, size_t n, size_t k, hipStream_t stream);
+                                  size_t m, size_t n, size_t k, hipStream_t stream,
+                                  bool causal = false);
 hipError_t launch_gemm_tn_batched(void* y, const void* x, const void* w, size_t batches,
-                                  size_t m, size_t n, size_t k, hipStream_t stream);
+                                  size_t m, size_t n, size_t k, hipStream_t stream,
+                                  bool causal = false);
 
 // Row reductions.
 constexpr size_t kLayerNormMaxCols = size_t{1} << 24;

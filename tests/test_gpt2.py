@@ -148,6 +148,34 @@ def test_run_twice_and_separate_buffers_give_the_same_bits(flint, cuda):
         assert a[4] == other[4]
 
 
+@pytest.mark.parametrize("length", [1024, 320])
+@pytest.mark.parametrize("force", [None, "128,192,3,64", "256,128,3,64", "256,256,3"])
+def test_causal_attention_products_change_no_bits(flint, cuda, monkeypatch, length, force):
+    """The attention GEMMs skip the tiles and k-ranges above the diagonal
+    (FLINT_ATTN_CAUSAL unset); computing everything (=0) must give the same
+    bits in every output and gradient, whichever tiles the pipeline uses."""
+    cfg = dict(layers=1, heads=4, width=256, block_size=1024, vocab=1000, padded_vocab=1024)
+    sequences = 2
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=11, trained=True)
+    params = {n: t.half().float() for n, t in params.items()}
+    idx, tgt = _tokens(cfg, sequences, length, 12)
+    if force is not None:
+        monkeypatch.setenv("FLINT_GEMM_PIPE", force)
+    monkeypatch.setenv("FLINT_ATTN_CAUSAL", "0")
+    full = _run(flint, cfg, sequences, length, params, idx, tgt, 0.25)
+    monkeypatch.delenv("FLINT_ATTN_CAUSAL")
+    causal = _run(flint, cfg, sequences, length, params, idx, tgt, 0.25)
+    for x, y in zip(full[:3], causal[:3]):
+        assert torch.equal(x.view(torch.int32) if x.dtype == torch.float32 else x,
+                           y.view(torch.int32) if y.dtype == torch.float32 else y)
+    for n in full[3]:
+        assert torch.equal(full[3][n].view(torch.int32), causal[3][n].view(torch.int32)), n
+    assert full[4] == causal[4]
+    assert bool(torch.isfinite(full[1]).all())
+
+
 def test_backward_accumulate_adds_one_pass(flint, cuda):
     """accumulate: every gradient gets this pass's added with one FP32 add, wte
     with two (old + output layer's part) + the embedding's part, so only wte may
