@@ -228,10 +228,28 @@ gemm_pipe(Operands op, TileArgs ta) {
     auto tile = [&](int i) {
         Tile t;
         int tm, tn;
-        if (L == Layout::kNT && op.causal)
+        if (L == Layout::kNT && op.causal) {
             map_tile_causal(ta, blockIdx.x + unsigned(i) * gridDim.x, BM, BN, &t.slice, &tm, &tn);
-        else
+        } else if (op.causal) {
+            // Causal NN / TN: a tile's k-range grows (NN) or shrinks (TN) with
+            // its row block. Tiles go out longest first, each round in the
+            // reverse order of the one before, so a workgroup's long tile of
+            // one round meets a short one in the next; no XCD remap (these
+            // tiles share no operand worth keeping in L2).
+            const unsigned total = unsigned(ta.tiles_per_slice) * unsigned(ta.slices);
+            const unsigned first = unsigned(i) * gridDim.x;
+            const unsigned in_round = min(gridDim.x, total - first);
+            const unsigned rank =
+                first + ((i & 1) ? in_round - 1 - blockIdx.x : unsigned(blockIdx.x));
+            const unsigned per_row = unsigned(ta.slices) * unsigned(ta.tiles_n);
+            const int d = int(rank / per_row);
+            tm = L == Layout::kNN ? ta.tiles_m - 1 - d : d;
+            const unsigned rem = rank % per_row;
+            t.slice = int(rem / unsigned(ta.tiles_n));
+            tn = int(rem % unsigned(ta.tiles_n));
+        } else {
             map_tile(ta, blockIdx.x + unsigned(i) * gridDim.x, &t.slice, &tm, &tn);
+        }
         t.m0 = tm * BM;
         t.n0 = tn * BN;
         t.k_begin = 0;
