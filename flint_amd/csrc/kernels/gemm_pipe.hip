@@ -103,7 +103,9 @@ struct PipeEpi {
         ST == Store::kBiasResidual || ST == Store::kTn || ST == Store::kDGelu;
     static constexpr int kOutElem = ST == Store::kBiasResidual || ST == Store::kTn ? 4 : 2;
     static constexpr int kWtn = WTN;
-    static constexpr int kPerChunk = kF32 ? 4 : 8;            // values per staged chunk
+    // Values per chunk: a chunk is one 16-byte store (8 FP16 or 4 FP32
+    // outputs); dGELU stages FP32 but stores FP16, 8 values a chunk.
+    static constexpr int kPerChunk = kF32 && ST != Store::kDGelu ? 4 : 8;
     static constexpr int kRows = (kF32 ? 16 : 32) / (COMPACT ? 2 : 1);   // rows staged at a time
     static constexpr int kLdw = kWtn + kPerChunk;             // staged row stride (values)
     static constexpr int kHalves = kRows * kLdw * (kF32 ? 2 : 1);   // per wave, in halves
@@ -547,8 +549,7 @@ gemm_pipe(Operands op, TileArgs ta) {
                 // Values the store pass reads back, loaded first so that their
                 // latency overlaps the staging writes: the residual, the old y
                 // of an accumulating TN, dGELU's pre.
-                constexpr bool kReads = ST == Store::kBiasResidual || ST == Store::kDGelu ||
-                                        ST == Store::kTn;
+                constexpr bool kReads = ST == Store::kBiasResidual || ST == Store::kTn;
                 f32x4 rd[kReads ? E::kPerLane : 1];
                 if constexpr (kResEarly) {
 #pragma unroll
@@ -570,6 +571,7 @@ gemm_pipe(Operands op, TileArgs ta) {
                         }
                     }
                 }
+                f16x8 pre8[ST == Store::kDGelu ? E::kPerLane : 1];
                 if constexpr (ST == Store::kDGelu) {
                     const auto rs = __builtin_amdgcn_make_buffer_rsrc(
                         const_cast<void*>(static_cast<const void*>(
@@ -578,10 +580,9 @@ gemm_pipe(Operands op, TileArgs ta) {
 #pragma unroll
                     for (int q = 0; q < E::kPerLane; ++q) {
                         int r, cc;
-                        const i32x2 p = __builtin_amdgcn_raw_buffer_load_b64(
-                            rs, chunk_at(j, h, q, 2, &r, &cc), 0, 0);
-                        const f16x4 ph = __builtin_bit_cast(f16x4, p);
-                        rd[q] = f32x4{float(ph[0]), float(ph[1]), float(ph[2]), float(ph[3])};
+                        pre8[q] = __builtin_bit_cast(
+                            f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                       rs, chunk_at(j, h, q, 2, &r, &cc), 0, 0));
                     }
                 }
 #pragma unroll
@@ -615,6 +616,11 @@ gemm_pipe(Operands op, TileArgs ta) {
                             }
                         }
                     }
+                    // Other lanes read what these lanes wrote: keep the reads
+                    // below (out of the branch). The compiler moved them into
+                    // it once, for the lanes that wrote only.
+                    __builtin_amdgcn_wave_barrier();
+                    asm volatile("" ::: "memory");
                     void* out = ST == Store::kBiasGelu && pass == 0 ? op.aux : op.y;
                     if (split) out = op.partials;
                     out = static_cast<char*>(out) + t.y_off * E::kOutElem;
@@ -624,15 +630,19 @@ gemm_pipe(Operands op, TileArgs ta) {
                     for (int q = 0; q < E::kPerLane; ++q) {
                         int r, cc;
                         if constexpr (ST == Store::kDGelu) {
-                            // y = RN16(sum * GELU'(pre)), 4 outputs = 8 bytes.
+                            // y = RN16(sum * GELU'(pre)), 8 outputs = 16 bytes.
                             const unsigned off = chunk_at(j, h, q, 2, &r, &cc);
-                            const f32x4 sv = *reinterpret_cast<const f32x4*>(
-                                reinterpret_cast<const float*>(cst) + r * E::kLdw + cc * 4);
-                            f16x4 o;
+                            const float* sp = reinterpret_cast<const float*>(cst) + r * E::kLdw + cc * 8;
+                            const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp);
+                            const f32x4 s1 = *reinterpret_cast<const f32x4*>(sp + 4);
+                            f16x8 o;
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) o[e] = _Float16(sv[e] * gelu_grad(rd[q][e]));
-                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, o), rout,
-                                                                  off, 0, kStoreAux);
+                            for (int e = 0; e < 4; ++e) {
+                                o[e] = _Float16(s0[e] * gelu_grad(float(pre8[q][e])));
+                                o[e + 4] = _Float16(s1[e] * gelu_grad(float(pre8[q][e + 4])));
+                            }
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, o), rout,
+                                                                   off, 0, kStoreAux);
                         } else if constexpr (E::kF32) {
                             // Residual: y = residual + (sum + bias). TN: y = sum,
                             // y = old + sum, or a split's partial.
@@ -650,6 +660,9 @@ gemm_pipe(Operands op, TileArgs ta) {
                                                                    off, 0, kStoreAux);
                         }
                     }
+                    // The next block's writes go after these reads.
+                    __builtin_amdgcn_wave_barrier();
+                    asm volatile("" ::: "memory");
                 }
             }
         }
@@ -700,7 +713,8 @@ bool pipe_forced(PipeConfig* out, bool* disabled) {
 // checks the same sum).
 size_t lds_bytes(const PipeConfig& c, Store st) {
     const bool f32 = st == Store::kBiasResidual || st == Store::kTn || st == Store::kDGelu;
-    const int wtn = c.bn / pipe_waves_n(c.bn), per = f32 ? 4 : 8, rows = f32 ? 16 : 32;
+    const int wtn = c.bn / pipe_waves_n(c.bn), per = f32 && st != Store::kDGelu ? 4 : 8,
+              rows = f32 ? 16 : 32;
     const size_t stages = size_t(c.stages) * (c.bm + c.bn) * c.bk * 2;
     const size_t staging = 4 * size_t(rows) * (wtn + per) * (f32 ? 4 : 2);
     return stages + staging <= kPipeMaxLds ? stages + staging : stages + staging / 2;
