@@ -381,7 +381,8 @@ float score_scale(size_t head_width) { return 1.0f / std::sqrt(float(head_width)
 // causal softmax passes read the visible chunks alone), and P and dS are zero
 // above it, so the pipeline skips those tiles and k-ranges. The skipped
 // products are exact zeros, so no value that is read changes.
-// FLINT_ATTN_CAUSAL=0 computes everything (the tests compare the two).
+// FLINT_ATTN_CAUSAL=0 computes everything and writes every zero (the tests
+// compare the two bit for bit).
 bool attn_causal() {
     const char* e = std::getenv("FLINT_ATTN_CAUSAL");
     return e == nullptr || !(e[0] == '0' && e[1] == '\0');
@@ -408,6 +409,34 @@ flint_status attn_tn(void* y, const void* x, const void* w, size_t batches, size
     return FLINT_OK;
 }
 
+// When the NN and TN products that read P and dS both take the causal path,
+// the softmax passes write the masked zeros only up to the end of the
+// 256-column block holding the diagonal: nothing reads past it.
+int attn_zero_span(size_t length, size_t head_width) {
+    using flint::GemmLayout;
+    const bool taken =
+        attn_causal() &&
+        flint::gemm_batched_causal_taken(GemmLayout::kNN, length, head_width, length) &&
+        flint::gemm_batched_causal_taken(GemmLayout::kTN, length, head_width, length);
+    return taken ? flint::kCausalZeroSpan : 0;
+}
+
+flint_status attn_softmax_forward(void* p, const void* s, size_t batches, size_t length,
+                                  size_t head_width, flint_stream st) {
+    FLINT_HIP_CHECK(flint::launch_causal_softmax_forward(p, s, batches * length, length,
+                                                         flint::to_hip(st),
+                                                         attn_zero_span(length, head_width)));
+    return FLINT_OK;
+}
+
+flint_status attn_softmax_backward(void* ds, const void* p, const void* dp, size_t batches,
+                                   size_t length, size_t head_width, flint_stream st) {
+    FLINT_HIP_CHECK(flint::launch_causal_softmax_backward(
+        ds, p, dp, batches * length, length, score_scale(head_width), flint::to_hip(st),
+        attn_zero_span(length, head_width)));
+    return FLINT_OK;
+}
+
 flint_status layer_norm(const flint_gpt2& m, const Norm& n, const void* x, void* y, void* mean,
                         void* rstd, flint_stream st) {
     return flint_layernorm_forward(y, mean, rstd, x, n.w->data, n.b->data, m.rows, m.cfg.width,
@@ -429,7 +458,7 @@ flint_status forward_layer(const flint_gpt2& m, const Layer& L, flint_stream st)
     }
     FLINT_TRY(attn_nt(m.scores, s.q, s.k, m.head_batches, c.length, c.length, hw, score_scale(hw),
                       st));
-    FLINT_TRY(flint_causal_softmax_forward(s.p, m.scores, m.head_batches, c.length, st));
+    FLINT_TRY(attn_softmax_forward(s.p, m.scores, m.head_batches, c.length, hw, st));
     FLINT_TRY(attn_nn(m.heads_out, s.p, s.v, m.head_batches, c.length, hw, c.length, st));
     FLINT_TRY(flint_heads_merge(s.attn_out, m.heads_out, c.sequences, c.length, c.heads, hw, w, 0,
                                 st));
@@ -484,7 +513,7 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
     FLINT_TRY(flint_heads_split(m.heads_out, m.dh, c.sequences, len, c.heads, hw, w, 0, st));
     FLINT_TRY(attn_tn(m.dv, s.p, m.heads_out, nb, len, hw, len, st));
     FLINT_TRY(attn_nt(m.scores, m.heads_out, s.v, nb, len, len, hw, 1.0f, st));
-    FLINT_TRY(flint_causal_softmax_backward(m.scores, s.p, m.scores, nb, len, score_scale(hw), st));
+    FLINT_TRY(attn_softmax_backward(m.scores, s.p, m.scores, nb, len, hw, st));
     FLINT_TRY(attn_nn(m.dq, m.scores, s.k, nb, len, hw, len, st));
     FLINT_TRY(attn_tn(m.dk, m.scores, s.q, nb, len, hw, len, st));
     const void* const parts[] = {m.dq, m.dk, m.dv};

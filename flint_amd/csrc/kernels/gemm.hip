@@ -903,6 +903,11 @@ hipError_t launch_gemm_nt_batched(void* y, const void* x, const void* w, size_t 
     return run<Layout::kNT, Store::kScale>(op, batches, 0, stream);
 }
 
+bool gemm_batched_causal_taken(GemmLayout l, size_t m, size_t n, size_t k) {
+    const Epilogue e = l == GemmLayout::kNT ? Epilogue::kScale : Epilogue::kNone;
+    return gemm_pipe_eligible(l, e, m, n, k) && (l == GemmLayout::kNT ? m == n : m == k);
+}
+
 hipError_t launch_gemm_nn_batched(void* y, const void* x, const void* w, size_t batches,
                                   size_t m, size_t n, size_t k, hipStream_t stream, bool causal) {
     if (gemm_pipe_eligible(GemmLayout::kNN, Epilogue::kNone, m, n, k))

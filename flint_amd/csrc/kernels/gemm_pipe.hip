@@ -162,6 +162,8 @@ gemm_pipe(Operands op, TileArgs ta) {
     // resource builtins below exist on the device side only.
 #if defined(__HIP_DEVICE_COMPILE__)
     static_assert(BK == 32 || BK == 64, "k-step");
+    static_assert(kCausalZeroSpan % BM == 0 && kCausalZeroSpan % BK == 0,
+                  "causal tiles must stay inside the softmax's zero span");
     constexpr int NS = BK / 16;                 // k16 sub-steps per k-step
     constexpr int WAVES_N = pipe_waves_n(BN);
     constexpr int WTM = BM / (4 / WAVES_N), WTN = BN / WAVES_N;

@@ -63,6 +63,13 @@ hipError_t launch_gemm_nn_batched(void* y, const void* x, const void* w, size_t 
 hipError_t launch_gemm_tn_batched(void* y, const void* x, const void* w, size_t batches,
                                   size_t m, size_t n, size_t k, hipStream_t stream,
                                   bool causal = false);
+// Whether a causal batched GEMM of this layout and shape takes the causal path
+// (the pipeline, with the square operand); otherwise it computes everything.
+bool gemm_batched_causal_taken(GemmLayout l, size_t m, size_t n, size_t k);
+// Rows of a causal tile and the k-step both divide this: a causal softmax
+// writing its zeros up to the end of each such block covers what the causal
+// GEMMs read.
+constexpr int kCausalZeroSpan = 256;
 
 // Row reductions.
 constexpr size_t kLayerNormMaxCols = size_t{1} << 24;
@@ -94,10 +101,15 @@ hipError_t launch_bias_gradient(void* dbias, const void* dy, size_t rows, size_t
 // Merges per-chunk (sum, error) partials left in workspace into out (cols FP32).
 hipError_t launch_bias_gradient_finish(void* out, const void* workspace, size_t rows,
                                        size_t cols, bool accumulate, hipStream_t stream);
+// zero_span 0 writes every chunk of a row (the ABI functions); Z > 0 (a
+// multiple of 8) writes the masked zeros only up to the end of the Z-column
+// block holding the diagonal, for consumers that read no further (the model's
+// causal GEMMs, whose tiles are at most 256 rows and k-steps divide 256).
 hipError_t launch_causal_softmax_forward(void* p, const void* s, size_t rows, size_t length,
-                                         hipStream_t stream);
+                                         hipStream_t stream, int zero_span = 0);
 hipError_t launch_causal_softmax_backward(void* ds, const void* p, const void* dp, size_t rows,
-                                          size_t length, float scale, hipStream_t stream);
+                                          size_t length, float scale, hipStream_t stream,
+                                          int zero_span = 0);
 hipError_t launch_softmax_cross_entropy(void* dlogits, void* row_loss, const void* logits,
                                         const void* targets, float scale, size_t rows,
                                         size_t vocab, size_t cols, hipStream_t stream);

@@ -424,10 +424,20 @@ layernorm_backward_dx_any(float* __restrict__ dx, const _Float16* __restrict__ d
 
 constexpr int kSmRowsPerBlock = 4;
 
+// Chunks of row t written by the causal passes: all of them, or with a zero
+// span Z, those below the end of the Z-column block holding the diagonal (the
+// model's causal GEMMs read no further; the chunks past it keep old values).
+__device__ __forceinline__ int written_chunks(int t, int chunks, int zero_span) {
+    if (zero_span == 0) return chunks;
+    const int end = (t / zero_span + 1) * (zero_span >> 3);
+    return end < chunks ? end : chunks;
+}
+
 // One wave per row of length L <= 1024: lane l holds chunks l and l + 64.
 // Row t sees columns 0..t; masked chunks are written as zeros and never read.
 __global__ void __launch_bounds__(256)
-causal_softmax_forward(h8* __restrict__ p, const h8* __restrict__ s, size_t rows, int length) {
+causal_softmax_forward(h8* __restrict__ p, const h8* __restrict__ s, size_t rows, int length,
+                       int zero_span) {
     for (size_t row = size_t(blockIdx.x) * kSmRowsPerBlock + (threadIdx.x >> 6); row < rows;
          row += size_t(gridDim.x) * kSmRowsPerBlock) {
     const int lane = threadIdx.x & 63;
@@ -465,10 +475,11 @@ causal_softmax_forward(h8* __restrict__ p, const h8* __restrict__ s, size_t rows
     }
     sum = sum_reduce<64>(sum);
     const float inv = __fdiv_rn(1.0f, sum);
+    const int written = written_chunks(t, chunks, zero_span);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int c = lane + i * 64;
-        if (c < chunks) {
+        if (c < written) {
             if (c < visible_chunks) {
                 float o[8];
 #pragma unroll
@@ -488,7 +499,7 @@ causal_softmax_forward(h8* __restrict__ p, const h8* __restrict__ s, size_t rows
 // ds may alias dp.
 __global__ void __launch_bounds__(256)
 causal_softmax_backward(h8* ds, const h8* __restrict__ p, const h8* dp, size_t rows, int length,
-                        float scale) {
+                        float scale, int zero_span) {
     for (size_t row = size_t(blockIdx.x) * kSmRowsPerBlock + (threadIdx.x >> 6); row < rows;
          row += size_t(gridDim.x) * kSmRowsPerBlock) {
     const int lane = threadIdx.x & 63;
@@ -511,10 +522,11 @@ causal_softmax_backward(h8* ds, const h8* __restrict__ p, const h8* dp, size_t r
     }
     d = comp_reduce<64>(d);
     if (!__builtin_isfinite(d.sum)) d.error = 0.0f;
+    const int written = written_chunks(t, chunks, zero_span);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int c = lane + i * 64;
-        if (c < chunks) {
+        if (c < written) {
             if (c < visible_chunks) {
                 const int vis = min(t + 1 - c * 8, 8);
                 float o[8];
@@ -790,19 +802,23 @@ hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const 
 }
 
 hipError_t launch_causal_softmax_forward(void* p, const void* s, size_t rows, size_t length,
-                                         hipStream_t stream) {
+                                         hipStream_t stream, int zero_span) {
+    if (zero_span < 0 || zero_span % 8 != 0) return hipErrorInvalidValue;
     const unsigned blocks = unsigned(std::min<size_t>((rows + kSmRowsPerBlock - 1) / kSmRowsPerBlock, kMaxBlocks));
     hipLaunchKernelGGL(causal_softmax_forward, dim3(blocks), dim3(256), 0, stream,
-                       static_cast<h8*>(p), static_cast<const h8*>(s), rows, int(length));
+                       static_cast<h8*>(p), static_cast<const h8*>(s), rows, int(length),
+                       zero_span);
     return hipGetLastError();
 }
 
 hipError_t launch_causal_softmax_backward(void* ds, const void* p, const void* dp, size_t rows,
-                                          size_t length, float scale, hipStream_t stream) {
+                                          size_t length, float scale, hipStream_t stream,
+                                          int zero_span) {
+    if (zero_span < 0 || zero_span % 8 != 0) return hipErrorInvalidValue;
     const unsigned blocks = unsigned(std::min<size_t>((rows + kSmRowsPerBlock - 1) / kSmRowsPerBlock, kMaxBlocks));
     hipLaunchKernelGGL(causal_softmax_backward, dim3(blocks), dim3(256), 0, stream,
                        static_cast<h8*>(ds), static_cast<const h8*>(p),
-                       static_cast<const h8*>(dp), rows, int(length), scale);
+                       static_cast<const h8*>(dp), rows, int(length), scale, zero_span);
     return hipGetLastError();
 }
 
