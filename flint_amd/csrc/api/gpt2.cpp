@@ -409,6 +409,25 @@ flint_status attn_tn(void* y, const void* x, const void* w, size_t batches, size
     return FLINT_OK;
 }
 
+// q, k and v to (merge: from) their heads layouts in one launch: the moves of
+// three flint_heads_split / flint_heads_merge calls at first = 0, w, 2w.
+flint_status attn_heads3(void* qkv, void* const parts[3], size_t sequences, size_t length,
+                         size_t heads, size_t head_width, bool merge, flint_stream st) {
+    const size_t w = heads * head_width;
+    if (3 * sequences * length * (w / 8) >= (size_t{1} << 32)) {   // past 32-bit indexing
+        for (size_t i = 0; i < 3; ++i) {
+            FLINT_TRY(merge ? flint_heads_merge(qkv, parts[i], sequences, length, heads,
+                                                head_width, 3 * w, i * w, st)
+                            : flint_heads_split(parts[i], qkv, sequences, length, heads,
+                                                head_width, 3 * w, i * w, st));
+        }
+        return FLINT_OK;
+    }
+    FLINT_HIP_CHECK(flint::launch_heads3(qkv, parts, sequences, length, heads, head_width, merge,
+                                         flint::to_hip(st)));
+    return FLINT_OK;
+}
+
 // When the NN and TN products that read P and dS both take the causal path,
 // the softmax passes write the masked zeros only up to the end of the
 // 256-column block holding the diagonal: nothing reads past it.
@@ -452,10 +471,7 @@ flint_status forward_layer(const flint_gpt2& m, const Layer& L, flint_stream st)
     FLINT_TRY(layer_norm(m, L.ln_1, s.x_in, s.h1, s.mean1, s.rstd1, st));
     FLINT_TRY(flint_gemm_nt_bias(m.qkv, s.h1, L.attn.half, L.attn.b->data, rows, 3 * w, w, st));
     void* const qkv_parts[] = {s.q, s.k, s.v};
-    for (size_t i = 0; i < 3; ++i) {
-        FLINT_TRY(flint_heads_split(qkv_parts[i], m.qkv, c.sequences, c.length, c.heads, hw,
-                                    3 * w, i * w, st));
-    }
+    FLINT_TRY(attn_heads3(m.qkv, qkv_parts, c.sequences, c.length, c.heads, hw, false, st));
     FLINT_TRY(attn_nt(m.scores, s.q, s.k, m.head_batches, c.length, c.length, hw, score_scale(hw),
                       st));
     FLINT_TRY(attn_softmax_forward(s.p, m.scores, m.head_batches, c.length, hw, st));
@@ -516,11 +532,8 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
     FLINT_TRY(attn_softmax_backward(m.scores, s.p, m.scores, nb, len, hw, st));
     FLINT_TRY(attn_nn(m.dq, m.scores, s.k, nb, len, hw, len, st));
     FLINT_TRY(attn_tn(m.dk, m.scores, s.q, nb, len, hw, len, st));
-    const void* const parts[] = {m.dq, m.dk, m.dv};
-    for (size_t i = 0; i < 3; ++i) {
-        FLINT_TRY(flint_heads_merge(m.qkv, parts[i], c.sequences, len, c.heads, hw, 3 * w, i * w,
-                                    st));
-    }
+    void* const parts[] = {m.dq, m.dk, m.dv};
+    FLINT_TRY(attn_heads3(m.qkv, parts, c.sequences, len, c.heads, hw, true, st));
     FLINT_TRY(weight_grad(m, *L.attn.w, m.qkv, s.h1, acc, st));
     FLINT_TRY(bias_grad(m, *L.attn.b, m.qkv, acc, st));
     FLINT_TRY(flint_gemm_nn(m.dh, m.qkv, L.attn.half, rows, w, 3 * w, st));

@@ -131,6 +131,11 @@ hipError_t launch_fp32_to_fp16(void* y, const void* x, size_t count, hipStream_t
 hipError_t launch_heads(void* y, const void* x, size_t batches, size_t length, size_t heads,
                         size_t head_width, size_t row_width, size_t first, bool merge,
                         hipStream_t stream);
+// The three q / k / v parts of a [rows][3 * heads * head_width] matrix split
+// into (merge: from) three heads layouts in one launch (the model's attention);
+// hipErrorInvalidValue past 2^32 16-byte chunks.
+hipError_t launch_heads3(void* wide, void* const parts[3], size_t batches, size_t length,
+                         size_t heads, size_t head_width, bool merge, hipStream_t stream);
 hipError_t launch_embedding_forward(void* x, const void* tokens, const void* wte,
                                     const void* wpe, size_t rows, size_t length, size_t width,
                                     hipStream_t stream);

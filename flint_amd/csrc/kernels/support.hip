@@ -88,6 +88,32 @@ heads_move(h8* __restrict__ y, const h8* __restrict__ x, size_t rows, size_t len
     }
 }
 
+// The model's attention: the three parts (q, k, v) of a [rows][3 * width]
+// matrix to (split) or from (merge) three heads layouts in one pass, the same
+// moves as three heads_move calls with first = 0, width, 2 * width. Index
+// arithmetic is 32-bit (the caller checks that the element count fits).
+__global__ void __launch_bounds__(256)
+heads_move3(h8* wide, h8* p0, h8* p1, h8* p2, unsigned rows, unsigned length, unsigned heads,
+            unsigned head_chunks, int merge) {
+    const unsigned per_part = rows * heads * head_chunks;
+    const unsigned row_chunks = 3 * heads * head_chunks;
+    for (unsigned i = blockIdx.x * 256 + threadIdx.x; i < 3 * per_part; i += gridDim.x * 256) {
+        const unsigned part = i / per_part;
+        const unsigned j = i - part * per_part;
+        const unsigned c = j % head_chunks;
+        unsigned rest = j / head_chunks;
+        const unsigned t = rest % length;
+        rest /= length;
+        const unsigned h = rest % heads;
+        const unsigned b = rest / heads;
+        const size_t at = size_t(b * length + t) * row_chunks + part * heads * head_chunks +
+                          h * head_chunks + c;
+        h8* const p = part == 0 ? p0 : (part == 1 ? p1 : p2);
+        if (merge) wide[at] = p[j];
+        else p[j] = wide[at];
+    }
+}
+
 // ------------------------------------------------------------ embedding fwd
 
 // One wave per row: x[r] = wte[tokens[r]] + wpe[r % length], one FP32 add each.
@@ -385,6 +411,19 @@ hipError_t launch_heads(void* y, const void* x, size_t batches, size_t length, s
     hipLaunchKernelGGL(heads_move, dim3(grid_for(total, 256)), dim3(256), 0, stream,
                        static_cast<h8*>(y), static_cast<const h8*>(x), rows, length, int(heads),
                        int(head_width / 8), int(row_width / 8), int(first / 8), merge ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_heads3(void* wide, void* const parts[3], size_t batches, size_t length,
+                         size_t heads, size_t head_width, bool merge, hipStream_t stream) {
+    const size_t rows = batches * length;
+    const size_t total = 3 * rows * heads * (head_width / 8);
+    if (head_width % 8 != 0 || total >= (size_t{1} << 32)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(heads_move3, dim3(grid_for(total, 256)), dim3(256), 0, stream,
+                       static_cast<h8*>(wide), static_cast<h8*>(parts[0]),
+                       static_cast<h8*>(parts[1]), static_cast<h8*>(parts[2]), unsigned(rows),
+                       unsigned(length), unsigned(heads), unsigned(head_width / 8),
+                       merge ? 1 : 0);
     return hipGetLastError();
 }
 
