@@ -498,10 +498,29 @@ flint_status bias_grad(const flint_gpt2& m, const Param& p, const void* dy, int 
     return flint_bias_gradient(p.grad, dy, m.rows, p.cols, acc, m.work, m.work_bytes, st);
 }
 
+// LayerNorm backward: dbeta and dgamma from one pass over dy and x (the
+// model's workspace holds both partial regions), bit-identical to
+// flint_layernorm_backward's separate passes, which FLINT_FUSED_SUMS=0 runs
+// instead (the tests compare the two), then dx.
+bool fused_sums() {
+    const char* e = std::getenv("FLINT_FUSED_SUMS");
+    return e == nullptr || !(e[0] == '0' && e[1] == '\0');
+}
+
 flint_status norm_backward(const flint_gpt2& m, const Norm& n, const void* x, const void* mean,
                            const void* rstd, int acc_dx, int acc, flint_stream st) {
-    return flint_layernorm_backward(m.dres, n.w->grad, n.b->grad, m.dh, x, mean, rstd, n.w->data,
-                                    m.rows, m.cfg.width, acc_dx, acc, m.work, m.work_bytes, st);
+    if (!fused_sums()) {
+        return flint_layernorm_backward(m.dres, n.w->grad, n.b->grad, m.dh, x, mean, rstd,
+                                        n.w->data, m.rows, m.cfg.width, acc_dx, acc, m.work,
+                                        m.work_bytes, st);
+    }
+    FLINT_HIP_CHECK(flint::launch_layernorm_param_grads(n.b->grad, n.w->grad, m.dh, x, mean, rstd,
+                                                        m.rows, m.cfg.width, acc != 0, m.work,
+                                                        m.work_bytes, flint::to_hip(st)));
+    FLINT_HIP_CHECK(flint::launch_layernorm_backward_dx(m.dres, m.dh, x, mean, rstd, n.w->data,
+                                                        m.rows, m.cfg.width, acc_dx != 0,
+                                                        flint::to_hip(st)));
+    return FLINT_OK;
 }
 
 // One layer backward, MLP then attention; dres holds the gradient of the

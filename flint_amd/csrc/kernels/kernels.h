@@ -105,6 +105,17 @@ hipError_t launch_bias_gradient_finish(void* out, const void* workspace, size_t 
 // multiple of 8) writes the masked zeros only up to the end of the Z-column
 // block holding the diagonal, for consumers that read no further (the model's
 // causal GEMMs, whose tiles are at most 256 rows and k-steps divide 256).
+// LayerNorm's dbeta and dgamma in two launches (one pass over dy and x for
+// both sets of chunk partials, one finish for both), bit-identical to
+// flint_layernorm_backward's four; workspace holds both partial regions
+// (2 x chunks x 2 x cols floats).
+hipError_t launch_layernorm_param_grads(void* dbeta, void* dgamma, const void* dy, const void* x,
+                                        const void* mean, const void* rstd, size_t rows,
+                                        size_t cols, bool accumulate, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream);
+hipError_t launch_layernorm_backward_dx(void* dx, const void* dy, const void* x, const void* mean,
+                                       const void* rstd, const void* gamma, size_t rows,
+                                       size_t cols, bool accumulate_dx, hipStream_t stream);
 hipError_t launch_causal_softmax_forward(void* p, const void* s, size_t rows, size_t length,
                                          hipStream_t stream, int zero_span = 0);
 hipError_t launch_causal_softmax_backward(void* ds, const void* p, const void* dp, size_t rows,

@@ -258,13 +258,8 @@ __device__ __forceinline__ float comp_value(const Comp& a) {
 // Merges chunk partials per column: each 32-lane half-wave owns 4 columns.
 // Lane l merges chunks l, l + 32, ... in order, then a butterfly over the 32
 // lanes (xor 16, 8, 4, 2, 1) merges those.
-__global__ void __launch_bounds__(256)
-column_finish(float* __restrict__ out, const float* __restrict__ partial, size_t chunks,
-              int cols, int accumulate) {
-    const int quad = blockIdx.x * 8 + (threadIdx.x >> 5);
-    const int quads = cols / 4;
-    if (quad >= quads) return;   // whole half-waves leave together
-    const int lane = threadIdx.x & 31;
+__device__ __forceinline__ void finish_quad(float* out, const float* partial, size_t chunks,
+                                            int cols, int accumulate, int quad, int lane) {
     Comp t[4];
     for (size_t c = lane; c < chunks; c += 32) {
         const f4 s = reinterpret_cast<const f4*>(partial + c * 2 * cols)[quad];
@@ -283,6 +278,89 @@ column_finish(float* __restrict__ out, const float* __restrict__ partial, size_t
                add_rn(old[3], r[3])};
     }
     *o = r;
+}
+
+__global__ void __launch_bounds__(256)
+column_finish(float* __restrict__ out, const float* __restrict__ partial, size_t chunks,
+              int cols, int accumulate) {
+    const int quad = blockIdx.x * 8 + (threadIdx.x >> 5);
+    if (quad >= cols / 4) return;   // whole half-waves leave together
+    finish_quad(out, partial, chunks, cols, accumulate, quad, threadIdx.x & 31);
+}
+
+// LayerNorm's dbeta and dgamma partials in one pass over dy and x (the model's
+// own workspace holds both regions): per 256-row chunk and column, exactly the
+// sums of column_partials<false, 1> and column_partials<true, 1>, in their
+// order, into part0 and part1. column_finish2 then merges both.
+__global__ void __launch_bounds__(kPhases * 64)
+column_partials2(float* part0, float* part1, const _Float16* __restrict__ dy,
+                 const float* __restrict__ x, const float* __restrict__ mean,
+                 const float* __restrict__ rstd, size_t rows, int cols, size_t chunks,
+                 size_t blocks) {
+    constexpr int kPer = kChunkRows / kPhases;
+    __shared__ float sums[2][kPhases - 1][64];
+    __shared__ float errs[2][kPhases - 1][64];
+    const int lane = threadIdx.x & 63;
+    const int ph = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    for (size_t b = blockIdx.x; b < blocks; b += gridDim.x) {
+        const int tile = int(b / chunks);
+        const size_t chunk = b - size_t(tile) * chunks;
+        const size_t first = chunk * kChunkRows;
+        const int count = rows - first < size_t(kChunkRows) ? int(rows - first) : kChunkRows;
+        const int n = count > ph ? (count - ph + kPhases - 1) / kPhases : 0;
+        const int col = tile * 64 + lane;
+        const bool live = col < cols;
+        const size_t step = size_t(kPhases) * size_t(cols);
+        size_t at = (first + ph) * size_t(cols) + col;
+        _Float16 d[kPer];
+        float xv[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const size_t use = k < n && live ? at : 0;
+            d[k] = dy[use];
+            xv[k] = x[use];
+            at += step;
+        }
+        Comp acc[2];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            if (k < n) {
+                const size_t r = first + ph + size_t(k) * kPhases;
+                comp_add(acc[0], float(d[k]));
+                comp_add_product(acc[1], float(d[k]), mul_rn(sub_rn(xv[k], mean[r]), rstd[r]));
+            }
+        }
+        if (ph > 0) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                sums[u][ph - 1][lane] = acc[u].sum;
+                errs[u][ph - 1][lane] = acc[u].error;
+            }
+        }
+        __syncthreads();
+        if (ph == 0 && live) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+#pragma unroll
+                for (int o = 0; o < kPhases - 1; ++o)
+                    comp_merge(acc[u], sums[u][o][lane], errs[u][o][lane]);
+                float* part = u == 0 ? part0 : part1;
+                part[chunk * 2 * cols + col] = acc[u].sum;
+                part[(chunk * 2 + 1) * cols + col] = acc[u].error;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// column_finish for two outputs at once (dbeta from part0, dgamma from part1).
+__global__ void __launch_bounds__(256)
+column_finish2(float* out0, float* out1, const float* part0, const float* part1, size_t chunks,
+               int cols, int accumulate) {
+    const int quad = blockIdx.x * 8 + (threadIdx.x >> 5);
+    if (quad >= cols / 4) return;   // whole half-waves leave together
+    finish_quad(out0, part0, chunks, cols, accumulate, quad, threadIdx.x & 31);
+    finish_quad(out1, part1, chunks, cols, accumulate, quad, threadIdx.x & 31);
 }
 
 hipError_t launch_partials(bool dgamma, float* partial, const void* dy, const void* x,
@@ -755,6 +833,27 @@ hipError_t launch_bias_gradient(void* dbias, const void* dy, size_t rows, size_t
     return launch_bias_gradient_finish(dbias, workspace, rows, cols, accumulate, stream);
 }
 
+hipError_t launch_layernorm_param_grads(void* dbeta, void* dgamma, const void* dy, const void* x,
+                                        const void* mean, const void* rstd, size_t rows,
+                                        size_t cols, bool accumulate, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream) {
+    const size_t chunks = (rows + kChunkRows - 1) / kChunkRows;
+    const size_t region = chunks * 2 * cols;   // floats
+    if (cols % 8 != 0 || 2 * region * sizeof(float) > workspace_bytes) return hipErrorInvalidValue;
+    auto* part0 = static_cast<float*>(workspace);
+    auto* part1 = part0 + region;
+    const size_t blocks = chunks * ((cols + 63) / 64);
+    hipLaunchKernelGGL(column_partials2, dim3(unsigned(std::min<size_t>(blocks, kMaxBlocks))),
+                       dim3(kPhases * 64), 0, stream, part0, part1,
+                       static_cast<const _Float16*>(dy), static_cast<const float*>(x),
+                       static_cast<const float*>(mean), static_cast<const float*>(rstd), rows,
+                       int(cols), chunks, blocks);
+    hipLaunchKernelGGL(column_finish2, dim3(unsigned((cols / 4 + 7) / 8)), dim3(256), 0, stream,
+                       static_cast<float*>(dbeta), static_cast<float*>(dgamma), part0, part1,
+                       chunks, int(cols), accumulate ? 1 : 0);
+    return hipGetLastError();
+}
+
 hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const void* dy,
                                      const void* x, const void* mean, const void* rstd,
                                      const void* gamma, size_t rows, size_t cols,
@@ -776,6 +875,13 @@ hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const 
         e != hipSuccess) {
         return e;
     }
+    return launch_layernorm_backward_dx(dx, dy, x, mean, rstd, gamma, rows, cols, accumulate_dx,
+                                        stream);
+}
+
+hipError_t launch_layernorm_backward_dx(void* dx, const void* dy, const void* x, const void* mean,
+                                       const void* rstd, const void* gamma, size_t rows,
+                                       size_t cols, bool accumulate_dx, hipStream_t stream) {
     const unsigned blocks = unsigned(std::min<size_t>((rows + 7) / 8, kMaxBlocks));
     auto* dxf = static_cast<float*>(dx);
     const auto* dyh = static_cast<const _Float16*>(dy);

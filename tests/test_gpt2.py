@@ -176,6 +176,28 @@ def test_causal_attention_products_change_no_bits(flint, cuda, monkeypatch, leng
     assert bool(torch.isfinite(full[1]).all())
 
 
+WIDE = dict(layers=1, heads=4, width=256, block_size=1024, vocab=1000, padded_vocab=1024)
+
+
+@pytest.mark.parametrize("cfg,sequences,length", [(TINY, 8, 64), (ODD, 2, 48), (WIDE, 2, 520)],
+                         ids=["tiny-8x64", "odd-2x48", "wide-2x520"])
+def test_fused_column_sums_change_no_bits(flint, cuda, monkeypatch, cfg, sequences, length):
+    """The model's LayerNorm dbeta and dgamma come from one partials pass and
+    one finish (FLINT_FUSED_SUMS unset); flint_layernorm_backward's separate
+    passes (=0) must give the same bits."""
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=13, trained=True)
+    idx, tgt = _tokens(cfg, sequences, length, 14)
+    monkeypatch.setenv("FLINT_FUSED_SUMS", "0")
+    plain = _run(flint, cfg, sequences, length, params, idx, tgt, 0.5)
+    monkeypatch.delenv("FLINT_FUSED_SUMS")
+    fused = _run(flint, cfg, sequences, length, params, idx, tgt, 0.5)
+    for n in plain[3]:
+        assert torch.equal(plain[3][n].view(torch.int32), fused[3][n].view(torch.int32)), n
+    assert plain[4] == fused[4]
+
+
 def test_backward_accumulate_adds_one_pass(flint, cuda):
     """accumulate: every gradient gets this pass's added with one FP32 add, wte
     with two (old + output layer's part) + the embedding's part, so only wte may
