@@ -4,23 +4,27 @@
 // gemm.hip's kernels.
 //
 // Why this shape of kernel (measured on MI355X):
-//  * A CU pulls about 110 GB/s (~45 B/clk) from L2 through the vector memory
-//    path, with direct-to-LDS or register loads alike. Feeding 4,096 FLOP/clk
-//    needs at least ~90 FLOP per loaded byte, i.e. a 256 x 192 (110 FLOP/B) or
-//    256 x 256 (128 FLOP/B) macro-tile. A workgroup of 4 waves then holds
-//    128 x 96 or 128 x 128 accumulators per wave (192 / 256 AGPRs), so one
-//    wave runs per SIMD and overlap has to come from the instruction stream,
-//    not from other waves.
-//  * The k-loop takes k-steps of 32 through S LDS stages. The loads of step
-//    g + S - 1 are issued half during the first and half during the second k16
-//    sub-step of the steps before it, one buffer_load ... lds after every
-//    second MFMA (every MFMA for 64-wide tiles), and the fragment reads of the next sub-step one after every
-//    MFMA: no burst of loads stalls the wave, and S - 1 steps of latency are
-//    covered. One barrier per step sits between the two sub-steps, after the
-//    last fragment read of the step.
+//  * A CU's L2 -> LDS rate depends on the row piece one load covers: 64-byte
+//    pieces of a row (k-steps of 32 FP16) stream at ~64 GB/s per CU, 128-byte
+//    pieces (k-steps of 64) at ~124 GB/s. Row-major operands therefore take
+//    k-steps of 64 wherever the tile's stages fit in LDS (k-major operands
+//    are whole lines either way).
+//  * Tiles of 128 x 192 to 256 x 256 load few bytes per FLOP; a workgroup of
+//    4 waves then holds 64 x 96 to 128 x 128 accumulators per wave (96 to
+//    256 AGPRs), so one wave runs per SIMD and overlap has to come from the
+//    instruction stream, not from other waves.
+//  * The k-loop takes k-steps of BK (32 or 64) through S LDS stages, each
+//    step BK / 16 MFMA sub-steps. The loads of step g + S - 1 are spread over
+//    the sub-steps of the steps before it, one buffer_load ... lds after every
+//    second MFMA (every MFMA where a sub-step has few MFMAs), and the fragment
+//    reads of the next sub-step one after every MFMA: no burst of loads stalls
+//    the wave, and about S - 1 steps of latency are covered. One barrier per
+//    step sits before its last sub-step, after the step's last fragment read
+//    of its own stage. With two stages (256-row tiles at k-steps of 64) a
+//    step's loads all go out right after the barrier that frees their stage.
 //  * Operands whose rows run along k (NT's x and w, NN's x) sit in LDS as
-//    [rows][32 k]. Operands stored k-major (NN's and TN's w, TN's x) are
-//    loaded as they lie, [32 k][rows], and their MFMA fragments come from
+//    [rows][BK k]. Operands stored k-major (NN's and TN's w, TN's x) are
+//    loaded as they lie, [BK k][rows], and their MFMA fragments come from
 //    ds_read_b64_tr_b16: within 16 lanes, lane j addresses 4 halves of row
 //    k0 + j / 4 at column c0 + 4 (j % 4), and lane i receives column c0 + i of
 //    rows k0 .. k0 + 3, so two such reads give a lane its 8 consecutive k.
@@ -29,16 +33,21 @@
 //  * Workgroups are persistent and walk their tiles as one stream of k-steps,
 //    so the next tile's first steps load under this tile's epilogue.
 //  * The epilogue stages each wave's accumulators through LDS, 32 rows (FP16
-//    outputs) or 16 rows (FP32 values) at a time, so that every global store
-//    instruction writes whole rows: 64 lanes x 16 B. Stores straight from the
-//    MFMA layout cover 32 rows x 16 B each and ran the output at under 2 TB/s.
-//    They are buffer stores: a chunk outside the output gets an offset past
-//    the resource's end and is dropped, so every wave issues the same count,
-//    which the k-loop's waits rely on to let them drain under the next tile.
+//    outputs) or 16 rows (FP32 values) at a time (half that where the stages
+//    leave too little LDS), so that every global store instruction writes
+//    whole row pieces: 64 lanes x 16 B. Stores straight from the MFMA layout
+//    cover 32 rows x 16 B each and ran the output at under 2 TB/s. They are
+//    non-temporal buffer stores: a chunk outside the output gets an offset
+//    past the resource's end and is dropped, so every wave issues the same
+//    count, which the k-loop's waits rely on to let them drain under the next
+//    tile.
 //  * Edge tiles need no separate path: loads past an operand's end read zeros
 //    (or, for a k-major operand's last columns, the next row's first values),
 //    a row of either operand only ever meets its own output row or column, and
 //    the stores are masked.
+//  * Causal attention (the GPT-2 model's batched products): NT computes only
+//    the output tiles at or below the diagonal; NN and TN cut each tile's
+//    k-range to where the square operand can be nonzero.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
