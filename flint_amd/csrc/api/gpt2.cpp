@@ -507,19 +507,22 @@ bool fused_sums() {
     return e == nullptr || !(e[0] == '0' && e[1] == '\0');
 }
 
+// On return dres holds the residual stream's gradient and dres_half its FP16
+// copy (written by the dx kernel, or converted after the ABI path).
 flint_status norm_backward(const flint_gpt2& m, const Norm& n, const void* x, const void* mean,
                            const void* rstd, int acc_dx, int acc, flint_stream st) {
     if (!fused_sums()) {
-        return flint_layernorm_backward(m.dres, n.w->grad, n.b->grad, m.dh, x, mean, rstd,
-                                        n.w->data, m.rows, m.cfg.width, acc_dx, acc, m.work,
-                                        m.work_bytes, st);
+        FLINT_TRY(flint_layernorm_backward(m.dres, n.w->grad, n.b->grad, m.dh, x, mean, rstd,
+                                           n.w->data, m.rows, m.cfg.width, acc_dx, acc, m.work,
+                                           m.work_bytes, st));
+        return flint_fp32_to_fp16(m.dres_half, m.dres, m.rows * m.cfg.width, st);
     }
     FLINT_HIP_CHECK(flint::launch_layernorm_param_grads(n.b->grad, n.w->grad, m.dh, x, mean, rstd,
                                                         m.rows, m.cfg.width, acc != 0, m.work,
                                                         m.work_bytes, flint::to_hip(st)));
     FLINT_HIP_CHECK(flint::launch_layernorm_backward_dx(m.dres, m.dh, x, mean, rstd, n.w->data,
                                                         m.rows, m.cfg.width, acc_dx != 0,
-                                                        flint::to_hip(st)));
+                                                        flint::to_hip(st), m.dres_half));
     return FLINT_OK;
 }
 
@@ -532,7 +535,8 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
     const size_t rows = m.rows, w = c.width, hw = m.head_width;
     const size_t nb = m.head_batches, len = c.length;
 
-    FLINT_TRY(flint_fp32_to_fp16(m.dres_half, m.dres, rows * w, st));
+    // dres_half = RN16(dres): written by the LayerNorm backward that produced
+    // dres (norm_backward), in place of the reference's conversion here.
     FLINT_TRY(weight_grad(m, *L.fc_proj.w, m.dres_half, s.gelu, acc, st));
     FLINT_TRY(bias_grad(m, *L.fc_proj.b, m.dres_half, acc, st));
     FLINT_TRY(flint_gemm_nn_dgelu(m.dpre, m.dres_half, L.fc_proj.half, s.pre, rows, 4 * w, w, st));
@@ -541,7 +545,6 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
     FLINT_TRY(flint_gemm_nn(m.dh, m.dpre, L.fc.half, rows, w, 4 * w, st));
     FLINT_TRY(norm_backward(m, L.ln_2, s.x_mid, s.mean2, s.rstd2, 1, acc, st));
 
-    FLINT_TRY(flint_fp32_to_fp16(m.dres_half, m.dres, rows * w, st));
     FLINT_TRY(weight_grad(m, *L.attn_proj.w, m.dres_half, s.attn_out, acc, st));
     FLINT_TRY(bias_grad(m, *L.attn_proj.b, m.dres_half, acc, st));
     FLINT_TRY(flint_gemm_nn(m.dh, m.dres_half, L.attn_proj.half, rows, w, w, st));

@@ -113,9 +113,12 @@ hipError_t launch_layernorm_param_grads(void* dbeta, void* dgamma, const void* d
                                         const void* mean, const void* rstd, size_t rows,
                                         size_t cols, bool accumulate, void* workspace,
                                         size_t workspace_bytes, hipStream_t stream);
+// LayerNorm dx alone; with dx_half, also RN16 of every dx value written (the
+// values flint_fp32_to_fp16 of dx would give).
 hipError_t launch_layernorm_backward_dx(void* dx, const void* dy, const void* x, const void* mean,
                                        const void* rstd, const void* gamma, size_t rows,
-                                       size_t cols, bool accumulate_dx, hipStream_t stream);
+                                       size_t cols, bool accumulate_dx, hipStream_t stream,
+                                       void* dx_half = nullptr);
 hipError_t launch_causal_softmax_forward(void* p, const void* s, size_t rows, size_t length,
                                          hipStream_t stream, int zero_span = 0);
 hipError_t launch_causal_softmax_backward(void* ds, const void* p, const void* dp, size_t rows,

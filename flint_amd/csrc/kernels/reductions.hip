@@ -396,13 +396,14 @@ hipError_t launch_partials(bool dgamma, float* partial, const void* dy, const vo
 // One 32-lane half-wave per row: lane l takes pieces l, l + 32, ... (up to PPL
 // of them, 8 columns each), adds g = dy gamma and g xhat over them in order
 // with plain FP32 adds, and a 32-lane butterfly totals them. The second pass
-// reuses the registers.
+// reuses the registers. With dx_half, RN16 of every dx value written goes
+// there too (the model's FP16 copy of the residual gradient).
 template <int PPL>
 __global__ void __launch_bounds__(256)
 layernorm_backward_dx(float* __restrict__ dx, const _Float16* __restrict__ dy,
                       const float* __restrict__ x, const float* __restrict__ mean,
                       const float* __restrict__ rstd, const float* __restrict__ gamma,
-                      size_t rows, int cols, int accumulate) {
+                      size_t rows, int cols, int accumulate, _Float16* __restrict__ dx_half) {
     for (size_t row = size_t(blockIdx.x) * 8 + (threadIdx.x >> 5); row < rows;
          row += size_t(gridDim.x) * 8) {
     const int lane = threadIdx.x & 31;
@@ -453,6 +454,12 @@ layernorm_backward_dx(float* __restrict__ dx, const _Float16* __restrict__ dy,
             }
             dp[0] = f4{o[0], o[1], o[2], o[3]};
             dp[1] = f4{o[4], o[5], o[6], o[7]};
+            if (dx_half != nullptr) {
+                h8 hv;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) hv[j] = _Float16(o[j]);
+                *reinterpret_cast<h8*>(dx_half + row * cols + p * 8) = hv;
+            }
         }
     }
     }
@@ -463,7 +470,7 @@ __global__ void __launch_bounds__(256)
 layernorm_backward_dx_any(float* __restrict__ dx, const _Float16* __restrict__ dy,
                           const float* __restrict__ x, const float* __restrict__ mean,
                           const float* __restrict__ rstd, const float* __restrict__ gamma,
-                          size_t rows, int cols, int accumulate) {
+                          size_t rows, int cols, int accumulate, _Float16* __restrict__ dx_half) {
     for (size_t row = size_t(blockIdx.x) * 8 + (threadIdx.x >> 5); row < rows;
          row += size_t(gridDim.x) * 8) {
     const int lane = threadIdx.x & 31;
@@ -493,6 +500,7 @@ layernorm_backward_dx_any(float* __restrict__ dx, const _Float16* __restrict__ d
             float v = mul_rn(rs, sub_rn(sub_rn(gv, g_mean), mul_rn(xh, gx_mean)));
             if (accumulate) v = add_rn(o[c], v);
             o[c] = v;
+            if (dx_half != nullptr) dx_half[row * cols + c] = _Float16(v);
         }
     }
     }
@@ -881,7 +889,8 @@ hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const 
 
 hipError_t launch_layernorm_backward_dx(void* dx, const void* dy, const void* x, const void* mean,
                                        const void* rstd, const void* gamma, size_t rows,
-                                       size_t cols, bool accumulate_dx, hipStream_t stream) {
+                                       size_t cols, bool accumulate_dx, hipStream_t stream,
+                                       void* dx_half) {
     const unsigned blocks = unsigned(std::min<size_t>((rows + 7) / 8, kMaxBlocks));
     auto* dxf = static_cast<float*>(dx);
     const auto* dyh = static_cast<const _Float16*>(dy);
@@ -891,10 +900,11 @@ hipError_t launch_layernorm_backward_dx(void* dx, const void* dy, const void* x,
     const auto* gf = static_cast<const float*>(gamma);
     const int c = int(cols);
     const int acc = accumulate_dx ? 1 : 0;
+    auto* dxh = static_cast<_Float16*>(dx_half);
     const size_t pieces = cols / 8;
 #define FLINT_DX(PPL)                                                                        \
     hipLaunchKernelGGL(layernorm_backward_dx<PPL>, dim3(blocks), dim3(256), 0, stream, dxf, dyh, \
-                       xf, mf, rf, gf, rows, c, acc)
+                       xf, mf, rf, gf, rows, c, acc, dxh)
     if (pieces <= 32) FLINT_DX(1);
     else if (pieces <= 64) FLINT_DX(2);
     else if (pieces <= 96) FLINT_DX(3);
@@ -902,7 +912,7 @@ hipError_t launch_layernorm_backward_dx(void* dx, const void* dy, const void* x,
     else if (pieces <= 256) FLINT_DX(8);
     else
         hipLaunchKernelGGL(layernorm_backward_dx_any, dim3(blocks), dim3(256), 0, stream, dxf,
-                           dyh, xf, mf, rf, gf, rows, c, acc);
+                           dyh, xf, mf, rf, gf, rows, c, acc, dxh);
 #undef FLINT_DX
     return hipGetLastError();
 }
