@@ -508,7 +508,8 @@ layernorm_backward_dx_any(float* __restrict__ dx, const _Float16* __restrict__ d
 
 // ------------------------------------------------------------ causal softmax
 
-constexpr int kSmRowsPerBlock = 4;
+constexpr int kSmRowsPerBlock = 4;   // waves per workgroup, one row group each
+constexpr int kSmRowsPerWave = 2;
 
 // Chunks of row t written by the causal passes: all of them, or with a zero
 // span Z, those below the end of the Z-column block holding the diagonal (the
@@ -521,16 +522,35 @@ __device__ __forceinline__ int written_chunks(int t, int chunks, int zero_span) 
 
 // One wave per row of length L <= 1024: lane l holds chunks l and l + 64.
 // Row t sees columns 0..t; masked chunks are written as zeros and never read.
+// A wave takes R consecutive rows and loads all of them before the first
+// reduction, so R times the bytes are in flight; each row's arithmetic is
+// the one-row order.
+template <int R>
 __global__ void __launch_bounds__(256)
 causal_softmax_forward(h8* __restrict__ p, const h8* __restrict__ s, size_t rows, int length,
                        int zero_span) {
-    for (size_t row = size_t(blockIdx.x) * kSmRowsPerBlock + (threadIdx.x >> 6); row < rows;
-         row += size_t(gridDim.x) * kSmRowsPerBlock) {
+    for (size_t row0 = (size_t(blockIdx.x) * kSmRowsPerBlock + (threadIdx.x >> 6)) * R;
+         row0 < rows; row0 += size_t(gridDim.x) * kSmRowsPerBlock * R) {
     const int lane = threadIdx.x & 63;
     const int chunks = length >> 3;
+    h8 raw[R][2];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const size_t row = row0 + r;
+        const int t = int(row % size_t(length));
+        const int visible_chunks = row < rows ? (t >> 3) + 1 : 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = lane + i * 64;
+            if (c < visible_chunks) raw[r][i] = s[row * chunks + c];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+    const size_t row = row0 + r;
+    if (row >= rows) break;
     const int t = int(row % size_t(length));
     const int visible_chunks = (t >> 3) + 1;
-    const h8* sr = s + row * chunks;
     h8* pr = p + row * chunks;
     float v[2][8];
     float mx = -__builtin_huge_valf();
@@ -538,7 +558,7 @@ causal_softmax_forward(h8* __restrict__ p, const h8* __restrict__ s, size_t rows
     for (int i = 0; i < 2; ++i) {
         const int c = lane + i * 64;
         if (c < visible_chunks) {
-            unpack8(sr[c], v[i]);
+            unpack8(raw[r][i], v[i]);
             const int vis = min(t + 1 - c * 8, 8);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
@@ -575,6 +595,7 @@ causal_softmax_forward(h8* __restrict__ p, const h8* __restrict__ s, size_t rows
                 pr[c] = h8{};
             }
         }
+    }
     }
     }
 }
@@ -920,8 +941,10 @@ hipError_t launch_layernorm_backward_dx(void* dx, const void* dy, const void* x,
 hipError_t launch_causal_softmax_forward(void* p, const void* s, size_t rows, size_t length,
                                          hipStream_t stream, int zero_span) {
     if (zero_span < 0 || zero_span % 8 != 0) return hipErrorInvalidValue;
-    const unsigned blocks = unsigned(std::min<size_t>((rows + kSmRowsPerBlock - 1) / kSmRowsPerBlock, kMaxBlocks));
-    hipLaunchKernelGGL(causal_softmax_forward, dim3(blocks), dim3(256), 0, stream,
+    constexpr size_t kRowsPerBlock = size_t(kSmRowsPerBlock) * kSmRowsPerWave;
+    const unsigned blocks =
+        unsigned(std::min<size_t>((rows + kRowsPerBlock - 1) / kRowsPerBlock, kMaxBlocks));
+    hipLaunchKernelGGL(causal_softmax_forward<kSmRowsPerWave>, dim3(blocks), dim3(256), 0, stream,
                        static_cast<h8*>(p), static_cast<const h8*>(s), rows, int(length),
                        zero_span);
     return hipGetLastError();
