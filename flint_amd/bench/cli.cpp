@@ -168,7 +168,18 @@ bool standard_protocol(const Options& o) {
 
 Command parse(int argc, char** argv) {
     Command c;
-    for (int i = 1; i < argc; ++i) c.args.push_back(argv[i]);
+    std::vector<std::string> all;
+    for (int i = 1; i < argc; ++i) all.push_back(argv[i]);
+    // The log records the arguments without --out and its path, so that no
+    // local path reaches it.
+    for (size_t i = 0; i < all.size(); ++i) {
+        if (all[i] == "--out") {
+            ++i;
+            continue;
+        }
+        if (all[i].rfind("--out=", 0) == 0) continue;
+        c.args.push_back(all[i]);
+    }
 
     // Options as given; their meaning is settled once the benchmark is known.
     std::map<std::string, std::string> given;
@@ -177,8 +188,8 @@ Command parse(int argc, char** argv) {
     static const char* kValued[] = {"--sizes", "--chains", "--layout", "--epilogue", "--lt-algo", "--shapes",
                                     "--rounds", "--max-rounds", "--warmup", "--sample-ms", "--out"};
     static const char* kFlags[] = {"--allow-busy", "--quick", "--help"};
-    for (size_t i = 0; i < c.args.size(); ++i) {
-        const std::string& arg = c.args[i];
+    for (size_t i = 0; i < all.size(); ++i) {
+        const std::string& arg = all[i];
         if (arg.rfind("--", 0) != 0) {
             if (have_benchmark) fail("unexpected argument: " + arg);
             benchmark = arg;
@@ -200,8 +211,8 @@ Command parse(int argc, char** argv) {
         if (eq != std::string::npos) {
             value = arg.substr(eq + 1);
         } else {
-            if (i + 1 >= c.args.size()) fail(name + " needs a value");
-            value = c.args[++i];
+            if (i + 1 >= all.size()) fail(name + " needs a value");
+            value = all[++i];
         }
         given[name] = value;
     }

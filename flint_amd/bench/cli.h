@@ -44,7 +44,7 @@ struct Command {
     std::vector<Shape> shapes;               // gemm
     Options options;
     std::string out;                         // empty: the default path
-    std::vector<std::string> args;           // argv[1:], as given
+    std::vector<std::string> args;           // argv[1:] without --out and its path
 };
 
 // Parses argv; throws UsageError. A command with help set runs nothing.

@@ -105,8 +105,10 @@ DeviceInfo device_info() {
     hipDeviceProp_t p;
     hip_check(hipGetDeviceProperties(&p, 0), "hipGetDeviceProperties");
     DeviceInfo d;
-    d.name = p.name;
     d.arch = p.gcnArchName;
+    // The marketing name comes from the driver's ID table, which a box may
+    // lack; the architecture then names the device.
+    d.name = p.name[0] ? std::string(p.name) : "AMD " + d.arch.substr(0, d.arch.find(':'));
     d.compute_capability = std::to_string(p.major) + "." + std::to_string(p.minor);
     d.cu_count = p.multiProcessorCount;
     d.rated_clock_mhz = p.clockRate / 1000.0;
