@@ -31,6 +31,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <ctime>
 #include <filesystem>
@@ -968,8 +969,12 @@ std::string utc_now(const char* format) {
 std::string report(const Command& c, const DeviceInfo& d, const std::vector<CaseResult>& cases) {
     // The repository root is three levels above build/release/bin.
     const std::string root = (exe_dir() / ".." / ".." / "..").lexically_normal().string();
-    const std::string sha = run_text("git -C '" + root + "' rev-parse HEAD 2>/dev/null");
+    std::string sha = run_text("git -C '" + root + "' rev-parse HEAD 2>/dev/null");
     const std::string dirty = sha.empty() ? "" : run_text("git -C '" + root + "' status --porcelain 2>/dev/null");
+    // A copy of the tree without its .git (a build shipped to another machine)
+    // can name its commit through FLINT_GIT_SHA; it is then taken as clean.
+    const char* env_sha = std::getenv("FLINT_GIT_SHA");
+    if (sha.empty() && env_sha && *env_sha) sha = env_sha;
     Json j;
     j.open('{');
     j.str("schema", "flint-bench/1");
