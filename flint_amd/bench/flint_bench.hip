@@ -19,9 +19,12 @@
 // so no launch finds its operands cached. Times are hipEvent pairs around a
 // batch of launches on one stream. The ratio is baseline time / Flint time.
 //
-// This build has no clock or power monitor: per-sample stats, clock-adjusted
-// fractions and the idle-GPU check of the reference are reported as null, and a
-// round is discarded only for a sample shorter than 0.9 x sample_ms.
+// monitor.h samples clocks, power, temperature and throttling through amd-smi:
+// each timed sample carries the statistics of the window it ran in, a round is
+// discarded when another process appeared on the GPU or a sample fell short of
+// 0.9 x sample_ms, and the compute fraction is also given at the window's mean
+// clock. Without amd-smi access those statistics are null. A run refuses to
+// start while other processes hold the GPU, unless --allow-busy.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 #include <hipblaslt/hipblaslt-ext.hpp>
@@ -45,6 +48,7 @@
 #include "cli.h"
 #include "flint/flint.h"
 #include "mfma_kernel.h"
+#include "monitor.h"
 
 namespace fb {
 namespace {
@@ -230,6 +234,7 @@ double median(std::vector<double> v) {
 struct Sample {
     long long launches = 0;
     double ms_per_launch = 0, sample_ms = 0;
+    std::optional<WindowStats> stats;
 };
 
 struct Round {
@@ -243,6 +248,8 @@ struct Side {
     long long launches_per_sample = 0;
     double min_sample_ms = 0, ms_per_launch = 0, gbs = 0, rated_fraction = 0, tflops = 0,
            rated_compute_fraction = 0;
+    std::optional<double> clock_adjusted_compute_fraction;
+    std::optional<WindowStats> stats;   // the valid samples' windows, merged by time
 };
 
 struct OutputCheck {
@@ -302,6 +309,25 @@ Side summarize(long long launches, const std::vector<const Sample*>& samples, co
         side.min_sample_ms = std::min(side.min_sample_ms, s->sample_ms);
     }
     side.ms_per_launch = median(per_launch);
+    if (samples[0]->stats) {
+        WindowStats m;
+        double sm = 0, mem = 0, pw = 0, act = 0, cap = 0, thm = 0;
+        for (const Sample* s : samples) {
+            const WindowStats& w = *s->stats;
+            m.seconds += w.seconds;
+            m.samples += w.samples;
+            m.failed_reads += w.failed_reads;
+            sm += w.sm_mhz * w.seconds, mem += w.mem_mhz * w.seconds, pw += w.power_w * w.seconds;
+            act += w.activity * w.seconds, cap += w.power_cap_share * w.seconds, thm += w.thermal_share * w.seconds;
+            m.temp_c_max = std::max(m.temp_c_max, w.temp_c_max);
+            m.new_process = m.new_process || w.new_process;
+        }
+        if (m.seconds > 0) {
+            m.sm_mhz = sm / m.seconds, m.mem_mhz = mem / m.seconds, m.power_w = pw / m.seconds;
+            m.activity = act / m.seconds, m.power_cap_share = cap / m.seconds, m.thermal_share = thm / m.seconds;
+        }
+        side.stats = m;
+    }
     if (spec.bytes_moved > 0) {
         side.gbs = spec.bytes_moved / (side.ms_per_launch * 1e-3) / 1e9;
         side.rated_fraction = side.gbs / kRatedBandwidthGBs;
@@ -310,11 +336,14 @@ Side summarize(long long launches, const std::vector<const Sample*>& samples, co
         side.tflops = spec.flops / (side.ms_per_launch * 1e-3) / 1e12;
         const double peak = spec.peak_flop_per_cu_per_clock * d.cu_count * d.rated_clock_mhz * 1e6 / 1e12;
         if (peak > 0) side.rated_compute_fraction = side.tflops / peak;
+        if (side.stats && side.stats->sm_mhz > 0)
+            side.clock_adjusted_compute_fraction =
+                side.tflops / (spec.peak_flop_per_cu_per_clock * d.cu_count * side.stats->sm_mhz * 1e6 / 1e12);
     }
     return side;
 }
 
-CaseResult run_case(const CaseSpec& spec, const DeviceInfo& d, const Options& o, hipStream_t stream) {
+CaseResult run_case(const CaseSpec& spec, const DeviceInfo& d, const Options& o, hipStream_t stream, Monitor& mon) {
     CaseResult r;
     r.spec = spec;
     hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
@@ -348,10 +377,15 @@ CaseResult run_case(const CaseSpec& spec, const DeviceInfo& d, const Options& o,
     }
     r.warmup_seconds = elapsed();
 
+    const bool monitored = mon.available();
+    double begin[2] = {0, 0}, end[2] = {0, 0};
+    int others = -1;
     auto sample = [&](int side) {
         Sample s;
         s.launches = launches[side];
+        begin[side] = mon.now();
         s.sample_ms = timer.time(*sides[side], stream, next, s.launches);
+        end[side] = mon.now();
         next += s.launches;
         s.ms_per_launch = s.sample_ms / s.launches;
         if (s.sample_ms < o.sample_ms)   // grow later samples back past sample_ms
@@ -362,6 +396,10 @@ CaseResult run_case(const CaseSpec& spec, const DeviceInfo& d, const Options& o,
     for (int i = 0; i < o.max_rounds && r.valid_rounds < o.rounds; ++i) {
         Round round;
         round.flint_first = r.one_sided || r.valid_rounds % 2 == 0;
+        if (monitored) {
+            mon.forget_before(mon.now() - 1.0);
+            others = mon.other_processes();
+        }
         if (r.one_sided) {
             round.flint = sample(0);
         } else if (round.flint_first) {
@@ -372,9 +410,17 @@ CaseResult run_case(const CaseSpec& spec, const DeviceInfo& d, const Options& o,
             round.flint = sample(0);
         }
         if (!r.one_sided) round.ratio = round.baseline.ms_per_launch / round.flint.ms_per_launch;
+        if (monitored) {
+            const int others_now = mon.other_processes();
+            round.flint.stats = mon.window(begin[0], end[0], others, others_now);
+            if (!r.one_sided) round.baseline.stats = mon.window(begin[1], end[1], others, others_now);
+        }
         for (int side = 0; side < n_sides && round.valid; ++side) {
             const Sample& s = side == 0 ? round.flint : round.baseline;
-            if (s.sample_ms < kShortestSample * o.sample_ms) {
+            if (s.stats && s.stats->new_process) {
+                round.valid = false;
+                round.discard_reason = "another process used the GPU";
+            } else if (s.sample_ms < kShortestSample * o.sample_ms) {
                 round.valid = false;
                 round.discard_reason = "a sample ran " + std::to_string(s.sample_ms) +
                                        " ms, short of the protocol's floor";
@@ -405,7 +451,7 @@ CaseResult run_case(const CaseSpec& spec, const DeviceInfo& d, const Options& o,
 
 // ---------------------------------------------------------------- copy
 
-CaseResult copy_case(unsigned long long bytes, const DeviceInfo& d, const Options& o, hipStream_t s) {
+CaseResult copy_case(unsigned long long bytes, const DeviceInfo& d, const Options& o, hipStream_t s, Monitor& mon) {
     const size_t stride = round256(bytes);
     CaseSpec spec;
     spec.benchmark = "copy";
@@ -432,7 +478,7 @@ CaseResult copy_case(unsigned long long bytes, const DeviceInfo& d, const Option
                       "hipMemcpyAsync");
         }
     };
-    CaseResult r = run_case(spec, d, o, s);
+    CaseResult r = run_case(spec, d, o, s, mon);
 
     // Output check: each side's copy of set 0 equals the source, bit for bit.
     std::vector<unsigned char> want(bytes), got(bytes);
@@ -454,7 +500,7 @@ CaseResult copy_case(unsigned long long bytes, const DeviceInfo& d, const Option
 
 // ---------------------------------------------------------------- mma
 
-CaseResult mma_case(int chains, const DeviceInfo& d, const Options& o, hipStream_t s) {
+CaseResult mma_case(int chains, const DeviceInfo& d, const Options& o, hipStream_t s, Monitor& mon) {
     const int blocks_per_cu = 2;   // 8 waves per CU: two per SIMD
     const int blocks = blocks_per_cu * d.cu_count;
     const int iters = kMfmaPerWave / chains;
@@ -471,7 +517,7 @@ CaseResult mma_case(int chains, const DeviceInfo& d, const Options& o, hipStream
         for (long long i = 0; i < count; ++i)
             hip_check(launch_mfma_loop(chains, blocks, flag, iters, st), "mfma_loop");
     };
-    CaseResult r = run_case(spec, d, o, s);
+    CaseResult r = run_case(spec, d, o, s, mon);
     int wrong = 0;
     hip_check(hipMemcpy(&wrong, bad.ptr, sizeof(int), hipMemcpyDeviceToHost), "hipMemcpy");
     r.outputs_match = wrong == 0;
@@ -546,7 +592,7 @@ void set_attr(hipblasLtMatmulDesc_t desc, hipblasLtMatmulDescAttributes_t attr, 
 }
 
 CaseResult gemm_case(const Shape& sh, Layout layout, Epilogue ep, const DeviceInfo& d, const Options& o,
-                     hipStream_t s, LtContext& lt) {
+                     hipStream_t s, LtContext& lt, Monitor& mon) {
     const size_t m = size_t(sh.m), n = size_t(sh.n), k = size_t(sh.k);
     const bool tn = layout == Layout::TN, residual = ep == Epilogue::BiasResidual;
     const bool has_pre = ep == Epilogue::BiasGelu || ep == Epilogue::DGelu;
@@ -741,7 +787,7 @@ CaseResult gemm_case(const Shape& sh, Layout layout, Epilogue ep, const DeviceIn
             else roc_call(set, Y.at(sy * set), tn, st);
         }
     };
-    CaseResult r = run_case(spec, d, o, s);
+    CaseResult r = run_case(spec, d, o, s, mon);
     if (ep != Epilogue::None) r.baseline_algorithm = algorithm;
 
     // Output check on set 0: Flint twice into differently poisoned outputs, the
@@ -831,12 +877,29 @@ struct Json {
     void str_or_null(const char* k, const std::string& v) { v.empty() ? null(k) : str(k, v); }
 };
 
+void write_stats(Json& j, const std::optional<WindowStats>& w) {
+    if (!w) return j.null("stats");
+    j.begin_obj("stats");
+    j.num("seconds", w->seconds);
+    j.integer("samples", w->samples);
+    j.integer("failed_reads", w->failed_reads);
+    j.num("sm_mhz", w->sm_mhz);
+    j.num("mem_mhz", w->mem_mhz);
+    j.num("power_w", w->power_w);
+    j.num("gfx_activity_percent", w->activity);
+    j.num("temp_c_max", w->temp_c_max);
+    j.num("power_cap_share", w->power_cap_share);
+    j.num("thermal_share", w->thermal_share);
+    j.boolean("new_process", w->new_process);
+    j.close('}');
+}
+
 void write_sample(Json& j, const char* k, const Sample& s) {
     j.begin_obj(k);
     j.integer("launches", s.launches);
     j.num("ms_per_launch", s.ms_per_launch);
     j.num("sample_ms", s.sample_ms);
-    j.null("stats");
+    write_stats(j, s.stats);
     j.close('}');
 }
 
@@ -850,8 +913,9 @@ void write_side(Json& j, const char* k, const Side& s) {
     j.null("clock_adjusted_fraction");
     j.num("tflops", s.tflops);
     j.num("rated_compute_fraction", s.rated_compute_fraction);
-    j.null("clock_adjusted_compute_fraction");
-    j.null("stats");
+    if (s.clock_adjusted_compute_fraction) j.num("clock_adjusted_compute_fraction", *s.clock_adjusted_compute_fraction);
+    else j.null("clock_adjusted_compute_fraction");
+    write_stats(j, s.stats);
     j.close('}');
 }
 
@@ -966,7 +1030,12 @@ std::string utc_now(const char* format) {
     return buf;
 }
 
-std::string report(const Command& c, const DeviceInfo& d, const std::vector<CaseResult>& cases) {
+struct AtStart {
+    bool monitored = false;
+    int other_processes = -1, utilization_percent = -1;
+};
+
+std::string report(const Command& c, const DeviceInfo& d, const std::vector<CaseResult>& cases, const AtStart& at) {
     // The repository root is three levels above build/release/bin.
     const std::string root = (exe_dir() / ".." / ".." / "..").lexically_normal().string();
     std::string sha = run_text("git -C '" + root + "' rev-parse HEAD 2>/dev/null");
@@ -1012,8 +1081,14 @@ std::string report(const Command& c, const DeviceInfo& d, const std::vector<Case
     j.boolean("quick", c.options.quick);
     j.str("lt_algo", lt_algo_name(c.options.lt_algo));
     j.close('}');
-    j.null("gpu_at_start");
-    j.str("monitor", "none: no clock, power or process sampling in this build");
+    j.begin_obj("gpu_at_start");
+    j.boolean("process_detection", at.other_processes >= 0);
+    if (at.other_processes >= 0) j.integer("other_processes", at.other_processes);
+    else j.null("other_processes");
+    if (at.utilization_percent >= 0) j.integer("utilization_percent", at.utilization_percent);
+    else j.null("utilization_percent");
+    j.close('}');
+    j.str("monitor", at.monitored ? "amd-smi gpu metrics, ~10 ms samples" : "unavailable: amd-smi could not open the device");
     j.begin_arr("cases");
     for (const CaseResult& r : cases) write_case(j, r);
     j.close(']');
@@ -1043,18 +1118,29 @@ void print_case(const CaseResult& r) {
 
 int run(const Command& c) {
     const DeviceInfo d = device_info();
+    Monitor mon;
+    AtStart at;
+    at.monitored = mon.available();
+    at.other_processes = mon.other_processes();
+    at.utilization_percent = mon.utilization_percent();
+    if (at.other_processes > 0) {
+        const std::string what = "the GPU is busy: " + std::to_string(at.other_processes) +
+                                 " other process(es) hold it; run with --allow-busy to measure anyway";
+        if (!c.options.allow_busy) throw Failure(what);
+        std::fprintf(stderr, "flint_bench: warning: %s\n", what.c_str());
+    }
     hipStream_t s = nullptr;
     hip_check(hipStreamCreate(&s), "hipStreamCreate");
     std::vector<CaseResult> cases;
     std::optional<LtContext> lt;
     if (c.benchmark == Benchmark::Gemm) lt.emplace();
     if (c.benchmark == Benchmark::Copy)
-        for (unsigned long long bytes : c.sizes) cases.push_back(copy_case(bytes, d, c.options, s)), print_case(cases.back());
+        for (unsigned long long bytes : c.sizes) cases.push_back(copy_case(bytes, d, c.options, s, mon)), print_case(cases.back());
     if (c.benchmark == Benchmark::Mma)
-        for (int chains : c.chains) cases.push_back(mma_case(chains, d, c.options, s)), print_case(cases.back());
+        for (int chains : c.chains) cases.push_back(mma_case(chains, d, c.options, s, mon)), print_case(cases.back());
     if (c.benchmark == Benchmark::Gemm)
         for (const Shape& sh : c.shapes)
-            cases.push_back(gemm_case(sh, c.layout, c.epilogue, d, c.options, s, *lt)), print_case(cases.back());
+            cases.push_back(gemm_case(sh, c.layout, c.epilogue, d, c.options, s, *lt, mon)), print_case(cases.back());
     hip_check(hipStreamDestroy(s), "hipStreamDestroy");
 
     std::filesystem::path out = c.out;
@@ -1066,7 +1152,7 @@ int run(const Command& c) {
               (std::string(benchmark_name(c.benchmark)) + "-" + gpu + "-" + utc_now("%Y%m%dT%H%M%SZ") + ".json");
     }
     if (out.has_parent_path()) std::filesystem::create_directories(out.parent_path());
-    const std::string text = report(c, d, cases);
+    const std::string text = report(c, d, cases, at);
     FILE* f = std::fopen(out.string().c_str(), "wb");
     if (!f || std::fwrite(text.data(), 1, text.size(), f) != text.size() || std::fclose(f) != 0)
         throw Failure("cannot write " + out.string());

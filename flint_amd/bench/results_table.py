@@ -6,7 +6,9 @@ Usage: python -m flint_amd.bench.results_table LOG.json [LOG.json ...]
 Each log gets a heading line (device, commit, command, protocol) and one row per
 case. Bandwidth cases (copy) show GB/s and the fraction of the 8 TB/s HBM peak;
 compute cases (mma, gemm) show TFLOP/s and the fraction of the dense FP16 MFMA
-peak at the rated clock. Two-sided cases add the baseline and the median ratio
+peak at the rated clock; with monitor statistics, also the mean graphics clock
+over Flint's samples, the fraction of the peak at that clock, and the share of
+the time the firmware's power cap (PPT) held the clock down. Two-sided cases add the baseline and the median ratio
 (baseline time / Flint time, above 1 when Flint is faster) with its range.
 A log whose numbers should not be quoted (a --quick run, options below the
 standard protocol, an unknown or dirty commit, a case that is not ok) says why.
@@ -76,7 +78,10 @@ def table(log):
     peak = "of FP16 peak" if compute else "of HBM peak"
     has_baseline = any(not c["one_sided"] for c in log["cases"])
     has_algo = any(c.get("baseline_algorithm") for c in log["cases"])
+    monitored = any(c["flint"].get("stats") for c in log["cases"])
     head = ["Case", "Flint ms", f"Flint {unit}", peak]
+    if monitored and compute:
+        head += ["SCLK MHz", "of peak at SCLK", "power-capped"]
     if has_baseline:
         head += ["Baseline", f"Baseline {unit}", "Ratio (median)", "Ratio range"]
     if has_algo:
@@ -87,6 +92,11 @@ def table(log):
     for c in log["cases"]:
         value, frac = rate(c, c["flint"])
         row = [case_name(c), f"{c['flint']['ms_per_launch']:.4f}", value, frac]
+        if monitored and compute:
+            st = c["flint"].get("stats")
+            adj = c["flint"].get("clock_adjusted_compute_fraction")
+            row += [f"{st['sm_mhz']:.0f}" if st else "-", pct(adj) if adj else "-",
+                    pct(st["power_cap_share"]) if st else "-"]
         if has_baseline:
             if c["one_sided"]:
                 row += ["-", "-", "-", "-"]

@@ -1,7 +1,7 @@
 """flint_bench: the command line (CPU: parsing needs no GPU), and quick end-to-end
 runs with their "flint-bench/1" JSON logs (GPU). Mirrors the reference's
 tests/test_bench.py:113-700: the same option errors, defaults and log checks,
-with rocBLAS and hipBLASLt as the baselines and no clock monitor."""
+with rocBLAS and hipBLASLt as the baselines and amd-smi as the monitor."""
 
 import json
 import statistics
@@ -236,6 +236,10 @@ def quick(exe, tmp_path, *args):
     assert data["schema"] == "flint-bench/1"
     assert data["args"] == list(args)
     assert data["quick"] is True and data["standard_protocol"] is False
+    start = data["gpu_at_start"]
+    assert isinstance(start["process_detection"], bool)
+    if start["utilization_percent"] is not None:
+        assert 0 <= start["utilization_percent"] <= 100
     return result, data
 
 
@@ -258,6 +262,27 @@ def assert_rounds(case, options, two_sided=True):
             [r[name]["ms_per_launch"] for r in valid]))
         for r in valid:
             assert r[name]["sample_ms"] >= 0.9 * options["sample_ms"]
+        if side["stats"] is not None:
+            assert_stats_follow_from_rounds(side["stats"], [r[name]["stats"] for r in valid])
+            if case["flops"] > 0:
+                # The firmware's clock readings lag short bursts of launches,
+                # so only the sign is pinned here.
+                assert side["clock_adjusted_compute_fraction"] > 0
+
+
+def assert_stats_follow_from_rounds(stats, windows):
+    """A side's stats merge its valid rounds' windows: counts add up, means are
+    weighted by each window's seconds, maxima and the new-process flag carry."""
+    seconds = sum(w["seconds"] for w in windows)
+    assert stats["seconds"] == pytest.approx(seconds)
+    assert stats["samples"] == sum(w["samples"] for w in windows)
+    assert stats["failed_reads"] == sum(w["failed_reads"] for w in windows)
+    for name in ("sm_mhz", "mem_mhz", "power_w", "gfx_activity_percent", "power_cap_share", "thermal_share"):
+        assert stats[name] == pytest.approx(sum(w[name] * w["seconds"] for w in windows) / seconds), name
+    assert stats["temp_c_max"] == max(w["temp_c_max"] for w in windows)
+    assert stats["new_process"] == any(w["new_process"] for w in windows)
+    for w in windows:
+        assert w["samples"] > 0 and w["sm_mhz"] > 0 and w["power_w"] > 0
 
 
 @pytest.mark.gpu
@@ -383,3 +408,51 @@ def test_epilogue_defaults_are_the_gpt2_layers(exe, tmp_path, args, labels):
     _, data = quick(exe, tmp_path, "gemm", *args, "--quick", "--allow-busy")
     assert [c["label"] for c in data["cases"]] == labels
     assert all(c["ok"] for c in data["cases"])
+
+
+# ------------------------------------------------------------------ CPU: results_table
+
+def synthetic_log(quick=False, sha="0123456789abcdef", dirty=False, ok=True, stats=True):
+    window = {"seconds": 1.0, "samples": 100, "failed_reads": 0, "sm_mhz": 2000.0, "mem_mhz": 2000.0,
+              "power_w": 1400.0, "gfx_activity_percent": 100.0, "temp_c_max": 60, "power_cap_share": 0.25,
+              "thermal_share": 0.0, "new_process": False}
+    side = {"ms_per_launch": 0.5, "tflops": 800.0, "rated_compute_fraction": 800 / 2516.6, "gbs": 0,
+            "rated_fraction": 0, "clock_adjusted_compute_fraction": 800 / (4096 * 256 * 2000e6 / 1e12),
+            "stats": window if stats else None}
+    case = {"benchmark": "gemm", "label": "8192x768x768", "layout": "nt", "epilogue": "bias", "flops": 2 * 8192 * 768 * 768,
+            "one_sided": False, "baseline_name": "hipBLASLt, FP32 bias", "flint": side,
+            "baseline": dict(side, ms_per_launch=0.6, tflops=666.7), "ratio": {"median": 1.2, "min": 1.1, "max": 1.3},
+            "baseline_algorithm": {"selection": "fastest", "used": 1, "candidates": [
+                {"index": 0, "solution_index": 7}, {"index": 1, "solution_index": 9}]},
+            "ok": ok, "outputs_match": ok, "output_check": {"rel_l2": 1e-6}, "valid_rounds": 10,
+            "rounds": [{}] * 10}
+    return {"schema": "flint-bench/1", "quick": quick, "standard_protocol": not quick, "args": ["gemm"],
+            "git": {"sha": sha, "dirty": dirty}, "timestamp_utc": "2026-01-01T00:00:00Z",
+            "device": {"name": "AMD gfx950", "arch": "gfx950", "cu_count": 256, "rated_sm_clock_mhz": 2400.0},
+            "cases": [case]}
+
+
+def test_results_table_rows():
+    from flint_amd.bench.results_table import table
+
+    text = table(synthetic_log())
+    assert "Not for quoting" not in text
+    (row,) = [line for line in text.splitlines() if line.startswith("| gemm nt+bias 8192x768x768")]
+    cells = [c.strip() for c in row.strip("|").split("|")]
+    assert cells[1:8] == ["0.5000", "800.0", "31.8%", "2000", "38.1%", "25.0%", "hipBLASLt, FP32 bias"]
+    assert cells[8:11] == ["666.7", "1.200", "1.100-1.300"]
+    assert cells[11] == "fastest: #1 of 2 (solution 9)"
+    assert cells[12:] == ["10/10", "ok, rel L2 1.0e-06"]
+    # Without monitor statistics the clock columns are left out.
+    assert "SCLK" not in table(synthetic_log(stats=False))
+
+
+@pytest.mark.parametrize("kwargs, reason", [
+    ({"quick": True}, "a --quick run"), ({"sha": "unknown"}, "built outside a git checkout"),
+    ({"dirty": True}, "uncommitted changes"), ({"ok": False}, "a case that is not ok"),
+])
+def test_results_table_says_why_a_log_is_not_for_quoting(kwargs, reason):
+    from flint_amd.bench.results_table import table
+
+    text = table(synthetic_log(**kwargs))
+    assert "Not for quoting:" in text and reason in text
