@@ -5,7 +5,10 @@
 
 #include <cstddef>
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
+
+#include "flint/flint_train.h"
 
 namespace flint {
 
@@ -158,5 +161,41 @@ hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, con
                                      size_t sequences, size_t length, size_t vocab, size_t width,
                                      bool accumulate_wte, bool accumulate_wpe, void* workspace,
                                      hipStream_t stream);
+
+// AdamW over many tensors (optimizer.hip). Each tensor is cut into chunks of
+// kAdamwChunk elements, one workgroup each; a launch takes up to kAdamwGroup
+// tensors by value. block_start[i] is tensor i's first workgroup in the launch
+// (block_start[count] the launch's workgroups); partial_offset is the launch's
+// first chunk among all of the step's chunks.
+constexpr int kAdamwGroup = 32;
+constexpr unsigned long long kAdamwChunk = 16384;
+constexpr size_t kAdamwMaxTensors = 4096;
+
+struct AdamwTensorArgs {
+    float* p;
+    const float* g;
+    float* m;
+    float* v;
+    __half* h;
+    unsigned long long n;
+    float decay;   // 1 - lr * weight_decay
+};
+
+struct AdamwGroup {
+    AdamwTensorArgs t[kAdamwGroup];
+    int block_start[kAdamwGroup + 1];
+    int count;
+    int partial_offset;
+};
+
+// Workspace of a step over `chunks` chunks: FP64 partials, then the decision.
+size_t adamw_workspace(size_t chunks);
+hipError_t launch_adamw_sumsq(const AdamwGroup& group, int blocks, void* workspace, const void* state,
+                              hipStream_t stream);
+hipError_t launch_adamw_decide(size_t chunks, void* workspace, void* state, const flint_adamw_options& o,
+                               hipStream_t stream);
+hipError_t launch_adamw_update(const AdamwGroup& group, int blocks, size_t chunks, const void* workspace,
+                               const flint_adamw_options& o, hipStream_t stream);
+hipError_t launch_train_state_init(void* state, float loss_scale, hipStream_t stream);
 
 }  // namespace flint

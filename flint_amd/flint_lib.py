@@ -18,6 +18,7 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "flint" / "flint.h"
+TRAIN_HEADER = ROOT / "include" / "flint" / "flint_train.h"
 LIBRARY = ROOT / "build" / "release" / "bin" / "libflint.so"
 
 OK = 0
@@ -47,11 +48,35 @@ class Gpt2ParameterInfo(ctypes.Structure):
 
 
 # Every function flint.h declares: name -> (restype, argtypes).
+class AdamwTensor(ctypes.Structure):
+    """flint_adamw_tensor (include/flint/flint_train.h)."""
+    _fields_ = [("param", ctypes.c_void_p), ("grad", ctypes.c_void_p), ("exp_avg", ctypes.c_void_p),
+                ("exp_avg_sq", ctypes.c_void_p), ("param_half", ctypes.c_void_p), ("count", ctypes.c_size_t),
+                ("weight_decay", ctypes.c_float)]
+
+
+class AdamwOptions(ctypes.Structure):
+    """flint_adamw_options (include/flint/flint_train.h)."""
+    _fields_ = [("lr", ctypes.c_float), ("beta1", ctypes.c_float), ("beta2", ctypes.c_float),
+                ("eps", ctypes.c_float), ("max_grad_norm", ctypes.c_float), ("growth_factor", ctypes.c_float),
+                ("backoff_factor", ctypes.c_float), ("growth_interval", ctypes.c_int)]
+
+
+class TrainState(ctypes.Structure):
+    """flint_train_state (include/flint/flint_train.h), 32 bytes."""
+    _fields_ = [("loss_scale", ctypes.c_float), ("growth_tracker", ctypes.c_int), ("step", ctypes.c_int),
+                ("found_inf", ctypes.c_int), ("grad_norm", ctypes.c_double), ("clip_coef", ctypes.c_double)]
+
+
 SIGNATURES = {
     "flint_version": (ctypes.c_char_p, []),
     "flint_status_string": (ctypes.c_char_p, [I]),
     "flint_last_error": (ctypes.c_char_p, []),
     "flint_copy": (I, [P, P, Z, P]),
+    "flint_adamw_defaults": (I, [ctypes.POINTER(AdamwOptions)]),
+    "flint_train_state_init": (I, [P, ctypes.c_float, P]),
+    "flint_adamw_workspace": (I, [ctypes.POINTER(AdamwTensor), Z, ctypes.POINTER(Z)]),
+    "flint_adamw_step": (I, [ctypes.POINTER(AdamwTensor), Z, P, ctypes.POINTER(AdamwOptions), P, Z, P]),
     "flint_gemm_nt": (I, [P, P, P, Z, Z, Z, P]),
     "flint_gemm_nt_bias": (I, [P, P, P, P, Z, Z, Z, P]),
     "flint_gemm_nt_bias_gelu": (I, [P, P, P, P, P, Z, Z, Z, P]),
@@ -155,6 +180,37 @@ class Flint:
     # -- GEMMs ----------------------------------------------------------------
     def copy(self, dst, src, nbytes, stream=None):
         self.check(self.lib.flint_copy(pointer(dst), pointer(src), nbytes, stream_handle(stream)))
+
+    # -- training step (flint_train.h) -------------------------------------------
+    def adamw_defaults(self):
+        o = AdamwOptions()
+        self.check(self.lib.flint_adamw_defaults(ctypes.byref(o)))
+        return o
+
+    @staticmethod
+    def adamw_tensors(tensors):
+        """dicts of param, grad, exp_avg, exp_avg_sq (FP32 tensors or addresses),
+        optional param_half, count and weight_decay -> a flint_adamw_tensor array."""
+        arr = (AdamwTensor * max(len(tensors), 1))()
+        for i, t in enumerate(tensors):
+            arr[i] = AdamwTensor(pointer(t["param"]), pointer(t["grad"]), pointer(t["exp_avg"]),
+                                 pointer(t["exp_avg_sq"]), pointer(t.get("param_half")),
+                                 t["count"] if "count" in t else t["param"].numel(), t.get("weight_decay", 0.0))
+        return arr
+
+    def train_state_init(self, state, loss_scale, stream=None):
+        self.check(self.lib.flint_train_state_init(pointer(state), loss_scale, stream_handle(stream)))
+
+    def adamw_workspace(self, tensors):
+        out = Z(0)
+        self.check(self.lib.flint_adamw_workspace(self.adamw_tensors(tensors), len(tensors), ctypes.byref(out)))
+        return out.value
+
+    def adamw_step(self, tensors, state, options, workspace, workspace_bytes=None, stream=None):
+        nbytes = workspace.numel() * workspace.element_size() if workspace_bytes is None else workspace_bytes
+        self.check(self.lib.flint_adamw_step(self.adamw_tensors(tensors), len(tensors), pointer(state),
+                                             ctypes.byref(options), pointer(workspace), nbytes,
+                                             stream_handle(stream)))
 
     def gemm_nt(self, y, x, w, m, n, k, stream=None):
         self.check(self.lib.flint_gemm_nt(pointer(y), pointer(x), pointer(w), m, n, k,
@@ -404,9 +460,11 @@ class Gpt2:
         return out.value
 
 
-def declared_functions(header=HEADER):
-    """Names of every FLINT_API function the header declares."""
+def declared_functions(header=None):
+    """Names of every FLINT_API function a header declares; by default those of
+    flint.h and of the training-step extension, flint_train.h."""
     import re
 
-    text = Path(header).read_text()
+    headers = [header] if header is not None else [HEADER, TRAIN_HEADER]
+    text = "".join(Path(h).read_text() for h in headers)
     return re.findall(r"FLINT_API\s+[^;(]*?\b(flint_\w+)\s*\(", text)

@@ -258,3 +258,54 @@ def rel_max_err(got, ref):
     if denom == 0:
         return float(np.max(np.abs(got - ref)))
     return float(np.max(np.abs(got - ref)) / denom)
+
+
+# --------------------------------------------------------------------------
+# AdamW step with clipping and a dynamic loss scale (the training-step
+# extension, include/flint/flint_train.h). The reference's step is
+# scripts/gpt2_torch.py:161-192 with the constants at :37-42, run by PyTorch
+# (2.10 in this image): GradScaler.unscale_ (grad * float(1 / scale)),
+# clip_grad_norm_ (norm over all tensors; coef = max_norm / (norm + 1e-6),
+# clamped to 1), AdamW (param *= 1 - lr * wd; exp_avg.lerp_(g, 1 - beta1);
+# exp_avg_sq = beta2 v + (1 - beta2) g^2; denom = sqrt(v) / sqrt(1 - beta2^t)
+# + eps; param -= lr / (1 - beta1^t) * m / denom) and GradScaler.update
+# (backoff on a non-finite gradient, growth after growth_interval finite
+# steps). All elementwise arithmetic is FP32 as in PyTorch; the norm is FP64.
+# Pinned in tests/test_train.py against torch.optim.AdamW, clip_grad_norm_ and
+# torch.amp.GradScaler on the CPU.
+# --------------------------------------------------------------------------
+
+def adamw_step(tensors, state, lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, max_grad_norm=1.0,
+               growth_factor=2.0, backoff_factor=0.5, growth_interval=2000):
+    """One step in place. tensors: dicts with float32 arrays param, grad,
+    exp_avg, exp_avg_sq and a float weight_decay. state: dict with loss_scale,
+    growth_tracker, step (updated in place). Returns (skipped, norm, clip)."""
+    f32 = np.float32
+    inv = f32(1.0 / float(f32(state["loss_scale"])))
+    unscaled = [t["grad"].astype(f32) * inv for t in tensors]
+    sumsq = sum(float(np.sum(u.astype(np.float64) ** 2)) for u in unscaled)
+    if not np.isfinite(sumsq):
+        state["loss_scale"] = float(f32(state["loss_scale"]) * f32(backoff_factor))
+        state["growth_tracker"] = 0
+        return True, float(np.sqrt(sumsq)), 0.0
+    norm = np.sqrt(sumsq)
+    clip = f32(min(1.0, max_grad_norm / (norm + 1e-6))) if max_grad_norm > 0 else f32(1.0)
+    state["step"] += 1
+    t_ = state["step"]
+    step_size = f32(lr / (1.0 - beta1 ** t_))
+    bc2_sqrt = f32(np.sqrt(1.0 - beta2 ** t_))
+    for t, u in zip(tensors, unscaled):
+        g = u * clip
+        p, m, v = t["param"], t["exp_avg"], t["exp_avg_sq"]
+        p *= f32(1.0 - lr * t["weight_decay"])
+        m += f32(1.0 - beta1) * (g - m)
+        v *= f32(beta2)
+        v += f32(1.0 - beta2) * (g * g)
+        denom = np.sqrt(v) / bc2_sqrt + f32(eps)
+        p -= step_size * (m / denom)
+    if state["growth_tracker"] + 1 == growth_interval:
+        state["loss_scale"] = float(f32(state["loss_scale"]) * f32(growth_factor))
+        state["growth_tracker"] = 0
+    else:
+        state["growth_tracker"] += 1
+    return False, float(norm), float(clip)
