@@ -404,6 +404,49 @@ def run(f, torch, dev, path, only=None):
         model.close()
         torch.cuda.empty_cache()
 
+    def section_adamw():
+        # One clipped, loss-scaled AdamW step over GPT-2 124M's 148 tensors
+        # (named_parameters shapes, decay on the matrices): 34 bytes of HBM
+        # traffic per parameter (gradient read twice, param/m/v read and
+        # written, the FP16 copy written). One set is 4.2 GB, past the cache.
+        shapes = [(50257, C), (1024, C)]
+        for _ in range(12):
+            shapes += [(C,), (C,), (3 * C, C), (3 * C,), (C, C), (C,), (C,), (C,), (4 * C, C), (4 * C,),
+                       (C, 4 * C), (C,)]
+        shapes += [(C,), (C,)]
+        gen = torch.Generator(device=dev).manual_seed(80)
+        ts = []
+        for shp in shapes:
+            n = math.prod(shp)
+            ts.append({"param": torch.randn(n, device=dev, generator=gen) * 0.02,
+                       "grad": torch.randn(n, device=dev, generator=gen) * 0.1,
+                       "exp_avg": torch.zeros(n, device=dev), "exp_avg_sq": torch.zeros(n, device=dev),
+                       "param_half": torch.empty(n, dtype=torch.float16, device=dev),
+                       "weight_decay": 0.1 if len(shp) == 2 else 0.0})
+        total = sum(t["param"].numel() for t in ts)
+        state = torch.zeros(8, dtype=torch.float32, device=dev)
+        f.train_state_init(state, 1024.0)
+        opts = f.adamw_defaults()
+        ws = torch.empty(f.adamw_workspace(ts), dtype=torch.uint8, device=dev)
+        ms = _time_gpu(torch, lambda _: f.adamw_step(ts, state, opts, ws), [0], per_round=8)
+        # CPU: torch's AdamW (foreach) with unscale and clipping on a 4M sample.
+        ns = 4 << 20
+        cp = [torch.nn.Parameter(torch.randn(ns) * 0.02)]
+        cp[0].grad = torch.randn(ns) * 0.1
+        copt = torch.optim.AdamW(cp, lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+        def cpu_step():
+            cp[0].grad.mul_(1 / 1024)
+            torch.nn.utils.clip_grad_norm_(cp, 1.0)
+            copt.step()
+
+        cpu_s = _time_cpu(cpu_step)
+        record(f"flint_adamw_step GPT-2 124M ({len(ts)} tensors, {total / 1e6:.1f}M params)", "red",
+               34 * total, ms, cpu_s=cpu_s, cpu_work=34 * ns,
+               note="3 kernels: gradient norm partials, decision, update + FP16 copy; 34 B/param")
+        del ts, ws
+        torch.cuda.empty_cache()
+
     if any(want(x) for x in ("flint_gemm_nt_batched", "flint_gemm_nn_batched",
                              "flint_gemm_tn_batched")):
         section_batched()
@@ -419,6 +462,8 @@ def run(f, torch, dev, path, only=None):
     if any(want(x) for x in ("flint_copy", "flint_fp32_to_fp16", "flint_heads_split",
                              "flint_heads_merge", "flint_embedding")):
         section_support()
+    if want("flint_adamw_step"):
+        section_adamw()
     Path(path).write_text(json.dumps(out, indent=1))
     return out
 
