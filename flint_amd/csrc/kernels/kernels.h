@@ -167,8 +167,8 @@ hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, con
 // tensors by value. block_start[i] is tensor i's first workgroup in the launch
 // (block_start[count] the launch's workgroups); partial_offset is the launch's
 // first chunk among all of the step's chunks.
-constexpr int kAdamwGroup = 32;
-constexpr unsigned long long kAdamwChunk = 16384;
+constexpr int kAdamwGroup = 64;   // 64 x 56-byte entries + starts: under 4 KB of kernel arguments
+constexpr unsigned long long kAdamwChunk = 8192;
 constexpr size_t kAdamwMaxTensors = 4096;
 
 struct AdamwTensorArgs {
@@ -187,6 +187,7 @@ struct AdamwGroup {
     int count;
     int partial_offset;
 };
+static_assert(sizeof(AdamwGroup) <= 4096, "AdamwGroup is passed as a kernel argument");
 
 // Workspace of a step over `chunks` chunks: FP64 partials, then the decision.
 size_t adamw_workspace(size_t chunks);

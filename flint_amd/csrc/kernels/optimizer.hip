@@ -5,7 +5,7 @@
 //
 // Three kernels per step, all on the caller's stream and none waiting on the
 // host:
-//   adamw_sumsq   one workgroup per 16,384-element chunk of a tensor: the sum
+//   adamw_sumsq   one workgroup per 8,192-element chunk of a tensor: the sum
 //                 of (grad / loss_scale)^2 over the chunk, in FP64, reduced in a
 //                 fixed tree, to partials[chunk]. A non-finite gradient makes its
 //                 partial non-finite.

@@ -20,7 +20,7 @@ import torch
 from flint_amd.flint_lib import AdamwOptions, FlintError, TrainState
 from oracle import oracle
 
-# Element counts: one chunk is 16,384 values; tails of 0-3 past a float4 and
+# Element counts: one chunk is 8,192 values; tails of 0-3 past a float4 and
 # several chunks per tensor.
 COUNTS = [768 * 4, 1, 3, 16384 * 2 + 7, 50304 + 2, 768, 16384, 5]
 
@@ -124,7 +124,8 @@ def test_workspace_and_its_check(flint):
     t = [{"param": 0, "grad": 0, "exp_avg": 0, "exp_avg_sq": 0, "count": 16384 * 3 + 1, "weight_decay": 0.0},
          {"param": 0, "grad": 0, "exp_avg": 0, "exp_avg_sq": 0, "count": 10, "weight_decay": 0.1}]
     need = flint.adamw_workspace(t)
-    assert need == (5 * 8 + 255) // 256 * 256 + 256   # five chunks of FP64 partials, then the decision
+    chunks = -(-(16384 * 3 + 1) // 8192) + 1   # 8,192-value chunks
+    assert need == (chunks * 8 + 255) // 256 * 256 + 256   # FP64 partials, then the decision
     o = flint.adamw_defaults()
     with pytest.raises(FlintError, match="needs .* bytes of workspace"):
         flint.check(flint.lib.flint_adamw_step(flint.adamw_tensors(t), 2, 4096, ctypes.byref(o), 8192, need - 1, None))
