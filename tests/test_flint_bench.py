@@ -264,7 +264,7 @@ def assert_rounds(case, options, two_sided=True):
             assert r[name]["sample_ms"] >= 0.9 * options["sample_ms"]
         if side["stats"] is not None:
             assert_stats_follow_from_rounds(side["stats"], [r[name]["stats"] for r in valid])
-            if case["flops"] > 0:
+            if case["flops"] > 0 and side["stats"]["samples"] > 0:
                 # The firmware's clock readings lag short bursts of launches,
                 # so only the sign is pinned here.
                 assert side["clock_adjusted_compute_fraction"] > 0
@@ -281,8 +281,12 @@ def assert_stats_follow_from_rounds(stats, windows):
         assert stats[name] == pytest.approx(sum(w[name] * w["seconds"] for w in windows) / seconds), name
     assert stats["temp_c_max"] == max(w["temp_c_max"] for w in windows)
     assert stats["new_process"] == any(w["new_process"] for w in windows)
+    # A short (--quick) sample can fall between two of the monitor's ~10 ms
+    # readings; a window that holds readings has a clock and a power.
     for w in windows:
-        assert w["samples"] > 0 and w["sm_mhz"] > 0 and w["power_w"] > 0
+        assert w["samples"] >= 0
+        if w["samples"] > 0:
+            assert w["sm_mhz"] > 0 and w["power_w"] > 0
 
 
 @pytest.mark.gpu
