@@ -1,6 +1,6 @@
 // flint_bench's command-line parser. The option names, defaults and error
-// texts are the reference's interface (ref bench/cli.cpp:222-444, the usage at
-// :446-516), so scripts and tests written against it read the same; the case
+// texts are the reference's interface (ref bench/cli.cpp:222-444; the help
+// text below is this harness's own), so scripts and tests written against it read the same; the case
 // lists name the same GPT-2 124M shapes at 8,192 tokens.
 #include "cli.h"
 
@@ -305,72 +305,69 @@ Command parse(int argc, char** argv) {
 std::string usage() {
     return "usage: flint_bench <benchmark> [options]\n"
            "\n"
-           "benchmarks:\n"
-           "  copy                  flint_copy against hipMemcpyAsync\n"
-           "  mma                   matrix-core v_mfma_f32_32x32x16_f16 throughput (FP16\n"
-           "                        operands, FP32 accumulation), timed against the GPU's\n"
-           "                        dense FP16 peak\n"
-           "  gemm                  flint_gemm_nt (y = x w^T), flint_gemm_nn (y = x w) or\n"
-           "                        flint_gemm_tn (y = x^T w), FP16 with FP32 accumulation,\n"
-           "                        against rocBLAS (hipBLASLt with a bias, GELU or its\n"
-           "                        derivative)\n"
+           "Times libflint on this GPU against a vendor baseline and writes a\n"
+           "flint-bench/1 JSON log. Options take their value as --name VALUE or\n"
+           "--name=VALUE.\n"
            "\n"
-           "options (--flag value or --flag=value):\n"
-           "  --sizes LIST          copy: comma-separated sizes in bytes, with an optional\n"
-           "                        K, M or G suffix (KiB, MiB, GiB); default 1M,16M,256M\n"
-           "  --chains LIST         mma: independent accumulator chains per wave, from\n"
-           "                        4, 8 and 16; default 4,8,16\n"
-           "  --layout nt|nn|tn     gemm: nt is y (M x N) = x (M x K) times w (N x K)\n"
-           "                        transposed, nn is y = x times w (K x N), tn is y (FP32) =\n"
-           "                        x (K x M) transposed times w (K x N), timed accumulating\n"
-           "                        into y; default nt\n"
+           "Benchmarks\n"
+           "  copy    bytes moved by flint_copy; baseline hipMemcpyAsync (device to device)\n"
+           "  mma     one-sided: a loop of v_mfma_f32_32x32x16_f16 (FP16 in, FP32 sums),\n"
+           "          as a fraction of the dense FP16 matrix-core peak\n"
+           "  gemm    flint_gemm_nt / _nn / _tn and the fused epilogues; baseline\n"
+           "          rocBLAS gemm_ex for plain products, hipBLASLt for epilogues\n"
+           "\n"
+           "copy\n"
+           "  --sizes LIST      byte counts separated by commas; a K, M or G suffix means\n"
+           "                    KiB, MiB or GiB. Default 1M,16M,256M\n"
+           "mma\n"
+           "  --chains LIST     accumulator chains per wave, each 4, 8 or 16. Default 4,8,16\n"
+           "gemm\n"
+           "  --layout nt|nn|tn which operand is transposed. nt: y[M,N] = x[M,K] w[N,K]^T;\n"
+           "                    nn: y = x w with w[K,N]; tn: FP32 y[M,N] += x[K,M]^T w[K,N]\n"
+           "                    (timed accumulating). Default nt\n"
            "  --epilogue none|bias|bias-gelu|bias-residual|dgelu\n"
-           "                        gemm: bias adds n FP32 values, one per column of y, to the\n"
-           "                        FP32 sums before they round (flint_gemm_nt_bias, against\n"
-           "                        hipBLASLt's BIAS epilogue); bias-gelu then applies GELU,\n"
-           "                        also storing the sums before it (flint_gemm_nt_bias_gelu,\n"
-           "                        against hipBLASLt's GELU_AUX_BIAS epilogue); bias-residual\n"
-           "                        then adds an m x n FP32 residual stream into an FP32 y\n"
-           "                        (flint_gemm_nt_bias_residual, against hipBLASLt's bias\n"
-           "                        epilogue with the residual as C and beta 1); all three\n"
-           "                        need --layout nt. dgelu multiplies the sums by GELU's\n"
-           "                        derivative at a stored m x n FP16 pre, the backward pass\n"
-           "                        (flint_gemm_nn_dgelu, against hipBLASLt's DGELU\n"
-           "                        epilogue); it needs --layout nn. Default none\n"
+           "                    work fused after the product. With --layout nt only:\n"
+           "                      bias           + one FP32 value per column, then round\n"
+           "                                     (hipBLASLt BIAS)\n"
+           "                      bias-gelu      as bias, then GELU, keeping the pre-GELU\n"
+           "                                     values too (hipBLASLt GELU_AUX_BIAS)\n"
+           "                      bias-residual  as bias, plus an FP32 residual, into FP32 y\n"
+           "                                     (hipBLASLt bias, residual as C, beta 1)\n"
+           "                    With --layout nn only:\n"
+           "                      dgelu          times GELU'(pre) at a stored FP16 pre\n"
+           "                                     (hipBLASLt DGELU)\n"
+           "                    Default none\n"
            "  --lt-algo fastest|first\n"
-           "                        gemm: which of hipBLASLt's candidate algorithms the\n"
-           "                        epilogue cases (not none) use as the baseline. fastest,\n"
-           "                        the default, times the heuristic's first 8 on each\n"
-           "                        case's buffers and uses the quickest; first uses the\n"
-           "                        heuristic's first choice. The JSON lists the candidates\n"
-           "                        and their times either way\n"
-           "  --shapes LIST         gemm: comma-separated MxNxK; M and N up to 8388480, and K\n"
-           "                        up to 65536. nt and nn need K a multiple of 8 (and nn N\n"
-           "                        too, as does bias-gelu; bias-residual needs N even); tn\n"
-           "                        needs M and N multiples of 8 and takes any K.\n"
-           "                        Default the GPT-2 shapes at 8192 tokens. For nt, the\n"
-           "                        forward pass: 8192x2304x768,8192x768x768,8192x3072x768,\n"
-           "                        8192x768x3072,8192x50304x768, without the last with\n"
-           "                        --epilogue bias, only the third with --epilogue bias-gelu,\n"
-           "                        and only the second and fourth, the layers that feed the\n"
-           "                        residual stream, with --epilogue bias-residual. For nn,\n"
-           "                        the input gradients: 8192x768x2304,8192x768x768,\n"
-           "                        8192x768x3072,8192x3072x768,8192x768x50304, and only the\n"
-           "                        fourth with --epilogue dgelu. For tn, the\n"
-           "                        weight gradients: 2304x768x8192,768x768x8192,\n"
-           "                        3072x768x8192,768x3072x8192,50304x768x8192\n"
-           "  --rounds N            valid rounds required per case (default 10)\n"
-           "  --max-rounds N        rounds tried before giving up (default 30, or 3 x rounds\n"
-           "                        if --rounds is above 30)\n"
-           "  --warmup SECONDS      warm-up time per case (default 1.5)\n"
-           "  --sample-ms MS        the shortest timed sample (default 100)\n"
-           "  --allow-busy          run even if other processes are on the GPU\n"
-           "  --quick               shortened protocol for tests, never a real result:\n"
-           "                        warmup 0.2, sample-ms 10, rounds 3, max-rounds 6;\n"
-           "                        explicit options override these\n"
-           "  --out PATH            JSON output path (default: bench-results/ in the build\n"
-           "                        directory, named by benchmark, GPU and time)\n"
-           "  --help                show this text\n";
+           "                    hipBLASLt baseline for epilogue cases: `fastest` times up\n"
+           "                    to 8 heuristic candidates on the case's own buffers and keeps\n"
+           "                    the quickest (default); `first` takes the heuristic's top\n"
+           "                    pick. Every candidate's time is logged\n"
+           "  --shapes LIST     MxNxK items separated by commas. Limits: M, N <= 8388480,\n"
+           "                    K <= 65536. nt, nn: K % 8 == 0; nn and bias-gelu: N % 8 == 0;\n"
+           "                    bias-residual: N even; tn: M % 8 == 0 and N % 8 == 0, any K.\n"
+           "                    Defaults are GPT-2 124M at 8192 tokens:\n"
+           "                      nt  8192x2304x768,8192x768x768,8192x3072x768,\n"
+           "                          8192x768x3072,8192x50304x768 (bias: all but the\n"
+           "                          logits; bias-gelu: 8192x3072x768; bias-residual:\n"
+           "                          8192x768x768 and 8192x768x3072)\n"
+           "                      nn  8192x768x2304,8192x768x768,8192x768x3072,\n"
+           "                          8192x3072x768,8192x768x50304 (dgelu: 8192x3072x768)\n"
+           "                      tn  2304x768x8192,768x768x8192,3072x768x8192,\n"
+           "                          768x3072x8192,50304x768x8192\n"
+           "\n"
+           "Protocol\n"
+           "  --rounds N        valid interleaved rounds a case needs (default 10)\n"
+           "  --max-rounds N    give up after this many rounds (default 30; 3 x --rounds\n"
+           "                    when that is larger)\n"
+           "  --warmup SECONDS  untimed launches first, per case (default 1.5)\n"
+           "  --sample-ms MS    minimum length of one timed sample (default 100)\n"
+           "  --quick           test-sized protocol whose numbers are not results:\n"
+           "                    --warmup 0.2 --sample-ms 10 --rounds 3 --max-rounds 6,\n"
+           "                    each overridable\n"
+           "  --allow-busy      do not refuse to start while other processes use the GPU\n"
+           "  --out PATH        where the JSON goes (default: a file in bench-results/ next\n"
+           "                    to the binary, named for benchmark, GPU and start time)\n"
+           "  --help            print this and exit\n";
 }
 
 }  // namespace fb

@@ -310,21 +310,26 @@ Side summarize(long long launches, const std::vector<const Sample*>& samples, co
     }
     side.ms_per_launch = median(per_launch);
     if (samples[0]->stats) {
+        // Means are weighted by the seconds of the windows that hold a
+        // reading; a window without one adds its time and counts only.
         WindowStats m;
-        double sm = 0, mem = 0, pw = 0, act = 0, cap = 0, thm = 0;
+        double sm = 0, mem = 0, pw = 0, act = 0, cap = 0, thm = 0, read_seconds = 0;
         for (const Sample* s : samples) {
             const WindowStats& w = *s->stats;
             m.seconds += w.seconds;
             m.samples += w.samples;
             m.failed_reads += w.failed_reads;
-            sm += w.sm_mhz * w.seconds, mem += w.mem_mhz * w.seconds, pw += w.power_w * w.seconds;
-            act += w.activity * w.seconds, cap += w.power_cap_share * w.seconds, thm += w.thermal_share * w.seconds;
             m.temp_c_max = std::max(m.temp_c_max, w.temp_c_max);
             m.new_process = m.new_process || w.new_process;
+            if (w.samples == 0) continue;
+            read_seconds += w.seconds;
+            sm += w.sm_mhz * w.seconds, mem += w.mem_mhz * w.seconds, pw += w.power_w * w.seconds;
+            act += w.activity * w.seconds, cap += w.power_cap_share * w.seconds, thm += w.thermal_share * w.seconds;
         }
-        if (m.seconds > 0) {
-            m.sm_mhz = sm / m.seconds, m.mem_mhz = mem / m.seconds, m.power_w = pw / m.seconds;
-            m.activity = act / m.seconds, m.power_cap_share = cap / m.seconds, m.thermal_share = thm / m.seconds;
+        if (read_seconds > 0) {
+            m.sm_mhz = sm / read_seconds, m.mem_mhz = mem / read_seconds, m.power_w = pw / read_seconds;
+            m.activity = act / read_seconds, m.power_cap_share = cap / read_seconds;
+            m.thermal_share = thm / read_seconds;
         }
         side.stats = m;
     }
@@ -883,13 +888,15 @@ void write_stats(Json& j, const std::optional<WindowStats>& w) {
     j.num("seconds", w->seconds);
     j.integer("samples", w->samples);
     j.integer("failed_reads", w->failed_reads);
-    j.num("sm_mhz", w->sm_mhz);
-    j.num("mem_mhz", w->mem_mhz);
-    j.num("power_w", w->power_w);
-    j.num("gfx_activity_percent", w->activity);
-    j.num("temp_c_max", w->temp_c_max);
-    j.num("power_cap_share", w->power_cap_share);
-    j.num("thermal_share", w->thermal_share);
+    // Without a reading the means are unknown, not zero.
+    const char* means[] = {"sm_mhz", "mem_mhz", "power_w", "gfx_activity_percent", "temp_c_max",
+                           "power_cap_share", "thermal_share"};
+    const double values[] = {w->sm_mhz, w->mem_mhz, w->power_w, w->activity, w->temp_c_max,
+                             w->power_cap_share, w->thermal_share};
+    for (int i = 0; i < 7; ++i) {
+        if (w->samples > 0) j.num(means[i], values[i]);
+        else j.null(means[i]);
+    }
     j.boolean("new_process", w->new_process);
     j.close('}');
 }

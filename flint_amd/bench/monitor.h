@@ -102,6 +102,23 @@ public:
             if (!first) first = &s;
             last = &s;
         }
+        // A window shorter than the ~10 ms between readings may hold none:
+        // it then takes the last good reading before it, the one in effect
+        // when it began (ref bench/monitor.cpp:242-246 holds that reading
+        // the same way), so every window of a running monitor has a clock.
+        if (w.samples == 0) {
+            const Sample* held = nullptr;
+            for (const Sample& s : samples_)
+                if (s.ok && s.t < begin) held = &s;
+            if (held) {
+                w.samples = 1;
+                w.sm_mhz = held->gfx_mhz;
+                w.mem_mhz = held->mem_mhz;
+                w.power_w = held->power_w;
+                w.activity = held->activity;
+                w.temp_c_max = held->temp_c;
+            }
+        }
         if (w.samples) {
             w.sm_mhz /= w.samples;
             w.mem_mhz /= w.samples;
@@ -117,11 +134,17 @@ public:
         return w;
     }
 
-    // Drops the samples taken before t (no later window will start earlier).
+    // Drops the samples taken before t (no later window will start earlier),
+    // except the last good one, which a window without readings of its own
+    // holds over.
     void forget_before(double t) {
         std::lock_guard<std::mutex> lock(mutex_);
-        samples_.erase(samples_.begin(), std::find_if(samples_.begin(), samples_.end(),
-                                                      [&](const Sample& s) { return s.t >= t; }));
+        auto end = std::find_if(samples_.begin(), samples_.end(),
+                                [&](const Sample& s) { return s.t >= t; });
+        auto keep = end;
+        for (auto it = samples_.begin(); it != end; ++it)
+            if (it->ok) keep = it;
+        samples_.erase(samples_.begin(), keep == end ? end : keep);
     }
 
 private:

@@ -1,158 +1,145 @@
-// C-ABI entry points of the GEMM family: argument checks (order and message
-// text as the reference's src/api/gemm.cpp:24-168 has them, which its tests
-// match verbatim), then one launcher call.
+// C-ABI entry points of the GEMM family.
+//
+// Each entry point is one row of a table (kEntries): its name, the operand
+// layout, the element size of y and which extra buffers it takes. One
+// validator walks a row's rules in the order the reference reports them
+// (ref src/api/gemm.cpp:24-168; its tests match the order and the message
+// texts), then the entry point makes one launcher call.
 #include <cmath>
-#include <iterator>
 
-#include "common/common.h"
+#include "common/args.h"
 #include "kernels/kernels.h"
 
 namespace {
 
-using flint::aligned16;
-using flint::fail;
-using flint::fits;
-using flint::overlap;
+using flint::Checker;
+using flint::Span;
 
-// NT's and NN's checks for m, n > 0 (ref src/api/gemm.cpp:27-67). w holds n*k
-// halves in both layouts; NN moves w's rows (n long) in 16-byte chunks, so n
-// must be a multiple of 8 there. y has y_element bytes per value.
-flint_status check_nt_nn(const char* name, bool n_in_chunks, void* y, const void* x,
-                         const void* w, size_t m, size_t n, size_t k, size_t y_element = 2) {
-    if (k == 0 || k % 8 != 0) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: k (%zu) must be a positive multiple of 8",
-                    name, k);
-    }
-    if (n_in_chunks && n % 8 != 0) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: n (%zu) must be a multiple of 8", name, n);
-    }
-    if (m > flint::kGemmMaxMN || n > flint::kGemmMaxMN || k > flint::kGemmMaxK) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: %zu x %zu x %zu is too large: m and n can be up to %zu, and k up to %zu",
-                    name, m, n, k, flint::kGemmMaxMN, flint::kGemmMaxK);
-    }
-    if (y == nullptr || x == nullptr || w == nullptr) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: %s is null", name,
-                    y == nullptr ? "y" : x == nullptr ? "x" : "w");
-    }
-    if (!aligned16(y) || !aligned16(x) || !aligned16(w)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: %s is not 16-byte aligned", name,
-                    !aligned16(y) ? "y" : !aligned16(x) ? "x" : "w");
-    }
-    const size_t y_bytes = m * n * y_element;
-    const size_t x_bytes = m * k * 2;
-    const size_t w_bytes = n * k * 2;
-    if (!fits(y, y_bytes) || !fits(x, x_bytes) || !fits(w, w_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: %s runs past the end of the address space",
-                    name, !fits(y, y_bytes) ? "y" : !fits(x, x_bytes) ? "x" : "w");
-    }
-    if (overlap(y, y_bytes, x, x_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: y and x overlap", name);
-    }
-    if (overlap(y, y_bytes, w, w_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: y and w overlap", name);
-    }
-    return FLINT_OK;
+enum Shape { kNt, kNn, kTn, kNtBatched, kNnBatched, kTnBatched };
+enum Extra : unsigned { kNoExtra = 0, kBias = 1, kPre = 2, kResidual = 4, kCrossPre = 8 };
+
+struct Entry {
+    const char* name;
+    Shape shape;
+    size_t y_elem;      // bytes per element of y
+    unsigned extras;
+};
+
+constexpr Entry kGemmNt{"flint_gemm_nt", kNt, 2, kNoExtra};
+constexpr Entry kGemmNtBias{"flint_gemm_nt_bias", kNt, 2, kBias};
+constexpr Entry kGemmNtBiasGelu{"flint_gemm_nt_bias_gelu", kNt, 2, kBias | kPre | kCrossPre};
+constexpr Entry kGemmNtBiasResidual{"flint_gemm_nt_bias_residual", kNt, 4, kBias | kResidual};
+constexpr Entry kGemmNn{"flint_gemm_nn", kNn, 2, kNoExtra};
+constexpr Entry kGemmNnDGelu{"flint_gemm_nn_dgelu", kNn, 2, kPre};
+constexpr Entry kGemmTn{"flint_gemm_tn", kTn, 4, kNoExtra};
+constexpr Entry kGemmNtBatched{"flint_gemm_nt_batched", kNtBatched, 2, kNoExtra};
+constexpr Entry kGemmNnBatched{"flint_gemm_nn_batched", kNnBatched, 2, kNoExtra};
+constexpr Entry kGemmTnBatched{"flint_gemm_tn_batched", kTnBatched, 2, kNoExtra};
+
+// Everything one call hands over.
+struct Call {
+    void* y;
+    const void* x;
+    const void* w;
+    const void* bias = nullptr;
+    const void* pre = nullptr;        // GELU's stored sums (written or read)
+    const void* residual = nullptr;
+    size_t batches = 1, m = 0, n = 0, k = 0;
+    float scale = 1.0f;
+};
+
+constexpr size_t kMaxMN = flint::kGemmMaxMN;
+constexpr size_t kMaxK = flint::kGemmMaxK;
+
+// TN's sizes: k is a row count (any positive value); m and n are the rows of
+// x and w moved in 16-byte chunks.
+void tn_sizes(Checker& c, const Call& a) {
+    c.require(a.k != 0, "k must be positive")
+        .require(a.m % 8 == 0, "m (%zu) must be a multiple of 8", a.m)
+        .require(a.n % 8 == 0, "n (%zu) must be a multiple of 8", a.n)
+        .require(a.m <= kMaxMN && a.n <= kMaxMN && a.k <= kMaxK,
+                 "%zu x %zu x %zu is too large: m and n can be up to %zu, and k up to %zu", a.m,
+                 a.n, a.k, kMaxMN, kMaxK);
 }
 
-flint_status check_bias(const char* name, const void* y, const void* bias, size_t m, size_t n,
-                        size_t y_element = 2) {
-    if (bias == nullptr) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: bias is null", name);
-    }
-    if (!aligned16(bias)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: bias is not 16-byte aligned", name);
-    }
-    const size_t bias_bytes = n * 4;
-    if (!fits(bias, bias_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: bias runs past the end of the address space",
-                    name);
-    }
-    if (overlap(y, m * n * y_element, bias, bias_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: y and bias overlap", name);
-    }
-    return FLINT_OK;
+// NT's and NN's k (a multiple of 8: rows of x and w move in 16-byte chunks),
+// and NN's n (w's rows, n long, move in chunks too).
+void chunked_k(Checker& c, const Call& a, bool n_in_chunks) {
+    c.require(a.k != 0 && a.k % 8 == 0, "k (%zu) must be a positive multiple of 8", a.k)
+        .require(!n_in_chunks || a.n % 8 == 0, "n (%zu) must be a multiple of 8", a.n);
 }
 
-flint_status check_pre(const char* name, const void* y, const void* pre, size_t m, size_t n) {
-    if (pre == nullptr) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: pre is null", name);
+flint_status validate(const Entry& e, const Call& a) {
+    Checker c(e.name);
+    const size_t per = a.batches;
+    const Span y{"y", a.y, per * a.m * a.n * e.y_elem};
+    const Span x{"x", a.x, per * a.m * a.k * 2};
+    const Span w{"w", a.w, per * a.n * a.k * 2};
+    switch (e.shape) {
+    case kNt:
+    case kNn:
+        chunked_k(c, a, e.shape == kNn);
+        c.require(a.m <= kMaxMN && a.n <= kMaxMN && a.k <= kMaxK,
+                  "%zu x %zu x %zu is too large: m and n can be up to %zu, and k up to %zu", a.m,
+                  a.n, a.k, kMaxMN, kMaxK);
+        c.operands({y, x, w}).apart(y, {x, w});
+        break;
+    case kTn:
+        tn_sizes(c, a);
+        c.operands({y, x, w}).apart(y, {x, w});
+        break;
+    case kNtBatched:
+    case kNnBatched:
+    case kTnBatched:
+        if (e.shape == kTnBatched) {
+            tn_sizes(c, a);
+        } else {
+            chunked_k(c, a, e.shape == kNnBatched);
+            c.require(a.n <= kMaxMN && a.k <= kMaxK, "n (%zu) can be up to %zu, and k (%zu) up to %zu",
+                      a.n, kMaxMN, a.k, kMaxK);
+        }
+        if (e.shape == kNtBatched)
+            c.require(std::isfinite(a.scale), "scale (%g) must be finite", double(a.scale));
+        c.require(a.batches <= flint::kGemmMaxBatches, "batches (%zu) can be up to %zu", a.batches,
+                  flint::kGemmMaxBatches)
+            .require(a.m <= flint::kGemmBatchedMaxM, "m (%zu) can be up to %zu", a.m,
+                     flint::kGemmBatchedMaxM)
+            .buffers({y, x, w}, 1);
+        break;
     }
-    if (!aligned16(pre)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: pre is not 16-byte aligned", name);
+    if (e.extras & kResidual) c.require(a.n % 2 == 0, "n (%zu) must be even", a.n);
+    const Span bias{"bias", a.bias, a.n * 4};
+    if (e.extras & kBias) c.operands({bias}).apart(y, {bias});
+    if (e.extras & kPre) {
+        const Span pre{"pre", a.pre, a.m * a.n * 2};
+        c.operands({pre}).apart(y, {pre});
+        // pre is an output of the forward epilogue: it must miss the inputs too.
+        if (e.extras & kCrossPre) c.apart(pre, {x, w, bias});
     }
-    const size_t pre_bytes = m * n * 2;
-    if (!fits(pre, pre_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: pre runs past the end of the address space",
-                    name);
+    if (e.extras & kResidual) {
+        const Span residual{"residual", a.residual, a.m * a.n * 4};
+        c.operands({residual}).apart(y, {residual});
     }
-    if (overlap(pre, pre_bytes, y, pre_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: y and pre overlap", name);
-    }
-    return FLINT_OK;
-}
-
-// TN: x (k x m) and w (k x n) move in 16-byte chunks along m and n; k, their
-// row count, can be anything from 1 (ref src/api/gemm.cpp:114-129).
-flint_status check_tn_dims(const char* name, size_t m, size_t n, size_t k) {
-    if (k == 0) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: k must be positive", name);
-    }
-    if (m % 8 != 0 || n % 8 != 0) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: %s (%zu) must be a multiple of 8", name,
-                    m % 8 != 0 ? "m" : "n", m % 8 != 0 ? m : n);
-    }
-    if (m > flint::kGemmMaxMN || n > flint::kGemmMaxMN || k > flint::kGemmMaxK) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: %zu x %zu x %zu is too large: m and n can be up to %zu, and k up to %zu",
-                    name, m, n, k, flint::kGemmMaxMN, flint::kGemmMaxK);
-    }
-    return FLINT_OK;
-}
-
-flint_status check_batched(const char* name, void* y, const void* x, const void* w,
-                           size_t batches, size_t m, size_t n, size_t k) {
-    if (batches > flint::kGemmMaxBatches) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: batches (%zu) can be up to %zu", name,
-                    batches, flint::kGemmMaxBatches);
-    }
-    if (m > flint::kGemmBatchedMaxM) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: m (%zu) can be up to %zu", name, m,
-                    flint::kGemmBatchedMaxM);
-    }
-    const flint::Buffer buffers[] = {
-        {"y", y, batches * m * n * 2},
-        {"x", x, batches * m * k * 2},
-        {"w", w, batches * n * k * 2},
-    };
-    return flint::check_buffers(name, buffers, std::size(buffers), 1);
-}
-
-flint_status check_batched_nt_nn(const char* name, bool n_in_chunks, size_t n, size_t k) {
-    if (k == 0 || k % 8 != 0) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: k (%zu) must be a positive multiple of 8",
-                    name, k);
-    }
-    if (n_in_chunks && n % 8 != 0) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: n (%zu) must be a multiple of 8", name, n);
-    }
-    if (n > flint::kGemmMaxMN || k > flint::kGemmMaxK) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: n (%zu) can be up to %zu, and k (%zu) up to %zu",
-                    name, n, flint::kGemmMaxMN, k, flint::kGemmMaxK);
-    }
-    return FLINT_OK;
+    return c.status();
 }
 
 }  // namespace
 
+#define FLINT_VALIDATE(entry, call)                                        \
+    do {                                                                   \
+        if (const flint_status s_ = validate(entry, call); s_ != FLINT_OK) \
+            return s_;                                                     \
+    } while (0)
+
 extern "C" {
+
+// m or n of 0 is an empty product: OK before any check, null pointers
+// included (ref src/api/gemm.cpp:174-176).
 
 FLINT_API flint_status flint_gemm_nt(void* y, const void* x, const void* w, size_t m, size_t n,
                                      size_t k, flint_stream stream) {
     if (m == 0 || n == 0) return FLINT_OK;
-    if (flint_status s = check_nt_nn("flint_gemm_nt", false, y, x, w, m, n, k); s != FLINT_OK) {
-        return s;
-    }
+    FLINT_VALIDATE(kGemmNt, (Call{y, x, w, nullptr, nullptr, nullptr, 1, m, n, k}));
     FLINT_HIP_CHECK(flint::launch_gemm_nt(y, x, w, nullptr, nullptr, flint::Epilogue::kNone, m, n,
                                           k, flint::to_hip(stream)));
     return FLINT_OK;
@@ -161,9 +148,7 @@ FLINT_API flint_status flint_gemm_nt(void* y, const void* x, const void* w, size
 FLINT_API flint_status flint_gemm_nt_bias(void* y, const void* x, const void* w, const void* bias,
                                           size_t m, size_t n, size_t k, flint_stream stream) {
     if (m == 0 || n == 0) return FLINT_OK;
-    constexpr const char* name = "flint_gemm_nt_bias";
-    if (flint_status s = check_nt_nn(name, false, y, x, w, m, n, k); s != FLINT_OK) return s;
-    if (flint_status s = check_bias(name, y, bias, m, n); s != FLINT_OK) return s;
+    FLINT_VALIDATE(kGemmNtBias, (Call{y, x, w, bias, nullptr, nullptr, 1, m, n, k}));
     FLINT_HIP_CHECK(flint::launch_gemm_nt(y, x, w, bias, nullptr, flint::Epilogue::kBias, m, n, k,
                                           flint::to_hip(stream)));
     return FLINT_OK;
@@ -173,20 +158,7 @@ FLINT_API flint_status flint_gemm_nt_bias_gelu(void* y, void* pre, const void* x
                                                const void* bias, size_t m, size_t n, size_t k,
                                                flint_stream stream) {
     if (m == 0 || n == 0) return FLINT_OK;
-    constexpr const char* name = "flint_gemm_nt_bias_gelu";
-    if (flint_status s = check_nt_nn(name, false, y, x, w, m, n, k); s != FLINT_OK) return s;
-    if (flint_status s = check_bias(name, y, bias, m, n); s != FLINT_OK) return s;
-    if (flint_status s = check_pre(name, y, pre, m, n); s != FLINT_OK) return s;
-    const size_t pre_bytes = m * n * 2;
-    if (overlap(pre, pre_bytes, x, m * k * 2)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: pre and x overlap", name);
-    }
-    if (overlap(pre, pre_bytes, w, n * k * 2)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: pre and w overlap", name);
-    }
-    if (overlap(pre, pre_bytes, bias, n * 4)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: pre and bias overlap", name);
-    }
+    FLINT_VALIDATE(kGemmNtBiasGelu, (Call{y, x, w, bias, pre, nullptr, 1, m, n, k}));
     FLINT_HIP_CHECK(flint::launch_gemm_nt(y, x, w, bias, pre, flint::Epilogue::kBiasGelu, m, n, k,
                                           flint::to_hip(stream)));
     return FLINT_OK;
@@ -197,26 +169,7 @@ FLINT_API flint_status flint_gemm_nt_bias_residual(void* y, const void* x, const
                                                    size_t m, size_t n, size_t k,
                                                    flint_stream stream) {
     if (m == 0 || n == 0) return FLINT_OK;
-    constexpr const char* name = "flint_gemm_nt_bias_residual";
-    if (flint_status s = check_nt_nn(name, false, y, x, w, m, n, k, 4); s != FLINT_OK) return s;
-    if (n % 2 != 0) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: n (%zu) must be even", name, n);
-    }
-    if (flint_status s = check_bias(name, y, bias, m, n, 4); s != FLINT_OK) return s;
-    if (residual == nullptr) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: residual is null", name);
-    }
-    if (!aligned16(residual)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: residual is not 16-byte aligned", name);
-    }
-    const size_t residual_bytes = m * n * 4;
-    if (!fits(residual, residual_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: residual runs past the end of the address space", name);
-    }
-    if (overlap(y, residual_bytes, residual, residual_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: y and residual overlap", name);
-    }
+    FLINT_VALIDATE(kGemmNtBiasResidual, (Call{y, x, w, bias, nullptr, residual, 1, m, n, k}));
     FLINT_HIP_CHECK(flint::launch_gemm_nt(y, x, w, bias, const_cast<void*>(residual),
                                           flint::Epilogue::kBiasResidual, m, n, k,
                                           flint::to_hip(stream)));
@@ -226,9 +179,7 @@ FLINT_API flint_status flint_gemm_nt_bias_residual(void* y, const void* x, const
 FLINT_API flint_status flint_gemm_nn(void* y, const void* x, const void* w, size_t m, size_t n,
                                      size_t k, flint_stream stream) {
     if (m == 0 || n == 0) return FLINT_OK;
-    if (flint_status s = check_nt_nn("flint_gemm_nn", true, y, x, w, m, n, k); s != FLINT_OK) {
-        return s;
-    }
+    FLINT_VALIDATE(kGemmNn, (Call{y, x, w, nullptr, nullptr, nullptr, 1, m, n, k}));
     FLINT_HIP_CHECK(flint::launch_gemm_nn(y, x, w, nullptr, flint::Epilogue::kNone, m, n, k,
                                           flint::to_hip(stream)));
     return FLINT_OK;
@@ -238,23 +189,19 @@ FLINT_API flint_status flint_gemm_nn_dgelu(void* y, const void* x, const void* w
                                            const void* pre, size_t m, size_t n, size_t k,
                                            flint_stream stream) {
     if (m == 0 || n == 0) return FLINT_OK;
-    constexpr const char* name = "flint_gemm_nn_dgelu";
-    if (flint_status s = check_nt_nn(name, true, y, x, w, m, n, k); s != FLINT_OK) return s;
-    if (flint_status s = check_pre(name, y, pre, m, n); s != FLINT_OK) return s;
+    FLINT_VALIDATE(kGemmNnDGelu, (Call{y, x, w, nullptr, pre, nullptr, 1, m, n, k}));
     FLINT_HIP_CHECK(flint::launch_gemm_nn(y, x, w, pre, flint::Epilogue::kDGelu, m, n, k,
                                           flint::to_hip(stream)));
     return FLINT_OK;
 }
 
 FLINT_API flint_status flint_gemm_tn_workspace(size_t m, size_t n, size_t k, size_t* bytes) {
-    if (bytes == nullptr) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "flint_gemm_tn_workspace: bytes is null");
-    }
+    Checker c("flint_gemm_tn_workspace");
+    if (!c.require(bytes != nullptr, "bytes is null").ok()) return c.status();
     *bytes = 0;
     if (m == 0 || n == 0) return FLINT_OK;
-    if (flint_status s = check_tn_dims("flint_gemm_tn_workspace", m, n, k); s != FLINT_OK) {
-        return s;
-    }
+    tn_sizes(c, Call{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1, m, n, k});
+    if (!c.ok()) return c.status();
     FLINT_HIP_CHECK(flint::gemm_tn_workspace(m, n, k, bytes));
     return FLINT_OK;
 }
@@ -263,48 +210,19 @@ FLINT_API flint_status flint_gemm_tn(void* y, const void* x, const void* w, size
                                      size_t k, int accumulate, void* workspace,
                                      size_t workspace_bytes, flint_stream stream) {
     if (m == 0 || n == 0) return FLINT_OK;
-    constexpr const char* name = "flint_gemm_tn";
-    if (flint_status s = check_tn_dims(name, m, n, k); s != FLINT_OK) return s;
-    if (y == nullptr || x == nullptr || w == nullptr) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: %s is null", name,
-                    y == nullptr ? "y" : x == nullptr ? "x" : "w");
-    }
-    if (!aligned16(y) || !aligned16(x) || !aligned16(w)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: %s is not 16-byte aligned", name,
-                    !aligned16(y) ? "y" : !aligned16(x) ? "x" : "w");
-    }
-    const size_t y_bytes = m * n * 4;
-    const size_t x_bytes = k * m * 2;
-    const size_t w_bytes = k * n * 2;
-    if (!fits(y, y_bytes) || !fits(x, x_bytes) || !fits(w, w_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: %s runs past the end of the address space",
-                    name, !fits(y, y_bytes) ? "y" : !fits(x, x_bytes) ? "x" : "w");
-    }
-    if (overlap(y, y_bytes, x, x_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: y and x overlap", name);
-    }
-    if (overlap(y, y_bytes, w, w_bytes)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: y and w overlap", name);
-    }
+    const Call call{y, x, w, nullptr, nullptr, nullptr, 1, m, n, k};
+    FLINT_VALIDATE(kGemmTn, call);
     size_t needed = 0;
     FLINT_HIP_CHECK(flint::gemm_tn_workspace(m, n, k, &needed));
+    Checker c(kGemmTn.name);
+    c.workspace(workspace, workspace_bytes, needed);
     if (needed > 0) {
-        if (workspace == nullptr || workspace_bytes < needed) {
-            return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: needs %zu bytes of workspace, given %zu",
-                        name, needed, workspace == nullptr ? size_t{0} : workspace_bytes);
-        }
-        if (!aligned16(workspace)) {
-            return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: workspace is not 16-byte aligned", name);
-        }
-        if (!fits(workspace, needed)) {
-            return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                        "%s: workspace runs past the end of the address space", name);
-        }
-        if (overlap(workspace, needed, y, y_bytes) || overlap(workspace, needed, x, x_bytes) ||
-            overlap(workspace, needed, w, w_bytes)) {
-            return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: workspace overlaps y, x or w", name);
-        }
+        const Span ws{"workspace", workspace, needed};
+        c.require(!ws.meets({"y", y, m * n * 4}) && !ws.meets({"x", x, k * m * 2}) &&
+                      !ws.meets({"w", w, k * n * 2}),
+                  "workspace overlaps y, x or w");
     }
+    if (!c.ok()) return c.status();
     FLINT_HIP_CHECK(flint::launch_gemm_tn(y, x, w, m, n, k, accumulate != 0, workspace,
                                           flint::to_hip(stream)));
     return FLINT_OK;
@@ -314,13 +232,7 @@ FLINT_API flint_status flint_gemm_nt_batched(void* y, const void* x, const void*
                                              size_t m, size_t n, size_t k, float scale,
                                              flint_stream stream) {
     if (batches == 0 || m == 0 || n == 0) return FLINT_OK;
-    constexpr const char* name = "flint_gemm_nt_batched";
-    if (flint_status s = check_batched_nt_nn(name, false, n, k); s != FLINT_OK) return s;
-    if (!std::isfinite(scale)) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: scale (%g) must be finite", name,
-                    static_cast<double>(scale));
-    }
-    if (flint_status s = check_batched(name, y, x, w, batches, m, n, k); s != FLINT_OK) return s;
+    FLINT_VALIDATE(kGemmNtBatched, (Call{y, x, w, nullptr, nullptr, nullptr, batches, m, n, k, scale}));
     FLINT_HIP_CHECK(flint::launch_gemm_nt_batched(y, x, w, batches, m, n, k, scale,
                                                   flint::to_hip(stream)));
     return FLINT_OK;
@@ -329,9 +241,7 @@ FLINT_API flint_status flint_gemm_nt_batched(void* y, const void* x, const void*
 FLINT_API flint_status flint_gemm_nn_batched(void* y, const void* x, const void* w, size_t batches,
                                              size_t m, size_t n, size_t k, flint_stream stream) {
     if (batches == 0 || m == 0 || n == 0) return FLINT_OK;
-    constexpr const char* name = "flint_gemm_nn_batched";
-    if (flint_status s = check_batched_nt_nn(name, true, n, k); s != FLINT_OK) return s;
-    if (flint_status s = check_batched(name, y, x, w, batches, m, n, k); s != FLINT_OK) return s;
+    FLINT_VALIDATE(kGemmNnBatched, (Call{y, x, w, nullptr, nullptr, nullptr, batches, m, n, k}));
     FLINT_HIP_CHECK(flint::launch_gemm_nn_batched(y, x, w, batches, m, n, k,
                                                   flint::to_hip(stream)));
     return FLINT_OK;
@@ -340,9 +250,7 @@ FLINT_API flint_status flint_gemm_nn_batched(void* y, const void* x, const void*
 FLINT_API flint_status flint_gemm_tn_batched(void* y, const void* x, const void* w, size_t batches,
                                              size_t m, size_t n, size_t k, flint_stream stream) {
     if (batches == 0 || m == 0 || n == 0) return FLINT_OK;
-    constexpr const char* name = "flint_gemm_tn_batched";
-    if (flint_status s = check_tn_dims(name, m, n, k); s != FLINT_OK) return s;
-    if (flint_status s = check_batched(name, y, x, w, batches, m, n, k); s != FLINT_OK) return s;
+    FLINT_VALIDATE(kGemmTnBatched, (Call{y, x, w, nullptr, nullptr, nullptr, batches, m, n, k}));
     FLINT_HIP_CHECK(flint::launch_gemm_tn_batched(y, x, w, batches, m, n, k,
                                                   flint::to_hip(stream)));
     return FLINT_OK;

@@ -23,7 +23,7 @@
 #include <string>
 #include <vector>
 
-#include "common/common.h"
+#include "common/args.h"
 #include "kernels/kernels.h"
 
 using flint::fail;
@@ -663,14 +663,14 @@ FLINT_API flint_status flint_gpt2_forward(flint_gpt2* model, const void* tokens,
     const flint_gpt2& m = *model;
     const flint_gpt2_config& c = m.cfg;
     const size_t rows = m.rows;
-    const flint::Buffer buffers[] = {
-        {"logits", m.logits, rows * c.padded_vocab * 2},
-        {"dlogits", m.dlogits, rows * c.padded_vocab * 2},
-        {"row_loss", m.row_loss, rows * 4},
-        {"tokens", tokens, rows * 2},
-        {"targets", targets, rows * 2},
-    };
-    FLINT_TRY(flint::check_buffers(name, buffers, std::size(buffers), 3));
+    FLINT_TRY(flint::Checker(name)
+                  .buffers({{"logits", m.logits, rows * c.padded_vocab * 2},
+                            {"dlogits", m.dlogits, rows * c.padded_vocab * 2},
+                            {"row_loss", m.row_loss, rows * 4},
+                            {"tokens", tokens, rows * 2},
+                            {"targets", targets, rows * 2}},
+                           3)
+                  .status());
     FLINT_TRY(flint_embedding_forward(m.layers[0].s.x_in, tokens, m.wte->data, m.wpe->data,
                                       c.sequences, c.length, c.padded_vocab, c.width, stream));
     for (const Layer& L : m.layers) FLINT_TRY(forward_layer(m, L, stream));
@@ -691,19 +691,17 @@ FLINT_API flint_status flint_gpt2_backward(flint_gpt2* model, const void* tokens
                     name);
     }
     const size_t rows = m.rows, w = c.width;
-    const flint::Buffer buffers[] = {
-        {"logits", m.logits, rows * c.padded_vocab * 2},
-        {"dlogits", m.dlogits, rows * c.padded_vocab * 2},
-        {"row_loss", m.row_loss, rows * 4},
-        {"tokens", tokens, rows * 2},
-    };
-    FLINT_TRY(flint::check_buffers(name, buffers, std::size(buffers), 3));
-    for (const Param& p : m.params) {
-        if (flint::overlap(tokens, rows * 2, p.grad, p.rows * p.cols * 4)) {
-            return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: tokens and the gradient of %s overlap",
-                        name, p.name.c_str());
-        }
-    }
+    flint::Checker check(name);
+    check.buffers({{"logits", m.logits, rows * c.padded_vocab * 2},
+                   {"dlogits", m.dlogits, rows * c.padded_vocab * 2},
+                   {"row_loss", m.row_loss, rows * 4},
+                   {"tokens", tokens, rows * 2}},
+                  3);
+    const flint::Span tok{"tokens", tokens, rows * 2};
+    for (const Param& p : m.params)
+        check.require(!tok.meets({"grad", p.grad, p.rows * p.cols * 4}),
+                      "tokens and the gradient of %s overlap", p.name.c_str());
+    FLINT_TRY(check.status());
     // Output layer (tied to wte): dwte (+)= dlogits^T h_f; dh = dlogits wte.
     FLINT_TRY(weight_grad(m, *m.wte, m.dlogits, m.h_f, accumulate, stream));
     FLINT_TRY(flint_gemm_nn(m.dh, m.dlogits, m.wte_half, rows, w, c.padded_vocab, stream));

@@ -2,12 +2,13 @@
 // checks, the cut of every tensor into chunks, and the launches of
 // kernels/optimizer.hip. No counterpart in the reference's ABI; the step it
 // implements is ref scripts/gpt2_torch.py:161-192 with the constants at :37-42.
+#include <algorithm>
 #include <cmath>
-#include <iterator>
+#include <cstdint>
 #include <string>
 #include <vector>
 
-#include "common/common.h"
+#include "common/args.h"
 #include "kernels/kernels.h"
 
 using flint::fail;
@@ -50,6 +51,46 @@ flint_status check_options(const char* name, const flint_adamw_options* o) {
     return FLINT_OK;
 }
 
+// No buffer of one tensor may overlap a buffer of another: a tensor listed
+// twice (a tied weight passed for both uses) would be stepped twice, and two
+// tensors sharing moments would race inside one launch. Each tensor's own
+// buffers are checked apart already, so after sorting all ranges by address
+// a range that overlaps any earlier one overlaps the earlier range reaching
+// furthest, which then belongs to another tensor.
+flint_status check_apart(const char* name, const flint_adamw_tensor* tensors, size_t count) {
+    struct Range {
+        uintptr_t begin, end;
+        size_t tensor;
+        const char* what;
+    };
+    std::vector<Range> ranges;
+    ranges.reserve(count * 5);
+    for (size_t i = 0; i < count; ++i) {
+        const flint_adamw_tensor& t = tensors[i];
+        if (t.count == 0) continue;
+        const auto add = [&](const void* p, size_t bytes, const char* what) {
+            if (p != nullptr) {
+                const uintptr_t b = reinterpret_cast<uintptr_t>(p);
+                ranges.push_back({b, b + bytes, i, what});
+            }
+        };
+        add(t.param, t.count * 4, "param");
+        add(t.exp_avg, t.count * 4, "exp_avg");
+        add(t.exp_avg_sq, t.count * 4, "exp_avg_sq");
+        add(t.param_half, t.count * 2, "param_half");
+        add(t.grad, t.count * 4, "grad");
+    }
+    std::sort(ranges.begin(), ranges.end(), [](const Range& a, const Range& b) { return a.begin < b.begin; });
+    const Range* reach = nullptr;
+    for (const Range& r : ranges) {
+        if (reach != nullptr && r.begin < reach->end && r.tensor != reach->tensor)
+            return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: tensor %zu's %s and tensor %zu's %s overlap", name,
+                        reach->tensor, reach->what, r.tensor, r.what);
+        if (reach == nullptr || r.end > reach->end) reach = &r;
+    }
+    return FLINT_OK;
+}
+
 }  // namespace
 
 FLINT_API flint_status flint_adamw_defaults(flint_adamw_options* options) {
@@ -62,8 +103,9 @@ FLINT_API flint_status flint_train_state_init(void* state, float loss_scale, fli
     constexpr const char* name = "flint_train_state_init";
     if (!(loss_scale > 0) || !std::isfinite(loss_scale))
         return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: loss_scale must be positive and finite", name);
-    const flint::Buffer buffers[] = {{"state", state, sizeof(flint_train_state)}};
-    if (flint_status s = flint::check_buffers(name, buffers, std::size(buffers), 1); s != FLINT_OK) return s;
+    if (flint_status s = flint::Checker(name).buffers({{"state", state, sizeof(flint_train_state)}}, 1).status();
+        s != FLINT_OK)
+        return s;
     FLINT_HIP_CHECK(flint::launch_train_state_init(state, loss_scale, flint::to_hip(stream)));
     return FLINT_OK;
 }
@@ -88,17 +130,18 @@ FLINT_API flint_status flint_adamw_step(const flint_adamw_tensor* tensors, size_
     if (workspace_bytes < needed)
         return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: needs %zu bytes of workspace, given %zu", name, needed,
                     workspace_bytes);
-    {
-        const flint::Buffer shared[] = {{"state", state, sizeof(flint_train_state)}, {"workspace", workspace, needed}};
-        if (flint_status s = flint::check_buffers(name, shared, std::size(shared), 2); s != FLINT_OK) return s;
-    }
+    if (flint_status s = flint::Checker(name)
+                             .buffers({{"state", state, sizeof(flint_train_state)}, {"workspace", workspace, needed}}, 2)
+                             .status();
+        s != FLINT_OK)
+        return s;
     // Each tensor's buffers: aligned, in range, the outputs apart from each
     // other, from the gradient, and from the state and workspace.
     for (size_t i = 0; i < count; ++i) {
         const flint_adamw_tensor& t = tensors[i];
         if (t.count == 0) continue;
         const size_t b4 = t.count * 4;
-        flint::Buffer buffers[7] = {
+        flint::Span buffers[7] = {
             {"param", t.param, b4},           {"exp_avg", t.exp_avg, b4}, {"exp_avg_sq", t.exp_avg_sq, b4},
             {"param_half", t.param_half, t.count * 2}, {"grad", t.grad, b4},
             {"state", state, sizeof(flint_train_state)}, {"workspace", workspace, needed},
@@ -111,11 +154,12 @@ FLINT_API flint_status flint_adamw_step(const flint_adamw_tensor* tensors, size_
             outputs = 3;
         }
         const size_t n = t.param_half == nullptr ? 6 : 7;
-        if (flint_status s = flint::check_buffers(name, buffers, n, outputs); s != FLINT_OK) {
+        if (flint_status s = flint::Checker(name).buffers(buffers, n, outputs).status(); s != FLINT_OK) {
             const std::string why = flint_last_error();
             return fail(s, "%s (tensor %zu)", why.c_str(), i);
         }
     }
+    if (flint_status s = check_apart(name, tensors, count); s != FLINT_OK) return s;
     if (chunks == 0) return FLINT_OK;
     const hipStream_t st = flint::to_hip(stream);
 

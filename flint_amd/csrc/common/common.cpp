@@ -1,13 +1,19 @@
 #include "common/common.h"
 
+#include <array>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
-#include <mutex>
 
 namespace {
 
-// Long enough for every message this library writes; longer ones truncate.
-thread_local char last_error[512] = "";
+// This thread's last message; 512 bytes hold every message the library writes.
+thread_local std::array<char, 512> g_message{};
+
+// Compute units per device ordinal (0 = not read yet). A race between two
+// first readers stores the same value twice.
+constexpr int kDevices = 64;
+std::array<std::atomic<int>, kDevices> g_cus{};
 
 }  // namespace
 
@@ -16,78 +22,48 @@ namespace flint {
 flint_status fail(flint_status status, const char* format, ...) {
     va_list args;
     va_start(args, format);
-    std::vsnprintf(last_error, sizeof last_error, format, args);
+    std::vsnprintf(g_message.data(), g_message.size(), format, args);
     va_end(args);
     return status;
 }
 
-flint_status check_buffers(const char* function, const Buffer* buffers, size_t count,
-                           size_t outputs) {
-    for (size_t i = 0; i < count; ++i) {
-        const Buffer& b = buffers[i];
-        if (b.pointer == nullptr) {
-            return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: %s is null", function, b.name);
-        }
-        if (!aligned16(b.pointer)) {
-            return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: %s is not 16-byte aligned", function,
-                        b.name);
-        }
-        if (!fits(b.pointer, b.bytes)) {
-            return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                        "%s: %s runs past the end of the address space", function, b.name);
-        }
-    }
-    for (size_t i = 0; i < outputs; ++i) {
-        for (size_t j = i + 1; j < count; ++j) {
-            if (overlap(buffers[i].pointer, buffers[i].bytes, buffers[j].pointer,
-                        buffers[j].bytes)) {
-                return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: %s and %s overlap", function,
-                            buffers[i].name, buffers[j].name);
-            }
-        }
-    }
-    return FLINT_OK;
+flint_status hip_failure(hipError_t error, const char* file, int line) {
+    (void)hipGetLastError();
+    return fail(FLINT_ERROR_CUDA, "%s: %s (%s:%d)", hipGetErrorName(error),
+                hipGetErrorString(error), file, line);
 }
 
 hipError_t device_cus(int* cus) {
-    static std::mutex lock;
-    static int cached[64] = {};
     int device = 0;
-    hipError_t e = hipGetDevice(&device);
-    if (e != hipSuccess) return e;
-    if (device >= 0 && device < 64) {
-        std::lock_guard<std::mutex> guard(lock);
-        if (cached[device] == 0) {
-            int n = 0;
-            e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
-            if (e != hipSuccess) return e;
-            cached[device] = n;
+    if (const hipError_t e = hipGetDevice(&device); e != hipSuccess) return e;
+    const bool cached = device >= 0 && device < kDevices;
+    if (cached) {
+        if (const int known = g_cus[device].load(std::memory_order_relaxed); known > 0) {
+            *cus = known;
+            return hipSuccess;
         }
-        *cus = cached[device];
-        return hipSuccess;
     }
-    return hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, device);
+    int n = 0;
+    if (const hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device);
+        e != hipSuccess)
+        return e;
+    if (cached) g_cus[device].store(n, std::memory_order_relaxed);
+    *cus = n;
+    return hipSuccess;
 }
 
 }  // namespace flint
 
 extern "C" {
 
-FLINT_API const char* flint_last_error(void) { return last_error; }
+FLINT_API const char* flint_last_error(void) { return g_message.data(); }
 
 FLINT_API const char* flint_version(void) { return "0.1.0"; }
 
 FLINT_API const char* flint_status_string(flint_status status) {
-    switch (status) {
-    case FLINT_OK:
-        return "ok";
-    case FLINT_ERROR_INVALID_ARGUMENT:
-        return "invalid argument";
-    case FLINT_ERROR_CUDA:
-        return "CUDA error";
-    default:
-        return "unknown status";
-    }
+    static const char* const kNames[] = {"ok", "invalid argument", "CUDA error"};
+    const int i = static_cast<int>(status);
+    return i >= 0 && i < 3 ? kNames[i] : "unknown status";
 }
 
 }  // extern "C"

@@ -53,6 +53,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <type_traits>
 
 #include "common/common.h"
 #include "kernels/gemm_common.h"
@@ -67,6 +68,16 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int cap63(int n) { return n < 63 ? n : 63; }
+
+// The two 4-half results of a pair of ds_read_b64_tr_b16, k 0..3 and 4..7.
+struct TrFrag {
+    i32x2 lo, hi;
+};
+__device__ __forceinline__ f16x8 as_f16x8(const f16x8& v) { return v; }
+__device__ __forceinline__ f16x8 as_f16x8(const TrFrag& f) {
+    return __builtin_shufflevector(__builtin_bit_cast(f16x4, f.lo), __builtin_bit_cast(f16x4, f.hi), 0,
+                                   1, 2, 3, 4, 5, 6, 7);
+}
 
 // Cache policy of the epilogue's stores: non-temporal (the nt bit). Outputs
 // are written once and read by a later kernel, not by this one; marked as
@@ -199,6 +210,12 @@ gemm_pipe(Operands op, TileArgs ta) {
     // are k-major ([32 k][rows] in LDS) or row-major ([rows][32 k]).
     constexpr bool kXM = L == Layout::kTN;
     constexpr bool kWM = L != Layout::kNT;
+    // A k-major fragment stays as the two halves its transposing reads wrote
+    // until the MFMA that uses it (after the lgkmcnt wait): joining them
+    // earlier could make the compiler copy registers the reads have not
+    // filled yet, since it cannot see that asm results are still in flight.
+    using XFrag = std::conditional_t<kXM, TrFrag, f16x8>;
+    using WFrag = std::conditional_t<kWM, TrFrag, f16x8>;
     constexpr bool kBias =
         ST == Store::kBias || ST == Store::kBiasGelu || ST == Store::kBiasResidual;
     using E = PipeEpi<WTN, ST, pipe_compact<BM, BN, S, BK, ST>()>;
@@ -392,11 +409,10 @@ gemm_pipe(Operands op, TileArgs ta) {
         const int k = kk * 16 + 8 * fc + (j >> 2);
         const unsigned a0 = unsigned(reinterpret_cast<uintptr_t>(
             (lds_half*)(region + k * rows + chunk)));
-        i32x2 lo, hi;
-        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo) : "v"(a0));
-        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(hi) : "v"(a0), "i"(4 * rows * 2));
-        return __builtin_shufflevector(__builtin_bit_cast(f16x4, lo), __builtin_bit_cast(f16x4, hi),
-                                       0, 1, 2, 3, 4, 5, 6, 7);
+        TrFrag f;
+        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(f.lo) : "v"(a0));
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(f.hi) : "v"(a0), "i"(4 * rows * 2));
+        return f;
     };
     // lgkmcnt(0) before a sub-step whose fragments include asm reads.
     auto wait_frags = [&]() {
@@ -407,24 +423,26 @@ gemm_pipe(Operands op, TileArgs ta) {
         }
     };
     // Fragment read idx (< FM: an x fragment, else a w fragment) of sub-step kk.
-    auto read_one = [&](int st, int kk, int idx, f16x8 (&xf)[FM], f16x8 (&wf)[FN]) {
+    auto read_one = [&](int st, int kk, int idx, XFrag (&xf)[FM], WFrag (&wf)[FN]) {
         const _Float16* s0 = stage(st);
         if (idx < FM) {
             const int r0 = wm * WTM + idx * 32;
-            xf[idx] = kXM ? frag_kmajor(s0, BM, r0, kk) : frag_rowmajor(s0, r0, kk);
+            if constexpr (kXM) xf[idx] = frag_kmajor(s0, BM, r0, kk);
+            else xf[idx] = frag_rowmajor(s0, r0, kk);
         } else {
             const int r0 = wn * WTN + (idx - FM) * 32;
-            wf[idx - FM] = kWM ? frag_kmajor(s0 + BM * BK, BN, r0, kk)
-                               : frag_rowmajor(s0 + BM * BK, r0, kk);
+            if constexpr (kWM) wf[idx - FM] = frag_kmajor(s0 + BM * BK, BN, r0, kk);
+            else wf[idx - FM] = frag_rowmajor(s0 + BM * BK, r0, kk);
         }
     };
     // The MFMAs of one k16 sub-step, with `between(q)` after MFMA q; the
     // scheduling fences keep this interleave exactly as written.
-    auto mfmas = [&](f16x8 (&xf)[FM], f16x8 (&wf)[FN], auto&& between) {
+    auto mfmas = [&](XFrag (&xf)[FM], WFrag (&wf)[FN], auto&& between) {
 #pragma unroll
         for (int q = 0; q < FM * FN; ++q) {
             const int i = q / FM, j = q % FM;
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[i], xf[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(wf[i]), as_f16x8(xf[j]),
+                                                               acc[i][j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             between(q);
             __builtin_amdgcn_sched_barrier(0);
@@ -447,7 +465,8 @@ gemm_pipe(Operands op, TileArgs ta) {
     wait_vm_lgkm0<(S - 2) * PER + POST>();
     block_sync();
 
-    f16x8 xf[2][FM], wf[2][FN];
+    XFrag xf[2][FM];
+    WFrag wf[2][FN];
 #pragma unroll
     for (int q = 0; q < FM + FN; ++q) read_one(0, 0, q, xf[0], wf[0]);
     int st = 0;

@@ -363,7 +363,7 @@ column_partials_f32(float* __restrict__ partial, const float* __restrict__ dy, s
 }  // namespace
 
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t stream) {
-    if (aligned16(dst) && aligned16(src)) {
+    if ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) % 16 == 0) {
         const size_t vecs = bytes / 16;
         if (vecs > 0) {
             hipLaunchKernelGGL(copy_vec, dim3(grid_for(vecs, 256)), dim3(256), 0, stream,

@@ -13,9 +13,10 @@ header, then `count` uint16 tokens with no padding, so the file is exactly
 
 `write_token_file` writes one; `TokenFile` memory-maps one after checking every
 header field and the size rule; `TokenFile.batch` cuts `sequences` rows of
-`length` tokens starting at a token offset into the int32 `tokens` and
-`targets` (the next token) that flint_gpt2_forward takes, the layout of the
-reference's training loop (B x T tokens, targets shifted by one).
+`length` tokens starting at a token offset into the uint16 `tokens` and
+`targets` (the next token) that flint_gpt2_forward takes (the ABI's token type,
+ref include/flint/flint.h:511-523), the layout of the reference's training loop
+(B x T tokens, targets shifted by one).
 `DataLoader` walks a list of shards in order, batch after batch, moving to the
 next shard when fewer than B*T+1 tokens remain in the current one.
 """
@@ -94,15 +95,17 @@ class TokenFile:
                        if count else np.zeros(0, "<u2"))
 
     def batch(self, offset, sequences, length):
-        """int32 (tokens, targets), each sequences x length, from tokens
-        [offset, offset + sequences * length + 1)."""
+        """uint16 (tokens, targets), each sequences x length and C-contiguous,
+        from tokens [offset, offset + sequences * length + 1): the arrays can be
+        copied to the device as they are and handed to flint_gpt2_forward."""
         need = sequences * length + 1
         if offset < 0 or offset + need > self.count:
             raise TokenFileError(f"{self.path}: a batch of {need} tokens at {offset} runs past {self.count}")
-        chunk = np.asarray(self.tokens[offset:offset + need], dtype=np.int32)
+        chunk = np.asarray(self.tokens[offset:offset + need], dtype=np.uint16)
         if chunk.size and chunk.max() >= VOCAB:
             raise TokenFileError(f"{self.path}: token {int(chunk.max())} is outside the GPT-2 vocabulary")
-        return (chunk[:-1].reshape(sequences, length).copy(), chunk[1:].reshape(sequences, length).copy())
+        return (np.ascontiguousarray(chunk[:-1].reshape(sequences, length)),
+                np.ascontiguousarray(chunk[1:].reshape(sequences, length)))
 
 
 class DataLoader:

@@ -1,6 +1,8 @@
 /* libflint training-step extension for MI355X: AdamW with global gradient
  * clipping and a dynamic loss scale, updating FP32 master weights and their
- * FP16 compute copies in two kernels and no host synchronisation.
+ * FP16 compute copies with no host synchronisation: three kernels (sum of
+ * squares, decide, update), the first and last launched once per group of up
+ * to 64 tensors.
  *
  * No counterpart in the reference's ABI. The reference's training step (ref
  * scripts/gpt2_torch.py:161-192, constants :37-42) runs on PyTorch:

@@ -1,6 +1,12 @@
-"""flint_bench: the command line (CPU: parsing needs no GPU), and quick end-to-end
-runs with their "flint-bench/1" JSON logs (GPU). Mirrors the reference's
-tests/test_bench.py:113-700: the same option errors, defaults and log checks,
+"""flint_bench: its command-line contract (CPU: parsing needs no GPU), quick
+end-to-end runs with their "flint-bench/1" JSON logs (GPU), and the results
+table (CPU).
+
+The command-line contract is written down as data: which options belong to
+which benchmark, the accepted values of each enumerated option, and the shape
+rules of each layout and epilogue. The rejection and acceptance cases are
+generated from those tables, so each rule is stated once. Option names and the
+message texts are the reference harness's interface (ref bench/cli.cpp:222-444),
 with rocBLAS and hipBLASLt as the baselines and amd-smi as the monitor."""
 
 import json
@@ -12,6 +18,7 @@ import pytest
 from flint_amd import flint_lib
 
 EXE = flint_lib.library_path().parent / "flint_bench"
+PREFIX = "flint_bench: "
 
 
 @pytest.fixture(scope="module")
@@ -29,199 +36,144 @@ def first_line(result):
     return result.stderr.splitlines()[0]
 
 
-# ------------------------------------------------------------------ CPU: parsing
+# ------------------------------------------------------------------ CPU: the contract as data
 
-def test_help(exe):
-    result = run(exe, "--help")
-    assert result.returncode == 0, result.stderr
-    assert "usage: flint_bench" in result.stdout
-    for text in ("copy", "mma", "gemm", "--sizes", "--chains", "--shapes", "--layout", "tn", "--epilogue",
-                 "bias", "bias-gelu", "dgelu", "bias-residual", "--lt-algo", "fastest", "first"):
-        assert text in result.stdout
-
-
-def test_unknown_option(exe):
-    result = run(exe, "copy", "--bogus")
-    assert result.returncode == 2
-    assert "unknown option: --bogus" in result.stderr
+BENCHMARKS = ("copy", "mma", "gemm")
+# option -> (the benchmark it belongs to, a value that benchmark accepts)
+OWNED = {"--sizes": ("copy", "1M"), "--chains": ("mma", "4"), "--shapes": ("gemm", "8x8x8"),
+         "--layout": ("gemm", "nt"), "--epilogue": ("gemm", "bias"), "--lt-algo": ("gemm", "first")}
+LAYOUTS = ("nt", "nn", "tn")
+EPILOGUE_LAYOUT = {"none": None, "bias": "nt", "bias-gelu": "nt", "bias-residual": "nt", "dgelu": "nn"}
+PROTOCOL = ("--rounds", "--max-rounds", "--warmup", "--sample-ms", "--allow-busy", "--quick", "--out", "--help")
 
 
-def test_unknown_benchmark(exe):
-    result = run(exe, "nope")
-    assert result.returncode == 2
-    assert "unknown benchmark: nope" in result.stderr
+def both_orders(a, b):
+    """The two orders of two option pairs: the parser checks combinations
+    after reading every option, so the order must not matter."""
+    return [a + b, b + a]
 
 
-def test_no_benchmark(exe):
-    result = run(exe)
-    assert result.returncode == 2
-    assert first_line(result) == "flint_bench: no benchmark given"
-
-
-@pytest.mark.parametrize("option, value, owner", [
-    ("--sizes", "1M", "copy"), ("--chains", "4", "mma"), ("--shapes", "8x8x8", "gemm"),
-    ("--layout", "nt", "gemm"), ("--epilogue", "bias", "gemm"), ("--lt-algo", "first", "gemm"),
-])
-def test_options_rejected_for_other_benchmarks(exe, option, value, owner):
-    for benchmark in ("copy", "mma", "gemm"):
-        if benchmark == owner:
-            continue
-        result = run(exe, benchmark, option, value)
-        assert result.returncode == 2
-        assert first_line(result) == f"flint_bench: {option} applies to {owner} only"
-
-
-def test_bad_chains_rejected(exe):
-    result = run(exe, "mma", "--chains", "5")
-    assert result.returncode == 2
-    assert "--chains" in result.stderr and "'5'" in result.stderr
-
-
-@pytest.mark.parametrize("sizes, reason", [("1X", "not a size"), ("0", "positive"), ("-1", "not a size"),
-                                           ("1M,", "not a size"), ("65G", "too large")])
-def test_bad_sizes_rejected(exe, sizes, reason):
-    result = run(exe, "copy", "--sizes", sizes)
-    assert result.returncode == 2
-    assert first_line(result).startswith("flint_bench: --sizes:") and reason in first_line(result)
-
-
-@pytest.mark.parametrize("value", ["Fastest", "second", "all", "1", ""])
-def test_bad_lt_algo_rejected(exe, value):
-    result = run(exe, "gemm", "--lt-algo", value)
-    assert result.returncode == 2, result.stdout
-    assert first_line(result) == f"flint_bench: --lt-algo: must be fastest or first: '{value}'"
-
-
-def test_lt_algo_accepted_for_gemm(exe):
-    for args in (("--lt-algo", "first"), ("--lt-algo=fastest",), ("--epilogue", "bias", "--lt-algo", "first")):
-        result = run(exe, "gemm", *args, "--help")
-        assert result.returncode == 0, result.stderr
-
-
-@pytest.mark.parametrize("epilogue", ["Bias", "relu", "gelu", "bias_gelu", ""])
-def test_bad_epilogue_rejected(exe, epilogue):
-    result = run(exe, "gemm", "--epilogue", epilogue)
-    assert result.returncode == 2, result.stdout
-    assert first_line(result).startswith("flint_bench: --epilogue:")
-    assert "none, bias, bias-gelu, bias-residual or dgelu" in first_line(result)
-
-
-@pytest.mark.parametrize("epilogue", ["bias", "bias-gelu", "bias-residual"])
-@pytest.mark.parametrize("layout", ["nn", "tn"])
-def test_bias_needs_layout_nt(exe, layout, epilogue):
-    for args in (("--layout", layout, "--epilogue", epilogue), ("--epilogue", epilogue, "--layout", layout)):
-        result = run(exe, "gemm", *args)
-        assert result.returncode == 2, result.stdout
-        assert first_line(result) == f"flint_bench: --epilogue {epilogue} needs --layout nt"
-    for args in (("--layout", "nt", "--epilogue", epilogue), ("--epilogue", epilogue),
-                 ("--layout", layout, "--epilogue", "none")):
-        result = run(exe, "gemm", *args, "--help")
-        assert result.returncode == 0, result.stderr
-
-
-@pytest.mark.parametrize("layout", ["nt", "tn"])
-def test_dgelu_needs_layout_nn(exe, layout):
-    cases = [("--layout", layout, "--epilogue", "dgelu"), ("--epilogue", "dgelu", "--layout", layout)]
-    if layout == "nt":
-        cases.append(("--epilogue", "dgelu"))
-    for args in cases:
-        result = run(exe, "gemm", *args)
-        assert result.returncode == 2, result.stdout
-        assert first_line(result) == "flint_bench: --epilogue dgelu needs --layout nn"
-    for args in (("--layout", "nn", "--epilogue", "dgelu"), ("--epilogue", "dgelu", "--layout", "nn")):
-        assert run(exe, "gemm", *args, "--help").returncode == 0
-
-
-@pytest.mark.parametrize("layout", ["TN", "NN", "nx", ""])
-def test_bad_layout_rejected(exe, layout):
-    result = run(exe, "gemm", "--layout", layout)
-    assert result.returncode == 2, result.stdout
-    assert first_line(result).startswith("flint_bench: --layout:") and "nt, nn or tn" in first_line(result)
-
-
-def test_nn_needs_n_a_multiple_of_8(exe):
-    for args in (("--layout", "nn", "--shapes", "8x12x8"), ("--shapes", "8x12x8", "--layout", "nn")):
-        result = run(exe, "gemm", *args)
-        assert result.returncode == 2, result.stdout
-        assert first_line(result).startswith("flint_bench: --shapes:")
-        assert "N must be a multiple of 8" in first_line(result)
-    assert run(exe, "gemm", "--layout", "nt", "--shapes", "8x12x8", "--help").returncode == 0
-    assert run(exe, "gemm", "--shapes", "8x12x8", "--layout", "nn", "--help").returncode == 2
-
-
-def test_bias_gelu_needs_n_a_multiple_of_8(exe):
-    for args in (("--epilogue", "bias-gelu", "--shapes", "8x12x8"), ("--shapes", "8x12x8", "--epilogue", "bias-gelu")):
-        result = run(exe, "gemm", *args)
-        assert result.returncode == 2, result.stdout
-        assert first_line(result) == (
-            "flint_bench: --shapes: N must be a multiple of 8 with --epilogue bias-gelu: '8x12x8'")
-    assert run(exe, "gemm", "--epilogue", "bias", "--shapes", "8x12x8", "--help").returncode == 0
-
-
-def test_bias_residual_needs_n_even(exe):
-    for args in (("--epilogue", "bias-residual", "--shapes", "8x13x8"),
-                 ("--shapes", "8x13x8", "--epilogue", "bias-residual"),
-                 ("--epilogue", "bias-residual", "--shapes", "8x12x8,8x7x8")):
-        result = run(exe, "gemm", *args)
-        assert result.returncode == 2, result.stdout
-        line = first_line(result)
-        assert line.startswith("flint_bench: --shapes: N must be even with --epilogue bias-residual: '8x")
-        assert line.endswith("x8'")
-    assert run(exe, "gemm", "--epilogue", "bias-residual", "--shapes", "8x14x8,8x2x8", "--help").returncode == 0
-    assert run(exe, "gemm", "--epilogue", "bias", "--shapes", "8x13x8", "--help").returncode == 0
-
-
-@pytest.mark.parametrize("shape, dimension", [("12x8x8", "M"), ("8x12x8", "N"), ("12x12x8", "M")])
-def test_tn_needs_m_and_n_multiples_of_8(exe, shape, dimension):
-    for args in (("--layout", "tn", "--shapes", shape), ("--shapes", shape, "--layout", "tn")):
-        result = run(exe, "gemm", *args)
-        assert result.returncode == 2, result.stdout
-        assert first_line(result).startswith("flint_bench: --shapes:")
-        assert f"{dimension} must be a multiple of 8 with --layout tn" in first_line(result)
-
-
-def test_tn_takes_any_k(exe):
-    result = run(exe, "gemm", "--layout", "tn", "--shapes", "8x8x1001,16x8x1,8x8x65536", "--help")
-    assert result.returncode == 0, result.stderr
+def rejections():
+    """(argv, exact first stderr line or (prefix, substring))."""
+    cases = [((), "no benchmark given"), (("nope",), ("unknown benchmark: nope", "")),
+             (("copy", "--bogus"), ("unknown option: --bogus", ""))]
+    for option, (owner, value) in OWNED.items():
+        for other in BENCHMARKS:
+            if other != owner:
+                cases.append(((other, option, value), f"{option} applies to {owner} only"))
+    for value in ("Fastest", "second", "all", "1", ""):
+        cases.append((("gemm", "--lt-algo", value), f"--lt-algo: must be fastest or first: '{value}'"))
+    for value in ("Bias", "relu", "gelu", "bias_gelu", ""):
+        cases.append((("gemm", "--epilogue", value),
+                      ("--epilogue:", "none, bias, bias-gelu, bias-residual or dgelu")))
+    for value in ("TN", "NN", "nx", ""):
+        cases.append((("gemm", "--layout", value), ("--layout:", "nt, nn or tn")))
+    for epilogue, needs in EPILOGUE_LAYOUT.items():
+        for layout in LAYOUTS:
+            if needs is None or layout == needs:
+                continue
+            for argv in both_orders(("--layout", layout), ("--epilogue", epilogue)):
+                cases.append((("gemm", *argv), f"--epilogue {epilogue} needs --layout {needs}"))
+    cases.append((("gemm", "--epilogue", "dgelu"), "--epilogue dgelu needs --layout nn"))
+    for argv in both_orders(("--layout", "nn"), ("--shapes", "8x12x8")):
+        cases.append((("gemm", *argv), ("--shapes:", "N must be a multiple of 8")))
+    for argv in both_orders(("--epilogue", "bias-gelu"), ("--shapes", "8x12x8")):
+        cases.append((("gemm", *argv),
+                      "--shapes: N must be a multiple of 8 with --epilogue bias-gelu: '8x12x8'"))
+    for shapes in ("8x13x8", "8x12x8,8x7x8"):
+        bad = [s for s in shapes.split(",") if int(s.split("x")[1]) % 2][0]
+        for argv in both_orders(("--epilogue", "bias-residual"), ("--shapes", shapes)):
+            cases.append((("gemm", *argv),
+                          f"--shapes: N must be even with --epilogue bias-residual: '{bad}'"))
+    for shape, dim in (("12x8x8", "M"), ("8x12x8", "N"), ("12x12x8", "M")):
+        for argv in both_orders(("--layout", "tn"), ("--shapes", shape)):
+            cases.append((("gemm", *argv), ("--shapes:", f"{dim} must be a multiple of 8 with --layout tn")))
     for layout in ("nt", "nn"):
-        result = run(exe, "gemm", "--layout", layout, "--shapes", "8x8x1001", "--help")
-        assert result.returncode == 2
-        assert "K must be a multiple of 8" in first_line(result)
-    result = run(exe, "gemm", "--layout", "tn", "--shapes", "8x8x65537", "--help")
-    assert result.returncode == 2
-    assert "limits" in first_line(result)
+        cases.append((("gemm", "--layout", layout, "--shapes", "8x8x1001"), ("--shapes:", "K must be a multiple of 8")))
+    cases.append((("gemm", "--layout", "tn", "--shapes", "8x8x65537"), ("--shapes:", "limits")))
+    for shapes, why in (("8x8", "not a shape"), ("8x8x8x8", "not a shape"), ("axbxc", "not a shape"),
+                        ("8x-8x8", "not a shape"), ("8x 8x8", "not a shape"), ("8x8x8,", "not a shape"),
+                        ("99999999999999999999x8x8", "not a shape"), ("0x8x8", "positive"),
+                        ("8x0x8", "positive"), ("8x8x0", "positive"), ("8x8x12", "multiple of 8"),
+                        ("8388481x8x8", "limits"), ("8x8388481x8", "limits"), ("8x8x65544", "limits")):
+        cases.append((("gemm", "--shapes", shapes), ("--shapes:", why)))
+    for sizes, why in (("1X", "not a size"), ("-1", "not a size"), ("1M,", "not a size"),
+                       ("0", "positive"), ("65G", "too large")):
+        cases.append((("copy", "--sizes", sizes), ("--sizes:", why)))
+    cases.append((("mma", "--chains", "5"), ("--chains", "'5'")))
+    for argv, message in ((("--rounds", "0"), "--rounds: must be between 1 and 1000000: '0'"),
+                          (("--rounds", "x"), "--rounds: not an integer: 'x'"),
+                          (("--rounds", "12", "--max-rounds", "11"), "--max-rounds: 11 is below --rounds 12"),
+                          (("--warmup", "-1"), "--warmup: must not be negative: '-1'"),
+                          (("--sample-ms", "0"), "--sample-ms: must be positive: '0'"),
+                          (("--out=",), "--out: empty path"),
+                          (("--quick=1",), "--quick takes no value"),
+                          (("--rounds",), "--rounds needs a value")):
+        cases.append((("copy", *argv), message))
+    return cases
 
 
-@pytest.mark.parametrize("shapes, reason", [
-    ("8x8", "not a shape"), ("8x8x8x8", "not a shape"), ("axbxc", "not a shape"), ("8x-8x8", "not a shape"),
-    ("8x 8x8", "not a shape"), ("8x8x8,", "not a shape"), ("0x8x8", "positive"), ("8x0x8", "positive"),
-    ("8x8x0", "positive"), ("8x8x12", "multiple of 8"), ("8388481x8x8", "limits"), ("8x8388481x8", "limits"),
-    ("8x8x65544", "limits"), ("99999999999999999999x8x8", "not a shape"),
-])
-def test_bad_shapes_rejected(exe, shapes, reason):
-    result = run(exe, "gemm", "--shapes", shapes)
+def acceptances():
+    """argv lists the parser takes (checked with --help, so nothing runs)."""
+    ok = [("gemm", "--lt-algo", "first"), ("gemm", "--lt-algo=fastest"),
+          ("gemm", "--epilogue", "bias", "--lt-algo", "first"),
+          ("gemm", "--layout", "nt", "--shapes", "8x12x8"),
+          ("gemm", "--epilogue", "bias", "--shapes", "8x12x8"),
+          ("gemm", "--epilogue", "bias-residual", "--shapes", "8x14x8,8x2x8"),
+          ("gemm", "--epilogue", "bias", "--shapes", "8x13x8"),
+          ("gemm", "--layout", "tn", "--shapes", "8x8x1001,16x8x1,8x8x65536"),
+          ("gemm", "--shapes", "8388480x8388480x65536,1x8x8")]
+    for epilogue, needs in EPILOGUE_LAYOUT.items():
+        layouts = LAYOUTS if needs is None else (needs,)
+        for layout in layouts:
+            ok.extend(("gemm", *argv) for argv in both_orders(("--layout", layout), ("--epilogue", epilogue)))
+    ok.append(("gemm", "--epilogue", "bias"))
+    return ok
+
+
+def _id(argv):
+    return " ".join(argv) or "(none)"
+
+
+@pytest.mark.parametrize("argv,expect", rejections(), ids=[_id(a) for a, _ in rejections()])
+def test_the_parser_rejects(exe, argv, expect):
+    result = run(exe, *argv)
     assert result.returncode == 2, result.stdout
-    assert first_line(result).startswith("flint_bench: --shapes:") and reason in first_line(result)
+    line = first_line(result)
+    if isinstance(expect, str):
+        assert line == PREFIX + expect
+    else:
+        head, part = expect
+        assert line.startswith(PREFIX + head) and part in line, line
 
 
-def test_shapes_at_the_limits_are_accepted_by_the_parser(exe):
-    assert run(exe, "gemm", "--shapes", "8388480x8388480x65536,1x8x8", "--help").returncode == 0
+@pytest.mark.parametrize("argv", acceptances(), ids=[_id(a) for a in acceptances()])
+def test_the_parser_accepts(exe, argv):
+    result = run(exe, *argv, "--help")
+    assert result.returncode == 0, result.stderr
 
 
-@pytest.mark.parametrize("args, message", [
-    (("--rounds", "0"), "--rounds: must be between 1 and 1000000: '0'"),
-    (("--rounds", "x"), "--rounds: not an integer: 'x'"),
-    (("--rounds", "12", "--max-rounds", "11"), "--max-rounds: 11 is below --rounds 12"),
-    (("--warmup", "-1"), "--warmup: must not be negative: '-1'"),
-    (("--sample-ms", "0"), "--sample-ms: must be positive: '0'"),
-    (("--out=",), "--out: empty path"),
-    (("--quick=1",), "--quick takes no value"),
-    (("--rounds",), "--rounds needs a value"),
-])
-def test_protocol_options_checked(exe, args, message):
-    result = run(exe, "copy", *args)
-    assert result.returncode == 2
-    assert first_line(result) == f"flint_bench: {message}"
+def test_help_names_every_benchmark_option_and_value(exe):
+    result = run(exe, "--help")
+    assert result.returncode == 0 and result.stdout.startswith("usage: flint_bench")
+    words = set(BENCHMARKS) | set(OWNED) | set(PROTOCOL) | set(LAYOUTS) | set(EPILOGUE_LAYOUT)
+    words |= {"fastest", "first"}
+    missing = sorted(w for w in words if w not in result.stdout)
+    assert not missing, missing
+
+
+def test_the_generated_tables_cover_each_rule():
+    """Every owned option is tried with every benchmark that does not own
+    it, and every epilogue with every layout it does not allow."""
+    argvs = [a for a, _ in rejections()]
+    for option, (owner, _) in OWNED.items():
+        assert sum(1 for a in argvs if option in a and a[0] != owner) >= len(BENCHMARKS) - 1
+    pairs = {(a[a.index("--layout") + 1], a[a.index("--epilogue") + 1]) for a in argvs
+             if "--layout" in a and "--epilogue" in a}
+    for epilogue, needs in EPILOGUE_LAYOUT.items():
+        for layout in LAYOUTS:
+            assert ((layout, epilogue) in pairs) == (needs is not None and layout != needs)
+    assert len(set(map(tuple, argvs))) == len(argvs), "duplicate cases"
 
 
 # ------------------------------------------------------------------ GPU: quick runs
@@ -277,12 +229,20 @@ def assert_stats_follow_from_rounds(stats, windows):
     assert stats["seconds"] == pytest.approx(seconds)
     assert stats["samples"] == sum(w["samples"] for w in windows)
     assert stats["failed_reads"] == sum(w["failed_reads"] for w in windows)
+    # Means weigh only the windows that hold a reading; without any they are null.
+    read = [w for w in windows if w["samples"] > 0]
+    read_seconds = sum(w["seconds"] for w in read)
     for name in ("sm_mhz", "mem_mhz", "power_w", "gfx_activity_percent", "power_cap_share", "thermal_share"):
-        assert stats[name] == pytest.approx(sum(w[name] * w["seconds"] for w in windows) / seconds), name
-    assert stats["temp_c_max"] == max(w["temp_c_max"] for w in windows)
+        if not read:
+            assert stats[name] is None, name
+            continue
+        expect = sum(w[name] * w["seconds"] for w in read) / read_seconds
+        assert stats[name] == pytest.approx(expect), name
+    if read:
+        assert stats["temp_c_max"] == max(w["temp_c_max"] for w in read)
     assert stats["new_process"] == any(w["new_process"] for w in windows)
-    # A short (--quick) sample can fall between two of the monitor's ~10 ms
-    # readings; a window that holds readings has a clock and a power.
+    # A window with no reading of its own holds the last one before it, so
+    # once the monitor has read the device every window has a clock.
     for w in windows:
         assert w["samples"] >= 0
         if w["samples"] > 0:

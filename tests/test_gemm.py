@@ -378,3 +378,153 @@ def test_batched_nn_tn_pipe_forced(flint, cuda, monkeypatch, cfg):
     torch.cuda.synchronize()
     ref = torch.bmm(xt.float().transpose(1, 2).contiguous(), w.float())
     assert rel_err(y2.cpu(), ref) <= TOL
+
+
+# the logits head's backward GEMMs at their full size. Both take the
+# 824 MB dlogits as an operand (NN as x, 8192 x 50304 row-major; TN as x, read
+# k-major), the largest buffers on the path; rows / columns are sampled for the
+# FP32 CPU reference.
+LOGITS_ROWS, LOGITS_VOCAB, LOGITS_WIDTH = 8192, 50304, 768
+
+
+def _sampled(count, total, seed):
+    g = torch.Generator().manual_seed(seed)
+    pick = torch.randperm(total, generator=g)[:count].sort().values
+    # The first and last rows of the output are always in: the largest offsets.
+    return torch.unique(torch.cat([pick, torch.tensor([0, total - 1])]))
+
+
+def test_logits_dx_nn_8192x768x50304(flint, cuda):
+    m, n, k = LOGITS_ROWS, LOGITS_WIDTH, LOGITS_VOCAB
+    dlogits = normal((m, k), 40, 1e-2, torch.float16)
+    wte = normal((k, n), 41, 0.02, torch.float16)
+    y = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
+    flint.gemm_nn(y, dlogits.to(cuda), wte.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    rows = _sampled(96, m, 42)
+    got = y.cpu()
+    assert bool(torch.isfinite(got).all())
+    assert rel_err(got[rows], ref_nn(dlogits[rows], wte)) <= TOL
+
+
+def test_logits_dw_tn_50304x768x8192_accumulates(flint, cuda):
+    m, n, k = LOGITS_VOCAB, LOGITS_WIDTH, LOGITS_ROWS
+    dlogits = normal((k, m), 43, 1e-2, torch.float16)       # x: k x m, read transposed
+    h = uniform((k, n), 44)                                   # w: the final LayerNorm's output
+    y0 = normal((m, n), 45)
+    y = y0.to(cuda)
+    flint.gemm_tn(y, dlogits.to(cuda), h.to(cuda), m, n, k, accumulate=True)
+    torch.cuda.synchronize()
+    rows = _sampled(96, m, 46)
+    got = y.cpu()
+    assert bool(torch.isfinite(got).all())
+    ref = dlogits[:, rows].float().T @ h.float() + y0[rows]
+    assert rel_err(got[rows], ref) <= TOL
+    # Every column of every sampled row moved off y0 (a skipped tile would not).
+    assert bool(((got[rows] - y0[rows]) != 0).float().mean() > 0.999)
+
+
+# Memory safety of the stores: every output of every entry point is placed 16,
+# 32 or 48 bytes into an allocation filled with a 16-bit pattern, with 4 KiB of
+# pattern after it; nothing outside the output may change. The shapes leave
+# partial tiles on both edges, and each pipeline configuration is forced in
+# turn (the edge handling differs between tile sizes).
+GUARD = 0x7C5A                      # an FP16 NaN pattern no kernel writes
+GUARD_AFTER = 2048                  # halves
+
+
+def _guarded(count_halves, offset_bytes, cuda):
+    """(allocation, view of count_halves halves offset_bytes in)."""
+    off = offset_bytes // 2
+    buf = torch.full((off + count_halves + GUARD_AFTER,), GUARD - 65536 if GUARD > 32767 else GUARD,
+                     dtype=torch.int16, device=cuda)
+    return buf, buf[off:off + count_halves], off
+
+
+def _assert_guards(name, buf, off, count):
+    b = buf.cpu()
+    pattern = GUARD - 65536 if GUARD > 32767 else GUARD
+    assert bool((b[:off] == pattern).all()), f"{name} wrote before its output"
+    assert bool((b[off + count:] == pattern).all()), f"{name} wrote past its output"
+
+
+GUARD_CASES = ["nt", "nt_bias", "nt_bias_gelu", "nt_bias_residual", "nn", "nn_dgelu", "tn", "tn_acc"]
+
+
+@pytest.mark.parametrize("force", [None, "128,192,3,64", "256,128,3,64", "256,256,3", "256,64,4"])
+@pytest.mark.parametrize("offset", [16, 32, 48])
+@pytest.mark.parametrize("case", GUARD_CASES)
+def test_outputs_stay_inside_their_buffers(flint, cuda, monkeypatch, case, offset, force):
+    if force is not None:
+        monkeypatch.setenv("FLINT_GEMM_PIPE", force)
+    m, n, k = (264, 200, 96) if not case.startswith("tn") else (264, 200, 1000)
+    x = uniform((m, k) if not case.startswith("tn") else (k, m), 50).to(cuda)
+    w_shape = (n, k) if case.startswith("nt") else (k, n)
+    w = uniform(w_shape, 51, -0.1, 0.1).to(cuda)
+    b = normal((n,), 52, 0.02).to(cuda)
+    f32_out = case in ("nt_bias_residual", "tn", "tn_acc")
+    halves = m * n * (2 if f32_out else 1)
+    ybuf, yh, yoff = _guarded(halves, offset, cuda)
+    y = yh.view(torch.float32 if f32_out else torch.float16).view(m, n)
+    if case == "tn_acc":
+        y.copy_(normal((m, n), 53).to(cuda))
+    pbuf, ph, poff = _guarded(m * n, offset, cuda)
+    pre = ph.view(torch.float16).view(m, n)
+    if case == "nn_dgelu":
+        pre.copy_(normal((m, n), 54, 1.0, torch.float16).to(cuda))
+    if case == "nt":
+        flint.gemm_nt(y, x, w, m, n, k)
+        ref = ref_nt(x.cpu(), w.cpu())
+    elif case == "nt_bias":
+        flint.gemm_nt_bias(y, x, w, b, m, n, k)
+        ref = ref_nt(x.cpu(), w.cpu()) + b.cpu()
+    elif case == "nt_bias_gelu":
+        flint.gemm_nt_bias_gelu(y, pre, x, w, b, m, n, k)
+        s = ref_nt(x.cpu(), w.cpu()) + b.cpu()
+        ref = torch.nn.functional.gelu(s.double(), approximate="tanh")
+    elif case == "nt_bias_residual":
+        r = normal((m, n), 55).to(cuda)
+        flint.gemm_nt_bias_residual(y, x, w, b, r, m, n, k)
+        ref = r.cpu() + (ref_nt(x.cpu(), w.cpu()) + b.cpu())
+    elif case == "nn":
+        flint.gemm_nn(y, x, w, m, n, k)
+        ref = ref_nn(x.cpu(), w.cpu())
+    elif case == "nn_dgelu":
+        flint.gemm_nn_dgelu(y, x, w, pre, m, n, k)
+        p = pre.cpu().double()
+        t = torch.tanh(0.7978845608028654 * (p + 0.044715 * p ** 3))
+        gp = 0.5 * (1 + t) + 0.5 * p * (1 - t * t) * 0.7978845608028654 * (1 + 3 * 0.044715 * p * p)
+        ref = ref_nn(x.cpu(), w.cpu()).double() * gp
+    else:
+        y0 = y.cpu().clone()
+        flint.gemm_tn(y, x, w, m, n, k, accumulate=case == "tn_acc")
+        ref = ref_tn(x.cpu(), w.cpu()) + (y0 if case == "tn_acc" else 0)
+    torch.cuda.synchronize()
+    _assert_guards(case, ybuf, yoff, halves)
+    if case in ("nt_bias_gelu", "nn_dgelu"):
+        _assert_guards(case + " pre", pbuf, poff, m * n)
+    assert rel_err(y.cpu(), ref) <= TOL
+
+
+@pytest.mark.parametrize("case", ["nt", "nn", "tn"])
+@pytest.mark.parametrize("side", [True, False], ids=["side-stream", "default-stream"])
+def test_gemm_is_ordered_on_the_given_stream(flint, cuda, case, side):
+    """A GEMM queued behind a long kernel and an input fill on the same stream
+    sees the filled input: the product then equals k exactly."""
+    m = n = k = 64
+    x = torch.zeros((m, k), dtype=torch.float16, device=cuda)
+    w = torch.ones((n, k), dtype=torch.float16, device=cuda)
+    y = torch.zeros((m, n), dtype=torch.float32 if case == "tn" else torch.float16, device=cuda)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream() if side else torch.cuda.current_stream()
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(50_000_000)
+        x.fill_(1)
+        if case == "nt":
+            flint.gemm_nt(y, x, w, m, n, k, stream=stream)
+        elif case == "nn":
+            flint.gemm_nn(y, x, w, m, n, k, stream=stream)
+        else:
+            flint.gemm_tn(y, x, w, m, n, k, stream=stream)
+    stream.synchronize()
+    assert bool((y.float() == k).all())

@@ -89,16 +89,16 @@ def _run(flint, cfg, sequences, length, params, idx, tgt, scale, separate=False)
     return logits, row_loss, dlogits, grads, mean
 
 
-@pytest.mark.parametrize("cfg,sequences,length", [(TINY, 2, 64), (TINY, 3, 32), (ODD, 2, 48)],
-                         ids=["tiny-2x64", "tiny-3x32", "odd-2x48"])
-@pytest.mark.parametrize("trained", [False, True], ids=["init", "trained"])
-def test_forward_and_backward_pass_the_gate(flint, cuda, cfg, sequences, length, trained):
+def _gate_case(flint, cfg, sequences, length, trained, idx=None, tgt=None):
+    """The whole-model gate (forward outputs and every gradient) for one
+    configuration and batch."""
     shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
                                 cfg["padded_vocab"])
     params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=5, trained=trained)
     # Start from FP16-representable masters, so the FP16 copies equal them.
     params = {n: t.half().float() for n, t in params.items()}
-    idx, tgt = _tokens(cfg, sequences, length, 6)
+    if idx is None:
+        idx, tgt = _tokens(cfg, sequences, length, 6)
     rows = sequences * length
     scale = 1024.0 / rows
     ref = G.gradients(params, idx, tgt, cfg, scale)
@@ -119,6 +119,78 @@ def test_forward_and_backward_pass_the_gate(flint, cuda, cfg, sequences, length,
     # mean_loss is the FP64 mean of row_loss.
     assert mean == pytest.approx(float(row_loss.double().mean()), rel=1e-15, abs=0)
     assert abs(mean - float(ref[1].double().mean())) <= 1e-3 * abs(float(ref[1].mean()))
+
+
+@pytest.mark.parametrize("cfg,sequences,length", [(TINY, 2, 64), (TINY, 3, 32), (ODD, 2, 48)],
+                         ids=["tiny-2x64", "tiny-3x32", "odd-2x48"])
+@pytest.mark.parametrize("trained", [False, True], ids=["init", "trained"])
+def test_forward_and_backward_pass_the_gate(flint, cuda, cfg, sequences, length, trained):
+    _gate_case(flint, cfg, sequences, length, trained)
+
+
+# GPT-2 124M itself (configs[4]'s model), at the reference's gate shapes (ref
+# tests/test_gpt2.py:686, :712-715; gradients ref tests/test_gpt2_backward.py:651-653).
+GPT2 = dict(layers=12, heads=12, width=768, block_size=1024, vocab=50257, padded_vocab=50304)
+
+
+@pytest.mark.parametrize("sequences,length", [(2, 256), (1, 1024), (8, 64)],
+                         ids=["2x256", "1x1024", "8x64"])
+@pytest.mark.parametrize("trained", [False, True], ids=["init", "trained"])
+def test_gpt2_124m_passes_the_gate(flint, cuda, sequences, length, trained):
+    _gate_case(flint, GPT2, sequences, length, trained)
+
+
+def test_gpt2_124m_full_batch_properties(flint, cuda):
+    """configs[4]'s own batch, 8 x 1024: every output and gradient finite, two
+    runs equal bit for bit, and the mean loss within 1e-3 of the FP32 CPU
+    model's on the same tokens."""
+    cfg, sequences, length = GPT2, 8, 1024
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=15, trained=False)
+    params = {n: t.half().float() for n, t in params.items()}
+    idx, tgt = _tokens(cfg, sequences, length, 16)
+    scale = 1024.0 / (sequences * length)
+    a = _run(flint, cfg, sequences, length, params, idx, tgt, scale)
+    b = _run(flint, cfg, sequences, length, params, idx, tgt, scale)
+    for x in a[:3]:
+        assert bool(torch.isfinite(x).all())
+    for n, g in a[3].items():
+        assert bool(torch.isfinite(g).all()), n
+        assert bool((g != 0).any()), n
+    for x, y in zip(a[:3], b[:3]):
+        assert torch.equal(x.view(torch.int32) if x.dtype == torch.float32 else x.view(torch.int16),
+                           y.view(torch.int32) if y.dtype == torch.float32 else y.view(torch.int16))
+    for n in a[3]:
+        assert torch.equal(a[3][n].view(torch.int32), b[3][n].view(torch.int32)), n
+    assert a[4] == b[4]
+    with torch.no_grad():
+        _, ref_loss = G.forward(params, idx, tgt, cfg)
+    ref_mean = float(ref_loss.double().mean())
+    print(f"mean loss: flint {a[4]:.6f} FP32 CPU {ref_mean:.6f}")
+    assert abs(a[4] - ref_mean) <= 1e-3 * ref_mean
+
+
+def test_a_token_file_batch_runs_through_the_model(flint, cuda, tmp_path):
+    """FLINTTOK -> DataLoader -> flint_gpt2_forward/backward: the loader's uint16
+    rows go to the device as they are (two bytes a token, the ABI's type) and
+    the model passes the gate on them."""
+    from flint_amd.tokens import DataLoader, write_token_file
+
+    cfg, sequences, length = TINY, 2, 64
+    g = torch.Generator().manual_seed(17)
+    stream = torch.randint(0, cfg["vocab"], (3 * sequences * length + 1,), generator=g)
+    write_token_file(tmp_path / "shard.bin", stream.numpy())
+    loader = DataLoader([tmp_path / "shard.bin"], sequences, length)
+    loader.next_batch()
+    tokens, targets = loader.next_batch()         # the second batch: offset 128
+    assert tokens.dtype == np.uint16 and tokens.shape == (sequences, length)
+    idx = torch.from_numpy(tokens.astype(np.int64))
+    tgt = torch.from_numpy(targets.astype(np.int64))
+    assert torch.equal(idx.reshape(-1), stream[128:256]) and torch.equal(tgt.reshape(-1), stream[129:257])
+    # The device copy of the loader's own bytes is what _dev16 makes of idx.
+    assert torch.equal(torch.from_numpy(tokens.view(np.int16)).reshape(-1).cuda(), _dev16(idx))
+    _gate_case(flint, cfg, sequences, length, True, idx, tgt)
 
 
 def test_parameters_are_named_in_order(flint, cuda):

@@ -176,13 +176,20 @@ def test_softmax_cross_entropy(flint, cuda, rows, vocab, cols):
     flint.softmax_cross_entropy(dl, loss, logits.to(cuda), t16.to(cuda), scale, rows, vocab,
                                 cols)
     torch.cuda.synchronize()
-    pick = torch.arange(0, rows, max(1, rows // 64))
-    ref_loss, ref_d = oracle.cross_entropy64(logits[pick].numpy(), t32[pick].numpy(), vocab, scale)
-    assert rel_err(loss.cpu()[pick], torch.from_numpy(ref_loss)) <= TOL
-    assert rel_err(dl.cpu()[pick], torch.from_numpy(ref_d)) <= TOL
-    el, ed = oracle.cross_entropy(logits[pick].numpy(), t32[pick].numpy(), vocab, scale)
-    same = (dl.cpu()[pick].numpy().view(np.int16) == ed.view(np.int16)).mean()
-    assert same >= 0.999
+    # Every row, in blocks of 512 (the FP64 reference of all 8,192 rows at
+    # once would hold 3.3 GB per array).
+    got_loss, got_d = loss.cpu(), dl.cpu()
+    same = 0
+    for r0 in range(0, rows, 512):
+        pick = torch.arange(r0, min(rows, r0 + 512))
+        ref_loss, ref_d = oracle.cross_entropy64(logits[pick].numpy(), t32[pick].numpy(), vocab,
+                                                 scale)
+        assert rel_err(got_loss[pick], torch.from_numpy(ref_loss)) <= TOL, r0
+        assert rel_err(got_d[pick], torch.from_numpy(ref_d)) <= TOL, r0
+        el, ed = oracle.cross_entropy(logits[pick].numpy(), t32[pick].numpy(), vocab, scale)
+        same += int((got_d[pick].numpy().view(np.int16) == ed.view(np.int16)).sum())
+    assert same >= 0.999 * rows * cols
+    pick = torch.arange(rows)
     # Bit-exact target gather: dlogits at the target carries p - 1 (negative)
     # and every other visible value is >= 0.
     d = dl.cpu()[pick].float()
@@ -190,6 +197,41 @@ def test_softmax_cross_entropy(flint, cuda, rows, vocab, cols):
     assert torch.all(d[torch.arange(len(pick)), tcol] <= 0)
     if cols > vocab:
         assert torch.all(dl.cpu()[:, vocab:] == 0)
+
+
+def test_cross_entropy_target_gather_is_exact(flint, cuda):
+    """Rows whose every logit but the maximum lies more than 104 below it: in
+    FP32 each of their exponentials is exactly 0, so sum = 1, row_loss =
+    max - l_t exactly, dlogits = +scale at the maximum, -scale at the target
+    and 0 elsewhere. The logits of a row are all distinct, so reading any
+    column but the target's gives another loss (ref cross_entropy.cu:145-147,
+    :163-166)."""
+    rows, vocab, cols = 4096, 50257, 50304
+    g = torch.Generator().manual_seed(31)
+    tgt = torch.randint(0, vocab, (rows,), generator=g, dtype=torch.int32)
+    top = (tgt + 1 + torch.randint(0, vocab - 1, (rows,), generator=g, dtype=torch.int32)) % vocab
+    col = torch.arange(cols, dtype=torch.float32)
+    r = torch.arange(rows, dtype=torch.float32)[:, None]
+    # q = (c + 7r) mod 2048 picks one of 2,048 distinct FP16 values: the
+    # binade [128, 256) in steps of 1/8, then [256, 512) in steps of 1/4.
+    q = torch.remainder(col[None, :] + 7 * r, 2048.0)
+    logits = torch.where(q < 1024, -(128.0 + q / 8), -(256.0 + (q - 1024) / 4)).half()
+    assert int((logits[0].float().unique()).numel()) == 2048
+    logits[torch.arange(rows), top.long()] = 3.0
+    dl = torch.empty((rows, cols), dtype=torch.float16, device=cuda)
+    loss = torch.empty(rows, device=cuda)
+    scale = 0.125
+    flint.softmax_cross_entropy(dl, loss, logits.to(cuda), tgt.to(torch.int16).to(cuda), scale, rows,
+                                vocab, cols)
+    torch.cuda.synchronize()
+    lt = logits[torch.arange(rows), tgt.long()].float()
+    expect = 3.0 - lt                      # log(1) - (l_t - max), exact in FP32
+    assert torch.equal(loss.cpu(), expect)
+    d = dl.cpu().float()
+    want = torch.zeros(rows, cols)
+    want[torch.arange(rows), top.long()] = scale
+    want[torch.arange(rows), tgt.long()] = -scale
+    assert torch.equal(d, want)
 
 
 def test_cross_entropy_special_values(flint, cuda):

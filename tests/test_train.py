@@ -145,6 +145,33 @@ def test_misaligned_and_overlapping_buffers_rejected(flint):
         flint.check(flint.lib.flint_adamw_step(flint.adamw_tensors(t), 1, 4096, ctypes.byref(o), 1 << 19, 1024, None))
 
 
+def test_tensors_sharing_memory_are_rejected(flint):
+    """A tensor listed twice, or two tensors whose buffers overlap, would be
+    stepped twice or race on their moments: the step refuses them before any
+    device work (the addresses below are never dereferenced)."""
+    o = flint.adamw_defaults()
+    base = 1 << 24
+
+    def tensor(at, count=64):
+        return {"param": at, "grad": at + 4096, "exp_avg": at + 8192, "exp_avg_sq": at + 12288,
+                "count": count, "weight_decay": 0.0}
+
+    state, ws = 4096, 1 << 22
+
+    def step(ts):
+        flint.check(flint.lib.flint_adamw_step(flint.adamw_tensors(ts), len(ts), state, ctypes.byref(o),
+                                               ws, 1 << 16, None))
+
+    with pytest.raises(FlintError, match="tensor 0's param and tensor 1's param overlap"):
+        step([tensor(base), tensor(base)])
+    # Tensor 1's grad lands inside tensor 0's exp_avg_sq; its other buffers are far away.
+    other = dict(tensor(base + (1 << 20)), grad=base + 12288 + 128)
+    with pytest.raises(FlintError, match="tensor 0's exp_avg_sq and tensor 1's grad overlap"):
+        step([tensor(base), other])
+    # Adjacent tensors (no shared byte) are not run here: the addresses are
+    # not device memory. The GPU tests step real adjacent tensors.
+
+
 # ------------------------------------------------------------------ GPU: parity with the oracle
 
 def to_dev(tensors, cuda, half_skip=2):
