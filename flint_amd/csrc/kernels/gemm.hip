@@ -839,6 +839,8 @@ hipError_t gemm_tn_workspace(size_t m, size_t n, size_t k, size_t* bytes) {
 
 hipError_t launch_gemm_nt(void* y, const void* x, const void* w, const void* bias, void* aux,
                           Epilogue e, size_t m, size_t n, size_t k, hipStream_t stream) {
+    if (gemm_pp_eligible(e, m, n, k))
+        return launch_gemm_pp(e, y, x, w, bias, aux, m, n, k, stream);
     if (gemm_pipe_eligible(GemmLayout::kNT, e, m, n, k))
         return launch_gemm_pipe(GemmLayout::kNT, e, y, x, w, bias, aux, 1.0f, 1, m, n, k, false,
                                 nullptr, 0, stream);

@@ -137,16 +137,33 @@ struct PipeEpi {
 };
 
 constexpr size_t kPipeMaxLds = 160 * 1024;
+constexpr bool is_bias_store(Store st) {
+    return st == Store::kBias || st == Store::kBiasGelu || st == Store::kBiasResidual;
+}
+// Two-stage tiles with 64-deep steps read fragments two sub-steps ahead (four
+// fragment buffers) where the accumulators and buffers fit in 320 registers;
+// their bias then waits in LDS (4 KB, 1 KB per wave) instead of registers.
+__host__ __device__ constexpr bool pipe_look2(int bm, int bn, int s, int bk) {
+    const int wn = pipe_waves_n(bn);
+    const int fm = bm / (4 / wn) / 32, fn = bn / wn / 32;
+    return s == 2 && bk == 64 && fm * fn * 16 + 16 * (fm + fn) <= 320;
+}
+__host__ __device__ constexpr size_t pipe_bias_lds(int bm, int bn, int s, int bk, Store st) {
+    return pipe_look2(bm, bn, s, bk) && is_bias_store(st) ? 4096 : 0;
+}
 // Whether a configuration stages its epilogue compactly (see PipeEpi).
 template <int BM, int BN, int S, int BK, Store ST>
 constexpr bool pipe_compact() {
     using E = PipeEpi<BN / pipe_waves_n(BN), ST>;
-    return size_t(S) * (BM + BN) * BK * 2 + 4 * size_t(E::kHalves) * 2 > kPipeMaxLds;
+    return size_t(S) * (BM + BN) * BK * 2 + 4 * size_t(E::kHalves) * 2 +
+               pipe_bias_lds(BM, BN, S, BK, ST) >
+           kPipeMaxLds;
 }
 template <int BM, int BN, int S, int BK, Layout L, Store ST>
 constexpr size_t pipe_lds_bytes() {
     using E = PipeEpi<BN / pipe_waves_n(BN), ST, pipe_compact<BM, BN, S, BK, ST>()>;
-    return size_t(S) * (BM + BN) * BK * 2 + 4 * size_t(E::kHalves) * 2;
+    return size_t(S) * (BM + BN) * BK * 2 + 4 * size_t(E::kHalves) * 2 +
+           pipe_bias_lds(BM, BN, S, BK, ST);
 }
 
 // Tiles of one slice at or below the diagonal of a causal NT output: row
@@ -225,7 +242,11 @@ gemm_pipe(Operands op, TileArgs ta) {
     static_assert((S - 2) * PER + PER < 64, "vmcnt range");
     // Buffer stores per wave per tile, bias loads per wave per tile.
     constexpr int kStores = FM * E::kSubs * E::kPerLane * E::kPasses;
-    constexpr int kBiasLoads = kBias ? FN * 4 : 0;
+    constexpr bool kLook2 = pipe_look2(BM, BN, S, BK);
+    constexpr bool kBiasLds = kBias && kLook2;
+    // Bias loads per wave per tile: FN * 4 into registers, or one 1 KB load
+    // into the wave's LDS bias block.
+    constexpr int kBiasLoads = kBiasLds ? 1 : (kBias ? FN * 4 : 0);
     // The residual is loaded into registers at tile start where it fits in
     // 128 VGPRs (128 x 192: 96), so that its latency hides under the k-loop.
     constexpr int kResAll = FM * E::kSubs * E::kPerLane;
@@ -233,7 +254,8 @@ gemm_pipe(Operands op, TileArgs ta) {
     constexpr int kEarlyLoads = kBiasLoads + (kResEarly ? kResAll : 0);
     // One LDS object for everything: with a second one, the compiler's LDS-DMA
     // alias tracking put a vmcnt(0) in front of every fragment read.
-    __shared__ __attribute__((aligned(16))) _Float16 lds[kStageHalves + 4 * E::kHalves];
+    __shared__ __attribute__((aligned(16)))
+    _Float16 lds[kStageHalves + 4 * E::kHalves + pipe_bias_lds(BM, BN, S, BK, ST) / 2];
     auto stage = [&](int st) { return lds + st * (BM + BN) * BK; };
 
     const int tid = threadIdx.x;
@@ -465,10 +487,21 @@ gemm_pipe(Operands op, TileArgs ta) {
     wait_vm_lgkm0<(S - 2) * PER + POST>();
     block_sync();
 
-    XFrag xf[2][FM];
-    WFrag wf[2][FN];
+    // Fragment buffers: two (sub-step kk reads kk + 1) with three or more
+    // stages; with two stages, four, indexed by sub-step: kk reads kk + 2, so
+    // the step's stage is read out by the end of sub-step NS - 3 and the
+    // barrier that frees it sits mid-step, leaving two sub-steps to issue the
+    // next step's loads (all of them in one sub-step outran the vector memory
+    // path: ~33 cycles per 1 KB load against 32 per MFMA).
+    constexpr int NB = kLook2 ? 4 : 2;
+    XFrag xf[NB][FM];
+    WFrag wf[NB][FN];
 #pragma unroll
     for (int q = 0; q < FM + FN; ++q) read_one(0, 0, q, xf[0], wf[0]);
+    if constexpr (kLook2) {
+#pragma unroll
+        for (int q = 0; q < FM + FN; ++q) read_one(0, 1, q, xf[1], wf[1]);
+    }
     int st = 0;
     // `cur` is the step whose remaining loads go out in the next sub-steps
     // 0 .. NS - 2.
@@ -477,7 +510,18 @@ gemm_pipe(Operands op, TileArgs ta) {
         // Bias of this lane's columns, for the epilogue: buffer loads with the
         // resource ending at n (columns past it read 0), FN * 4 of them per wave.
         f32x4 bias[kBias ? FN : 1][4];
-        if constexpr (kBias) {
+        float* const bias_lds = reinterpret_cast<float*>(lds + kStageHalves + 4 * E::kHalves) +
+                                wave * 256;
+        if constexpr (kBiasLds) {
+            // One load puts columns col0 .. col0 + 255 of the bias in this
+            // wave's 1 KB block (those past n read 0); the epilogue reads them
+            // back once the k-loop's waits have retired it.
+            const auto rbias = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(op.bias), 0, unsigned(n) * 4u, 0x00020000);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rbias, (__attribute__((address_space(3))) void*)(lds_half*)bias_lds, 16,
+                unsigned(lane) * 16u, unsigned(t.n0 + wn * WTN) * 4u, 0, 0);
+        } else if constexpr (kBias) {
             const auto rbias = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float*>(op.bias), 0, unsigned(n) * 4u, 0x00020000);
 #pragma unroll
@@ -526,6 +570,47 @@ gemm_pipe(Operands op, TileArgs ta) {
         for (int s = 0; s < steps; ++s) {
             Issue nxt = cur;
             advance(nxt);
+          if constexpr (kLook2) {
+            static_assert(NS == 4, "two-stage tiles take 64-deep steps");
+            // Sub-steps 0 and 1: read sub-steps 2 and 3 of this step.
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                wait_frags();
+                mfmas(xf[kk], wf[kk], [&](int q) {
+                    if (q < FM + FN) read_one(st, kk + 2, q, xf[kk + 2], wf[kk + 2]);
+                });
+            }
+            // Step s + 1 (loaded during the second half of the step before)
+            // has landed; at a tile's first step the previous tile's stores
+            // and this tile's bias (and residual) loads, issued after it, may
+            // stay in flight. After the barrier stage st is free.
+            if (s == 0) {
+                if (i == 0) wait_vm_lgkm0<cap63(kEarlyLoads)>();
+                else wait_vm_lgkm0<cap63(kEarlyLoads + kStores)>();
+            } else {
+                wait_vm_lgkm0<0>();
+            }
+            block_sync();
+            const int st_next = st + 1 == S ? 0 : st + 1;
+            // Sub-steps 2 and 3: read sub-steps 0 and 1 of the next step, and
+            // issue the loads of the step after it into stage st, half in each.
+            constexpr int kHalf = (PER + 1) / 2;
+#pragma unroll
+            for (int kk = 2; kk < 4; ++kk) {
+                wait_frags();
+                mfmas(xf[kk], wf[kk], [&](int q) {
+                    if (q < FM + FN) read_one(st_next, kk - 2, q, xf[kk - 2], wf[kk - 2]);
+                    const int li = (kk - 2) * kHalf + q;
+                    if (q < kHalf && li < PER) issue_q(nxt, li);
+                });
+                // Loads without a slot (fewer MFMAs than loads) go out here.
+#pragma unroll
+                for (int q = FM * FN; q < kHalf; ++q)
+                    if ((kk - 2) * kHalf + q < PER) issue_q(nxt, (kk - 2) * kHalf + q);
+            }
+            st = st_next;
+            cur = nxt;
+          } else {
             // Sub-steps 0 .. NS - 2: reads of the sub-step after, the rest of
             // step `cur`'s loads.
 #pragma unroll
@@ -567,10 +652,24 @@ gemm_pipe(Operands op, TileArgs ta) {
             }
             st = st_next;
             cur = nxt;
+          }
         }
 
         // ---- epilogue: per staged block of a wave, registers -> staging ->
         // whole 16-byte row chunks to HBM.
+        // The bias block's load (kBiasLds) retired at the second step's wait;
+        // a one-step tile waits for it here. Its values are read where they
+        // are added, so that they take no registers across the epilogue (the
+        // next tile's first fragments are live there).
+        if constexpr (kBiasLds) {
+            if (steps == 1) wait_vmcnt<0>();
+        }
+        auto bias_of = [&](int ii, int g4) {
+            if constexpr (kBiasLds)
+                return *reinterpret_cast<const f32x4*>(bias_lds + ii * 32 + g4 * 8 + fc * 4);
+            else
+                return bias[ii][g4];
+        };
         const bool accumulate = ST == Store::kTn && !split && op.accumulate;
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
@@ -629,7 +728,7 @@ gemm_pipe(Operands op, TileArgs ta) {
                             for (int g4 = 0; g4 < 4; ++g4) {
                                 f32x4 v = {acc[ii][j][g4 * 4 + 0], acc[ii][j][g4 * 4 + 1],
                                            acc[ii][j][g4 * 4 + 2], acc[ii][j][g4 * 4 + 3]};
-                                if constexpr (kBias) v += bias[ii][g4];
+                                if constexpr (kBias) v += bias_of(ii, g4);
                                 if constexpr (ST == Store::kScale) v *= op.scale;
                                 const int at = srow * E::kLdw + ii * 32 + g4 * 8 + fc * 4;
                                 if constexpr (E::kF32) {
@@ -745,7 +844,8 @@ size_t lds_bytes(const PipeConfig& c, Store st) {
     const bool f32 = st == Store::kBiasResidual || st == Store::kTn || st == Store::kDGelu;
     const int wtn = c.bn / pipe_waves_n(c.bn), per = f32 && st != Store::kDGelu ? 4 : 8,
               rows = f32 ? 16 : 32;
-    const size_t stages = size_t(c.stages) * (c.bm + c.bn) * c.bk * 2;
+    const size_t stages = size_t(c.stages) * (c.bm + c.bn) * c.bk * 2 +
+                          pipe_bias_lds(c.bm, c.bn, c.stages, c.bk, st);
     const size_t staging = 4 * size_t(rows) * (wtn + per) * (f32 ? 4 : 2);
     return stages + staging <= kPipeMaxLds ? stages + staging : stages + staging / 2;
 }

@@ -528,3 +528,46 @@ def test_gemm_is_ordered_on_the_given_stream(flint, cuda, case, side):
             flint.gemm_tn(y, x, w, m, n, k, stream=stream)
     stream.synchronize()
     assert bool((y.float() == k).all())
+
+
+# The eight-wave ping-pong NT kernel (gemm_pp.hip), each tile forced: edge
+# tiles on both sides, more tiles than CUs (so persistent workgroups run two
+# or three tiles and the k-step stream crosses tile boundaries), and a GPT-2
+# depth. Outputs start as NaN so a missed store shows.
+PP_SHAPES = [(264, 200, 128), (8408, 2040, 128), (1000, 3072, 768)]
+
+
+@pytest.mark.parametrize("m,n,k", PP_SHAPES)
+@pytest.mark.parametrize("epilogue", ["none", "bias", "bias_gelu", "bias_residual"])
+@pytest.mark.parametrize("force", ["256,256", "256,192", "256,128"])
+def test_nt_pingpong_forced(flint, cuda, monkeypatch, force, epilogue, m, n, k):
+    if force == "256,256" and epilogue != "none":
+        pytest.skip("256 x 256 serves the plain product only")
+    monkeypatch.setenv("FLINT_GEMM_PP", force)
+    x = uniform((m, k), 70)
+    w = normal((n, k), 71, 0.05, torch.float16)
+    b = normal((n,), 72, 0.02)
+    ref = ref_nt(x, w)
+    xd, wd, bd = x.to(cuda), w.to(cuda), b.to(cuda)
+    if epilogue == "bias_residual":
+        r = normal((m, n), 73)
+        y = torch.full((m, n), float("nan"), device=cuda)
+        flint.gemm_nt_bias_residual(y, xd, wd, bd, r.to(cuda), m, n, k)
+        ref = r + (ref + b)
+    else:
+        y = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
+        if epilogue == "none":
+            flint.gemm_nt(y, xd, wd, m, n, k)
+        elif epilogue == "bias":
+            flint.gemm_nt_bias(y, xd, wd, bd, m, n, k)
+            ref = ref + b
+        else:
+            pre = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
+            flint.gemm_nt_bias_gelu(y, pre, xd, wd, bd, m, n, k)
+            torch.cuda.synchronize()
+            assert rel_err(pre.cpu(), ref + b) <= TOL
+            ref = torch.nn.functional.gelu((ref + b).double(), approximate="tanh")
+    torch.cuda.synchronize()
+    got = y.cpu()
+    assert bool(torch.isfinite(got).all())
+    assert rel_err(got, ref) <= TOL

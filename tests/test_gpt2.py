@@ -189,7 +189,7 @@ def test_a_token_file_batch_runs_through_the_model(flint, cuda, tmp_path):
     tgt = torch.from_numpy(targets.astype(np.int64))
     assert torch.equal(idx.reshape(-1), stream[128:256]) and torch.equal(tgt.reshape(-1), stream[129:257])
     # The device copy of the loader's own bytes is what _dev16 makes of idx.
-    assert torch.equal(torch.from_numpy(tokens.view(np.int16)).reshape(-1).cuda(), _dev16(idx))
+    assert torch.equal(torch.from_numpy(tokens.view(np.int16).copy()).reshape(-1).cuda(), _dev16(idx))
     _gate_case(flint, cfg, sequences, length, True, idx, tgt)
 
 
