@@ -6,6 +6,7 @@
 #include <cmath>
 
 #include "common/args.h"
+#include "flint/flint_noalloc.h"
 #include "kernels/kernels.h"
 
 namespace {
@@ -134,6 +135,22 @@ FLINT_API flint_status flint_bias_gradient(void* dbias, const void* dy, size_t r
     if (!c.ok()) return c.status();
     FLINT_HIP_CHECK(flint::launch_bias_gradient(dbias, dy, rows, cols, accumulate != 0, workspace,
                                                 flint::to_hip(stream)));
+    return FLINT_OK;
+}
+
+FLINT_API flint_status flint_bias_gradient_noalloc(void* dbias, const void* dy, size_t rows,
+                                                   size_t cols, int accumulate,
+                                                   flint_stream stream) {
+    Checker c("flint_bias_gradient_noalloc");
+    if (!bias_sizes(c, rows, cols).ok() || cols == 0) return c.status();
+    const size_t needed = flint::bias_gradient_workspace(rows, cols);
+    c.require(needed <= flint::kBiasGradientScratchBytes,
+              "%zu x %zu needs %zu bytes of scratch, more than the %zu the library holds", rows,
+              cols, needed, flint::kBiasGradientScratchBytes)
+        .buffers({{"dbias", dbias, cols * 4}, {"dy", dy, rows * cols * 2}}, 1);
+    if (!c.ok()) return c.status();
+    FLINT_HIP_CHECK(flint::launch_bias_gradient_noalloc(dbias, dy, rows, cols, accumulate != 0,
+                                                        flint::to_hip(stream)));
     return FLINT_OK;
 }
 

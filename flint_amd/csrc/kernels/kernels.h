@@ -107,6 +107,12 @@ hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const 
                                      hipStream_t stream);
 hipError_t launch_bias_gradient(void* dbias, const void* dy, size_t rows, size_t cols,
                                 bool accumulate, void* workspace, hipStream_t stream);
+// The same two passes with the partials in the library's per-device scratch
+// array (kBiasGradientScratchBytes; no allocation). Sizes whose partials do
+// not fit return hipErrorInvalidValue.
+constexpr size_t kBiasGradientScratchBytes = size_t{4} << 20;
+hipError_t launch_bias_gradient_noalloc(void* dbias, const void* dy, size_t rows, size_t cols,
+                                        bool accumulate, hipStream_t stream);
 // Merges per-chunk (sum, error) partials left in workspace into out (cols FP32).
 hipError_t launch_bias_gradient_finish(void* out, const void* workspace, size_t rows,
                                        size_t cols, bool accumulate, hipStream_t stream);

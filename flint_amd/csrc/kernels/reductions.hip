@@ -17,9 +17,11 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstdint>
+#include <mutex>
 
 #include "common/common.h"
 #include "kernels/kernels.h"
@@ -1014,6 +1016,55 @@ hipError_t launch_softmax_cross_entropy(void* dlogits, void* row_loss, const voi
         done += n;
     }
     return hipSuccess;
+}
+
+}  // namespace flint
+
+// ---- the bias gradient without a caller's workspace ------------------------
+//
+// flint_bias_gradient_noalloc keeps the column partials in `scratch`, a
+// device array of kBiasGradientScratchBytes that every device the library
+// runs on holds until the process ends. The array's name is only a host-side
+// handle: host code uses the address hipGetSymbolAddress returns for the
+// current device, read once per device on that device's first call. Calls on
+// one device share the array, so calls that overlap in time on one device
+// (two streams, two threads) race on it; calls in one stream's order do not.
+// The partials pass writes every partial the finish pass reads, so nothing
+// needs clearing between calls.
+static __device__ __align__(256) unsigned char scratch[flint::kBiasGradientScratchBytes];
+
+namespace flint {
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_lock;
+std::atomic<void*> g_scratch[kScratchDevices];
+
+hipError_t scratch_address(void** out) {
+    int device = 0;
+    if (hipError_t e = hipGetDevice(&device); e != hipSuccess) return e;
+    if (device < 0 || device >= kScratchDevices) return hipErrorInvalidDevice;
+    void* p = g_scratch[device].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> guard(g_scratch_lock);
+        p = g_scratch[device].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess) return e;
+            g_scratch[device].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_bias_gradient_noalloc(void* dbias, const void* dy, size_t rows, size_t cols,
+                                        bool accumulate, hipStream_t stream) {
+    if (bias_gradient_workspace(rows, cols) > kBiasGradientScratchBytes) return hipErrorInvalidValue;
+    void* ws = nullptr;
+    if (hipError_t e = scratch_address(&ws); e != hipSuccess) return e;
+    return launch_bias_gradient(dbias, dy, rows, cols, accumulate, ws, stream);
 }
 
 }  // namespace flint

@@ -19,6 +19,7 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "flint" / "flint.h"
 TRAIN_HEADER = ROOT / "include" / "flint" / "flint_train.h"
+NOALLOC_HEADER = ROOT / "include" / "flint" / "flint_noalloc.h"
 LIBRARY = ROOT / "build" / "release" / "bin" / "libflint.so"
 
 OK = 0
@@ -87,6 +88,8 @@ SIGNATURES = {
     "flint_gemm_tn_workspace": (I, [Z, Z, Z, ctypes.POINTER(Z)]),
     "flint_bias_gradient": (I, [P, P, Z, Z, I, P, Z, P]),
     "flint_bias_gradient_workspace": (I, [Z, Z, ctypes.POINTER(Z)]),
+    # flint_noalloc.h (no counterpart in the reference)
+    "flint_bias_gradient_noalloc": (I, [P, P, Z, Z, I, P]),
     "flint_gemm_nt_batched": (I, [P, P, P, Z, Z, Z, Z, F, P]),
     "flint_gemm_nn_batched": (I, [P, P, P, Z, Z, Z, Z, P]),
     "flint_gemm_tn_batched": (I, [P, P, P, Z, Z, Z, Z, P]),
@@ -277,6 +280,11 @@ class Flint:
         self.check(self.lib.flint_bias_gradient_workspace(rows, cols, ctypes.byref(out)))
         return out.value
 
+    def bias_gradient_noalloc(self, dbias, dy, rows, cols, accumulate=False, stream=None):
+        """flint_bias_gradient with the library's own scratch array (no workspace)."""
+        self.check(self.lib.flint_bias_gradient_noalloc(pointer(dbias), pointer(dy), rows, cols,
+                                                        int(bool(accumulate)), stream_handle(stream)))
+
     def bias_gradient(self, dbias, dy, rows, cols, accumulate=False, workspace=None,
                       workspace_bytes=None, stream=None):
         if workspace is None:
@@ -465,6 +473,6 @@ def declared_functions(header=None):
     flint.h and of the training-step extension, flint_train.h."""
     import re
 
-    headers = [header] if header is not None else [HEADER, TRAIN_HEADER]
+    headers = [header] if header is not None else [HEADER, TRAIN_HEADER, NOALLOC_HEADER]
     text = "".join(Path(h).read_text() for h in headers)
     return re.findall(r"FLINT_API\s+[^;(]*?\b(flint_\w+)\s*\(", text)

@@ -16,6 +16,8 @@ def test_header_matches_signatures():
     # training-step extension, which has no counterpart in the reference.
     assert len(flint_lib.declared_functions(flint_lib.HEADER)) == 40
     assert len(flint_lib.declared_functions(flint_lib.TRAIN_HEADER)) == 4
+    # flint_noalloc.h: one entry point for callers that cannot allocate.
+    assert flint_lib.declared_functions(flint_lib.NOALLOC_HEADER) == ["flint_bias_gradient_noalloc"]
     declared = flint_lib.declared_functions()
     assert sorted(declared) == sorted(flint_lib.SIGNATURES)
 
