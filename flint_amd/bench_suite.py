@@ -361,6 +361,36 @@ def run(f, torch, dev, path, only=None):
             del wte, wpe, xs, dx, dwte, dwpe, ws
         torch.cuda.empty_cache()
 
+    def section_attention():
+        # The fused causal attention at GPT-2 124M's shape: 96 batches (8
+        # sequences x 12 heads) of 1024 x 64. Work counted as the causal half
+        # of the products: forward 2 (S, PV), backward 5 (S recomputed
+        # once for P, dP, dV, dK, dQ), 2 * 96 * 64 * 1024^2 / 2 FLOP each.
+        Bn, Tn, D = B, T, 64
+        half = 2 * Bn * D * Tn * Tn / 2
+        sets = []
+        for i in range(2):
+            q, k, v, g = (normal((Bn, Tn, D), 90 + 4 * i + j, 1.0, torch.float16).to(dev) for j in range(4))
+            o = torch.empty_like(q)
+            lse = torch.empty((Bn, Tn), device=dev)
+            sets.append((q, k, v, g, o, lse, torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)))
+        ws = torch.empty(f.attention_backward_workspace(Bn, Tn, D), dtype=torch.uint8, device=dev)
+        if want("flint_attention_forward"):
+            ms = _time_gpu(torch, lambda st: f.attention_forward(st[4], st[5], st[0], st[1], st[2], Bn, Tn,
+                                                                 D, 0.125), sets, per_round=8)
+            record("flint_attention_forward causal 96x1024x64", "gemm", 2 * half, ms,
+                   note="causal half of S = QK^T and O = PV; scores never stored")
+        if want("flint_attention_backward"):
+            for st in sets:
+                f.attention_forward(st[4], st[5], st[0], st[1], st[2], Bn, Tn, D, 0.125)
+            ms = _time_gpu(torch, lambda st: f.attention_backward(st[6], st[7], st[8], st[3], st[0], st[1],
+                                                                  st[2], st[4], st[5], Bn, Tn, D, 0.125,
+                                                                  workspace=ws), sets, per_round=8)
+            record("flint_attention_backward causal 96x1024x64", "gemm", 5 * half, ms,
+                   note="causal half of S (recomputed), dP, dV, dK, dQ; deterministic (no atomics)")
+        del sets, ws
+        torch.cuda.empty_cache()
+
     def section_gpt2():
         # A whole GPT-2 124M training step: 12 layers, width 768,
         # 12 heads, 8 x 1024 tokens, padded vocabulary 50,304; forward through
@@ -369,6 +399,8 @@ def run(f, torch, dev, path, only=None):
         from flint_amd.flint_lib import Gpt2
 
         L_, S_, T_ = 12, 8, 1024
+        # The fused attention unless FLINT_FLASH=0 (read when the model is created).
+        flash = os.environ.get("FLINT_FLASH", "1") != "0"
         model = Gpt2(f, L_, H, C, T_, V, VP, S_, T_, backward=True)
         g = torch.Generator().manual_seed(5)
         for name, addr, rows, cols in model.parameters():
@@ -392,7 +424,9 @@ def run(f, torch, dev, path, only=None):
 
         ms = _time_gpu(torch, step, [0], rounds=5, per_round=5)
         flops = 7.0013e12
-        entry = {"kernel": "gpt2_124m_train_step 8x1024 (forward + backward)", "ms": round(ms, 4),
+        label = "fused attention" if flash else "stored scores and probabilities"
+        entry = {"kernel": f"gpt2_124m_train_step 8x1024 (forward + backward, {label})",
+                 "ms": round(ms, 4),
                  "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
                  "frac_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_TF, 4),
                  "tokens_per_s": round(S_ * T_ / (ms * 1e-3)), "cpu_threads": threads,
@@ -457,6 +491,8 @@ def run(f, torch, dev, path, only=None):
         section_softmax()
     if want("flint_softmax_cross_entropy"):
         section_ce()
+    if want("flint_attention_forward") or want("flint_attention_backward"):
+        section_attention()
     if want("gpt2_124m_train_step"):
         section_gpt2()
     if any(want(x) for x in ("flint_copy", "flint_fp32_to_fp16", "flint_heads_split",

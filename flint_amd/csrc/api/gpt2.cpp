@@ -73,6 +73,7 @@ struct Saved {
     void *x_in = nullptr, *x_mid = nullptr, *x_out = nullptr;
     void *h1 = nullptr, *mean1 = nullptr, *rstd1 = nullptr;
     void *q = nullptr, *k = nullptr, *v = nullptr, *p = nullptr;
+    void *o = nullptr, *lse = nullptr;   // fused attention: heads' output, log-sum-exp
     void* attn_out = nullptr;
     void *h2 = nullptr, *mean2 = nullptr, *rstd2 = nullptr;
     void *gelu = nullptr, *pre = nullptr;
@@ -98,6 +99,10 @@ size_t round_up(size_t b) { return (b + kAlign - 1) / kAlign * kAlign; }
 struct flint_gpt2 {
     flint_gpt2_config cfg{};
     size_t rows = 0, head_width = 0, head_batches = 0;
+    // Fused attention (attention.hip) in place of the stored scores and
+    // probabilities; decided at creation (head width 64, FLINT_FLASH not "0").
+    bool flash = false;
+    void* attn_work = nullptr;   // the fused backward's D
     std::deque<Param> params;   // stable addresses
     Param* wte = nullptr;
     Param* wpe = nullptr;
@@ -223,6 +228,15 @@ flint_status size_workspaces(flint_gpt2& m) {
 
 // Declares every parameter (named_parameters order), gradient, compute copy,
 // activation and scratch buffer as a request; allocation comes after.
+// Whether the model runs the fused causal attention: head width 64 (the
+// kernels' width), unless FLINT_FLASH=0 asks for the stored scores and
+// probabilities (the reference's sequence; the bit-exactness tests of the
+// causal products use it).
+bool use_flash(size_t head_width) {
+    const char* e = std::getenv("FLINT_FLASH");
+    return head_width == 64 && !(e != nullptr && e[0] == '0' && e[1] == '\0');
+}
+
 flint_status plan(flint_gpt2& m) {
     const flint_gpt2_config& c = m.cfg;
     const bool bwd = c.backward != 0;
@@ -230,6 +244,7 @@ flint_status plan(flint_gpt2& m) {
     m.rows = c.sequences * c.length;
     m.head_width = w / c.heads;
     m.head_batches = c.sequences * c.heads;
+    m.flash = use_flash(m.head_width);
 
     m.wte = param(m, "wte.weight", c.padded_vocab, w);
     m.wpe = param(m, "wpe.weight", c.block_size, w);
@@ -278,7 +293,12 @@ flint_status plan(flint_gpt2& m) {
             req(&s.q, heads);
             req(&s.k, heads);
             req(&s.v, heads);
-            req(&s.p, matrix);
+            if (m.flash) {
+                req(&s.o, heads);
+                req(&s.lse, m.head_batches * c.length * 4);
+            } else {
+                req(&s.p, matrix);
+            }
             req(&s.attn_out, half_rows);
             req(&s.h2, half_rows);
             req(&s.mean2, rows * 4);
@@ -290,7 +310,8 @@ flint_status plan(flint_gpt2& m) {
         req(&m.mean_f, rows * 4);
         req(&m.rstd_f, rows * 4);
         req(&m.qkv, rows * 3 * w * 2);
-        req(&m.scores, matrix);
+        if (m.flash) req(&m.attn_work, m.head_batches * c.length * 4);
+        else req(&m.scores, matrix);
         req(&m.heads_out, heads);
         FLINT_TRY(size_workspaces(m));
         req(&m.dres, resid);
@@ -313,8 +334,12 @@ flint_status plan(flint_gpt2& m) {
         req(&s.q, heads);
         req(&s.k, heads);
         req(&s.v, heads);
-        req(&m.scores, matrix);
-        req(&s.p, matrix);
+        if (m.flash) {
+            req(&s.lse, m.head_batches * c.length * 4);
+        } else {
+            req(&m.scores, matrix);
+            req(&s.p, matrix);
+        }
         req(&m.heads_out, heads);
         req(&s.attn_out, half_rows);
         req(&s.gelu, rows * 4 * w * 2);
@@ -375,6 +400,7 @@ flint_status allocate(flint_gpt2& m) {
 }
 
 float score_scale(size_t head_width) { return 1.0f / std::sqrt(float(head_width)); }
+
 
 // The six attention products go to the batched GEMMs' causal variants: the
 // scores and their gradient are read only at or below the diagonal (the
@@ -472,11 +498,19 @@ flint_status forward_layer(const flint_gpt2& m, const Layer& L, flint_stream st)
     FLINT_TRY(flint_gemm_nt_bias(m.qkv, s.h1, L.attn.half, L.attn.b->data, rows, 3 * w, w, st));
     void* const qkv_parts[] = {s.q, s.k, s.v};
     FLINT_TRY(attn_heads3(m.qkv, qkv_parts, c.sequences, c.length, c.heads, hw, false, st));
-    FLINT_TRY(attn_nt(m.scores, s.q, s.k, m.head_batches, c.length, c.length, hw, score_scale(hw),
-                      st));
-    FLINT_TRY(attn_softmax_forward(s.p, m.scores, m.head_batches, c.length, hw, st));
-    FLINT_TRY(attn_nn(m.heads_out, s.p, s.v, m.head_batches, c.length, hw, c.length, st));
-    FLINT_TRY(flint_heads_merge(s.attn_out, m.heads_out, c.sequences, c.length, c.heads, hw, w, 0,
+    // The heads' output: per layer (s.o) when the fused backward reads it.
+    void* heads_o = m.flash && c.backward ? s.o : m.heads_out;
+    if (m.flash) {
+        FLINT_HIP_CHECK(flint::launch_attention_forward(heads_o, s.lse, s.q, s.k, s.v,
+                                                        m.head_batches, c.length, score_scale(hw),
+                                                        flint::to_hip(st)));
+    } else {
+        FLINT_TRY(attn_nt(m.scores, s.q, s.k, m.head_batches, c.length, c.length, hw,
+                          score_scale(hw), st));
+        FLINT_TRY(attn_softmax_forward(s.p, m.scores, m.head_batches, c.length, hw, st));
+        FLINT_TRY(attn_nn(heads_o, s.p, s.v, m.head_batches, c.length, hw, c.length, st));
+    }
+    FLINT_TRY(flint_heads_merge(s.attn_out, heads_o, c.sequences, c.length, c.heads, hw, w, 0,
                                 st));
     FLINT_TRY(flint_gemm_nt_bias_residual(s.x_mid, s.attn_out, L.attn_proj.half,
                                           L.attn_proj.b->data, s.x_in, rows, w, w, st));
@@ -549,11 +583,17 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
     FLINT_TRY(bias_grad(m, *L.attn_proj.b, m.dres_half, acc, st));
     FLINT_TRY(flint_gemm_nn(m.dh, m.dres_half, L.attn_proj.half, rows, w, w, st));
     FLINT_TRY(flint_heads_split(m.heads_out, m.dh, c.sequences, len, c.heads, hw, w, 0, st));
-    FLINT_TRY(attn_tn(m.dv, s.p, m.heads_out, nb, len, hw, len, st));
-    FLINT_TRY(attn_nt(m.scores, m.heads_out, s.v, nb, len, len, hw, 1.0f, st));
-    FLINT_TRY(attn_softmax_backward(m.scores, s.p, m.scores, nb, len, hw, st));
-    FLINT_TRY(attn_nn(m.dq, m.scores, s.k, nb, len, hw, len, st));
-    FLINT_TRY(attn_tn(m.dk, m.scores, s.q, nb, len, hw, len, st));
+    if (m.flash) {
+        FLINT_HIP_CHECK(flint::launch_attention_backward(m.dq, m.dk, m.dv, m.heads_out, s.q, s.k,
+                                                         s.v, s.o, s.lse, m.attn_work, nb, len,
+                                                         score_scale(hw), flint::to_hip(st)));
+    } else {
+        FLINT_TRY(attn_tn(m.dv, s.p, m.heads_out, nb, len, hw, len, st));
+        FLINT_TRY(attn_nt(m.scores, m.heads_out, s.v, nb, len, len, hw, 1.0f, st));
+        FLINT_TRY(attn_softmax_backward(m.scores, s.p, m.scores, nb, len, hw, st));
+        FLINT_TRY(attn_nn(m.dq, m.scores, s.k, nb, len, hw, len, st));
+        FLINT_TRY(attn_tn(m.dk, m.scores, s.q, nb, len, hw, len, st));
+    }
     void* const parts[] = {m.dq, m.dk, m.dv};
     FLINT_TRY(attn_heads3(m.qkv, parts, c.sequences, len, c.heads, hw, true, st));
     FLINT_TRY(weight_grad(m, *L.attn.w, m.qkv, s.h1, acc, st));

@@ -1,0 +1,520 @@
+// Fused causal attention for gfx950, head width 64: the forward pass
+// O = softmax(scale Q K^T, causal) V with its per-query log-sum-exp, and the
+// backward pass to dQ, dK and dV, without materialising the length x length
+// scores or probabilities in HBM.
+//
+// Layout: q, k, v, o, dO, dQ, dK, dV are [batches][length][64] FP16; lse and
+// D (the backward's row sums of dO * O) are [batches][length] FP32.
+//
+// How the work maps to the hardware:
+//  * Scores come from v_mfma_f32_32x32x16_f16 computing S^T = K Q^T (keys as
+//    the MFMA's rows, queries as its columns): each lane then holds one query
+//    (lane % 32) and 16 keys per 32-key block (8a + 4h + b for register
+//    4a + b, h = lane / 32), so a query's running max, sum and rescale are
+//    per-lane values and the row reductions are in-register plus one exchange
+//    with lane ^ 32.
+//  * The probabilities feed the next MFMA straight from those registers as
+//    its B operand (queries as columns, keys as k): within a 16-key step a
+//    lane holds keys 4h .. 4h + 3 and 8 + 4h .. 8 + 4h + 3, and the k order of
+//    an MFMA is free as long as both operands agree, so the A operand (V^T or
+//    K^T, d as rows) is read with the same key order by two ds_read_b64_tr_b16,
+//    each giving a lane 4 consecutive rows (keys) of one column (d) of the
+//    row-major LDS tile.
+//  * K and V tiles of 64 keys (8 KB each) stream into LDS with direct-to-LDS
+//    buffer loads, double-buffered, one barrier per block; rows are 128 bytes
+//    with 16-byte chunks XOR-swizzled by (row >> 1) & 7. Loads past the
+//    sequence read zeros.
+//  * exp is exp2 of scores pre-scaled by scale * log2(e); lse is kept in log2
+//    units inside the kernels and stored as a natural log.
+//  * The backward is deterministic (no atomics): one kernel owns a block of
+//    queries and accumulates dQ over the keys (it also writes D), a second
+//    owns a block of keys and accumulates dK and dV over the queries; both
+//    recompute P from Q, K and lse (FlashAttention-2's scheme).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "common/common.h"
+#include "kernels/gemm_common.h"
+#include "kernels/kernels.h"
+
+namespace flint {
+namespace {
+
+constexpr int kHd = 64;                  // head width
+constexpr int kTile = 64 * kHd;          // halves in a 64-row tile (8 KB)
+constexpr int kAttnThreads = 256;        // 4 waves
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int akey(int row) { return (row >> 1) & 7; }
+
+struct TrPair {
+    i32x2 lo, hi;
+};
+__device__ __forceinline__ f16x8 join(const TrPair& f) {
+    return __builtin_shufflevector(__builtin_bit_cast(f16x4, f.lo), __builtin_bit_cast(f16x4, f.hi),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
+}
+// lgkmcnt(0): the transposing reads are inline asm, invisible to the
+// compiler's wait insertion.
+__device__ __forceinline__ void wait_lds() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* base, unsigned bytes) {
+    const uint64_t v = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+    void* p = reinterpret_cast<void*>((uint64_t(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(p, 0, bytes, 0x00020000);
+}
+
+// Rows r0 .. r0 + 63 of a [rows][64] FP16 matrix into a tile: 8 loads of 1 KB
+// (8 rows each), two per wave. Lane l writes row l / 8 at chunk position
+// l % 8, which holds global chunk (l % 8) ^ key(row).
+__device__ __forceinline__ void load_tile(_Float16* tile, __amdgpu_buffer_rsrc_t rs, int r0,
+                                          int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int u = wave + 4 * i;
+        const int row = u * 8 + (lane >> 3);
+        const unsigned voff = unsigned(((r0 + row) * kHd + (((lane & 7) ^ akey(row)) * 8)) * 2);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(lds_half*)(tile + u * 512), 16, voff, 0, 0, 0);
+    }
+}
+
+// An MFMA operand with tile rows as its rows and d as k: lane l gets row
+// r0 + l % 32, halves 16 kk + 8 (l / 32) .. + 8.
+__device__ __forceinline__ f16x8 frag_rows(const _Float16* tile, int r0, int kk, int lane) {
+    const int row = r0 + (lane & 31);
+    const int chunk = kk * 2 + (lane >> 5);
+    return *reinterpret_cast<const f16x8*>(tile + row * kHd + ((chunk ^ akey(row)) * 8));
+}
+
+// An MFMA operand with d as its rows and tile rows as k, in the permuted k
+// order of the register-held probabilities: lane l (d = 32 db + l % 32,
+// h = l / 32) gets tile rows k0 + 4h .. + 3 (k 0..3) and k0 + 8 + 4h .. + 3
+// (k 4..7) of column d. Within 16 lanes, lane j addresses 4 halves of row
+// base + j / 4 at column c0 + 4 (j % 4); lane i receives column c0 + i.
+__device__ __forceinline__ TrPair frag_tr(const _Float16* tile, int k0, int db, int lane) {
+    const int j = lane & 15;
+    const int c0 = 32 * db + 16 * ((lane >> 4) & 1);
+    const int base = k0 + 4 * (lane >> 5);
+    const int col = c0 + 4 * (j & 3);
+    auto addr = [&](int row) {
+        return unsigned(reinterpret_cast<uintptr_t>(
+            (lds_half*)(tile + row * kHd + (((col >> 3) ^ akey(row)) * 8) + (col & 7))));
+    };
+    TrPair f;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(f.lo) : "v"(addr(base + (j >> 2))));
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(f.hi) : "v"(addr(base + 8 + (j >> 2))));
+    return f;
+}
+
+// The value of lane ^ 32 (the other half of the wave holds the same query).
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
+
+__device__ __forceinline__ f16x8 to_half8(const f32x16& v, int base) {
+    f16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = _Float16(v[base + e]);
+    return h;
+}
+
+// ---------------------------------------------------------------- forward
+
+__global__ void __launch_bounds__(kAttnThreads)
+attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16* q,
+             const _Float16* k, const _Float16* v, int batches, int length, float c) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * 2 * kTile];   // [buf][K, V]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int fr = lane & 31, h = lane >> 5;
+    const int nqb = (length + 127) / 128;
+    const int qb = nqb - 1 - int(blockIdx.x) / batches;      // longest blocks first
+    const int b = int(blockIdx.x) % batches;
+    const size_t mat = size_t(length) * kHd;
+    const unsigned bytes = unsigned(mat * 2);
+    const auto rq = rsrc_of(q + b * mat, bytes);
+    const auto rk = rsrc_of(k + b * mat, bytes);
+    const auto rv = rsrc_of(v + b * mat, bytes);
+    const int q0 = qb * 128 + wave * 32;
+    const int qi = q0 + fr;
+
+    f16x8 qf[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+        qf[kk] = __builtin_bit_cast(
+            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, unsigned((qi * kHd + 16 * kk + 8 * h) * 2), 0, 0));
+
+    float m = -INFINITY, l = 0.0f;
+    f32x16 oacc[2] = {f32x16{}, f32x16{}};
+    const int q_last = min(qb * 128 + 127, length - 1);
+    const int nkb = q_last / 64 + 1;
+    load_tile(lds, rk, 0, wave, lane);
+    load_tile(lds + kTile, rv, 0, wave, lane);
+    for (int j = 0; j < nkb; ++j) {
+        wait_vmcnt<0>();
+        block_sync();
+        const _Float16* kt = lds + (j & 1) * 2 * kTile;
+        const _Float16* vt = kt + kTile;
+        if (j + 1 < nkb) {
+            _Float16* nt = lds + ((j + 1) & 1) * 2 * kTile;
+            load_tile(nt, rk, 64 * (j + 1), wave, lane);
+            load_tile(nt + kTile, rv, 64 * (j + 1), wave, lane);
+        }
+        const int kbase = 64 * j;
+        if (kbase > q0 + 31) continue;          // every key above every query of the wave
+        f32x16 s[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb)
+                s[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(kt, 32 * hb, kk, lane), qf[kk],
+                                                               s[hb], 0, 0, 0);
+        const bool diag = kbase + 63 > q0;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float t = s[hb][r] * c;
+                if (diag && kbase + 32 * hb + 8 * (r >> 2) + 4 * h + (r & 3) > qi) t = -INFINITY;
+                s[hb][r] = t;
+                mx = fmaxf(mx, t);
+            }
+        mx = fmaxf(mx, xor32(mx));
+        const float m_new = fmaxf(m, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        float sum = 0.0f;
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = __builtin_amdgcn_exp2f(s[hb][r] - m_new);
+                s[hb][r] = p;
+                sum += p;
+            }
+        sum += xor32(sum);
+        l = l * alpha + sum;
+        m = m_new;
+#pragma unroll
+        for (int db = 0; db < 2; ++db) oacc[db] *= alpha;
+        TrPair vf[4][2];
+#pragma unroll
+        for (int cs = 0; cs < 4; ++cs)
+#pragma unroll
+            for (int db = 0; db < 2; ++db) vf[cs][db] = frag_tr(vt, 16 * cs, db, lane);
+        wait_lds();
+#pragma unroll
+        for (int cs = 0; cs < 4; ++cs) {
+            const f16x8 pf = to_half8(s[cs >> 1], 8 * (cs & 1));
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(vf[cs][db]), pf, oacc[db], 0, 0, 0);
+        }
+    }
+    wait_vmcnt<0>();
+    if (qi < length) {
+        const float inv = 1.0f / l;
+        _Float16* orow = out + b * mat + size_t(qi) * kHd;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const f16x4 o4 = {_Float16(oacc[db][4 * a] * inv), _Float16(oacc[db][4 * a + 1] * inv),
+                                  _Float16(oacc[db][4 * a + 2] * inv), _Float16(oacc[db][4 * a + 3] * inv)};
+                *reinterpret_cast<f16x4*>(orow + 32 * db + 8 * a + 4 * h) = o4;
+            }
+        if (h == 0) lse[size_t(b) * length + qi] = (m + __builtin_amdgcn_logf(l)) * kLn2;
+    }
+}
+
+// ---------------------------------------------------------------- backward: dQ (and D)
+
+__global__ void __launch_bounds__(kAttnThreads)
+attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Float16* q,
+                 const _Float16* k, const _Float16* v, const _Float16* o, const _Float16* dout,
+                 const float* lse, int batches, int length, float c, float scale) {
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * 2 * kTile];   // [buf][K, V]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int fr = lane & 31, h = lane >> 5;
+    const int nqb = (length + 127) / 128;
+    const int qb = nqb - 1 - int(blockIdx.x) / batches;
+    const int b = int(blockIdx.x) % batches;
+    const size_t mat = size_t(length) * kHd;
+    const unsigned bytes = unsigned(mat * 2);
+    const auto rq = rsrc_of(q + b * mat, bytes);
+    const auto rk = rsrc_of(k + b * mat, bytes);
+    const auto rv = rsrc_of(v + b * mat, bytes);
+    const auto ro = rsrc_of(o + b * mat, bytes);
+    const auto rdo = rsrc_of(dout + b * mat, bytes);
+    const int q0 = qb * 128 + wave * 32;
+    const int qi = q0 + fr;
+
+    f16x8 qf[4], df[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        const unsigned off = unsigned((qi * kHd + 16 * kk + 8 * h) * 2);
+        qf[kk] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+        df[kk] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0));
+    }
+    // D = sum_d dO * O for this lane's query: halves 32 h .. 32 h + 31 here,
+    // the rest from lane ^ 32.
+    float dd = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        const unsigned off = unsigned((qi * kHd + 32 * h + 8 * kk) * 2);
+        const f16x8 ov = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, 0));
+        const f16x8 gv = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dd = __builtin_fmaf(float(gv[e]), float(ov[e]), dd);
+    }
+    dd += xor32(dd);
+    const float lse2 = qi < length ? lse[size_t(b) * length + qi] * kLog2e : 0.0f;
+    if (qi < length && h == 0) dsum[size_t(b) * length + qi] = dd;
+
+    f32x16 acc[2] = {f32x16{}, f32x16{}};   // dQ^T[d][q]
+    const int q_last = min(qb * 128 + 127, length - 1);
+    const int nkb = q_last / 64 + 1;
+    load_tile(lds, rk, 0, wave, lane);
+    load_tile(lds + kTile, rv, 0, wave, lane);
+    for (int j = 0; j < nkb; ++j) {
+        wait_vmcnt<0>();
+        block_sync();
+        const _Float16* kt = lds + (j & 1) * 2 * kTile;
+        const _Float16* vt = kt + kTile;
+        if (j + 1 < nkb) {
+            _Float16* nt = lds + ((j + 1) & 1) * 2 * kTile;
+            load_tile(nt, rk, 64 * (j + 1), wave, lane);
+            load_tile(nt + kTile, rv, 64 * (j + 1), wave, lane);
+        }
+        const int kbase = 64 * j;
+        if (kbase > q0 + 31) continue;
+        f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                s[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(kt, 32 * hb, kk, lane), qf[kk],
+                                                               s[hb], 0, 0, 0);
+                dp[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(vt, 32 * hb, kk, lane), df[kk],
+                                                                dp[hb], 0, 0, 0);
+            }
+        const bool diag = kbase + 63 > q0;
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float p = __builtin_amdgcn_exp2f(s[hb][r] * c - lse2);
+                if (diag && kbase + 32 * hb + 8 * (r >> 2) + 4 * h + (r & 3) > qi) p = 0.0f;
+                s[hb][r] = p * (dp[hb][r] - dd);       // dS^T
+            }
+        TrPair kf[4][2];
+#pragma unroll
+        for (int cs = 0; cs < 4; ++cs)
+#pragma unroll
+            for (int db = 0; db < 2; ++db) kf[cs][db] = frag_tr(kt, 16 * cs, db, lane);
+        wait_lds();
+#pragma unroll
+        for (int cs = 0; cs < 4; ++cs) {
+            const f16x8 sf = to_half8(s[cs >> 1], 8 * (cs & 1));
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+                acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(kf[cs][db]), sf, acc[db], 0, 0, 0);
+        }
+    }
+    wait_vmcnt<0>();
+    if (qi < length) {
+        _Float16* row = dq + b * mat + size_t(qi) * kHd;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const f16x4 o4 = {_Float16(acc[db][4 * a] * scale), _Float16(acc[db][4 * a + 1] * scale),
+                                  _Float16(acc[db][4 * a + 2] * scale), _Float16(acc[db][4 * a + 3] * scale)};
+                *reinterpret_cast<f16x4*>(row + 32 * db + 8 * a + 4 * h) = o4;
+            }
+    }
+}
+
+// ---------------------------------------------------------------- backward: dK, dV
+
+// A workgroup owns 128 keys (32 per wave) and walks the query blocks of 64 at
+// or after its first key. S[q][key] = Q K^T with queries as the MFMA's rows:
+// a lane holds one key (lane % 32) and 16 queries per 32-query block, whose
+// lse and D come from the block's LDS copy.
+__global__ void __launch_bounds__(kAttnThreads)
+attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _Float16* q,
+                   const _Float16* k, const _Float16* v, const _Float16* dout, const float* lse,
+                   const float* dsum, int batches, int length, float c, float scale) {
+    // [buf][Q tile, dO tile] then [buf][lse2 64, D 64].
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * 2 * kTile];
+    __shared__ __attribute__((aligned(16))) float rowstat[2][2][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int fr = lane & 31, h = lane >> 5;
+    const int nkb = (length + 127) / 128;
+    const int kb = int(blockIdx.x) / batches;                // earliest keys have the most queries
+    const int b = int(blockIdx.x) % batches;
+    const size_t mat = size_t(length) * kHd;
+    const unsigned bytes = unsigned(mat * 2);
+    const auto rq = rsrc_of(q + b * mat, bytes);
+    const auto rk = rsrc_of(k + b * mat, bytes);
+    const auto rv = rsrc_of(v + b * mat, bytes);
+    const auto rdo = rsrc_of(dout + b * mat, bytes);
+    const float* lse_b = lse + size_t(b) * length;
+    const float* d_b = dsum + size_t(b) * length;
+    (void)nkb;
+    const int k0 = kb * 128 + wave * 32;      // this wave's first key
+    const int ki = k0 + fr;                   // this lane's key
+
+    f16x8 kf[4], vf[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        const unsigned off = unsigned((ki * kHd + 16 * kk + 8 * h) * 2);
+        kf[kk] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+        vf[kk] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+    }
+    f32x16 dka[2] = {f32x16{}, f32x16{}}, dva[2] = {f32x16{}, f32x16{}};   // dK^T, dV^T [d][key]
+    const int qs0 = (kb * 128) / 64;          // first query block
+    const int nqb = (length + 63) / 64;
+    // The block's tiles, and (wave 0, one query a lane) its lse in log2 units
+    // and D. The two register loads go out first, so that waiting for them
+    // before their LDS writes does not wait for the tiles.
+    auto stage_rows = [&](int buf, int qblk) {
+        _Float16* t = lds + buf * 2 * kTile;
+        const int qq = 64 * qblk + lane;
+        float lv = 0.0f, dv0 = 0.0f;
+        if (wave == 0 && qq < length) {
+            lv = lse_b[qq];
+            dv0 = d_b[qq];
+        }
+        load_tile(t, rq, 64 * qblk, wave, lane);
+        load_tile(t + kTile, rdo, 64 * qblk, wave, lane);
+        if (wave == 0) {
+            rowstat[buf][0][lane] = lv * kLog2e;
+            rowstat[buf][1][lane] = dv0;
+        }
+    };
+    stage_rows(0, qs0);
+    for (int qblk = qs0; qblk < nqb; ++qblk) {
+        const int buf = (qblk - qs0) & 1;
+        wait_vmcnt<0>();
+        __syncthreads();
+        const _Float16* qt = lds + buf * 2 * kTile;
+        const _Float16* gt = qt + kTile;
+        const float* l2 = rowstat[buf][0];
+        const float* dd = rowstat[buf][1];
+        if (qblk + 1 < nqb) stage_rows(buf ^ 1, qblk + 1);
+        const int qbase = 64 * qblk;
+        if (qbase + 63 < k0) continue;        // every query of the block precedes every key of the wave
+        f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh) {
+                s[qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(qt, 32 * qh, kk, lane), kf[kk],
+                                                               s[qh], 0, 0, 0);
+                dp[qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(gt, 32 * qh, kk, lane), vf[kk],
+                                                                dp[qh], 0, 0, 0);
+            }
+        const bool diag = qbase < k0 + 31;
+        f32x16 ds[2];
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const int qr = 32 * qh + 8 * a + 4 * h;   // query row in the block, + b
+                const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2 + qr);
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(dd + qr);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * a + e;
+                    float p = __builtin_amdgcn_exp2f(s[qh][r] * c - l4[e]);
+                    if (diag && ki > qbase + qr + e) p = 0.0f;
+                    if (qbase + qr + e >= length) p = 0.0f;
+                    s[qh][r] = p;
+                    ds[qh][r] = p * (dp[qh][r] - d4[e]);
+                }
+            }
+        TrPair gtr[4][2], qtr[4][2];
+#pragma unroll
+        for (int cs = 0; cs < 4; ++cs)
+#pragma unroll
+            for (int db = 0; db < 2; ++db) {
+                gtr[cs][db] = frag_tr(gt, 16 * cs, db, lane);
+                qtr[cs][db] = frag_tr(qt, 16 * cs, db, lane);
+            }
+        wait_lds();
+#pragma unroll
+        for (int cs = 0; cs < 4; ++cs) {
+            const f16x8 pf = to_half8(s[cs >> 1], 8 * (cs & 1));
+            const f16x8 sf = to_half8(ds[cs >> 1], 8 * (cs & 1));
+#pragma unroll
+            for (int db = 0; db < 2; ++db) {
+                dva[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(gtr[cs][db]), pf, dva[db], 0, 0, 0);
+                dka[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(qtr[cs][db]), sf, dka[db], 0, 0, 0);
+            }
+        }
+    }
+    wait_vmcnt<0>();
+    if (ki < length) {
+        _Float16* krow = dk + b * mat + size_t(ki) * kHd;
+        _Float16* vrow = dv + b * mat + size_t(ki) * kHd;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const f16x4 k4 = {_Float16(dka[db][4 * a] * scale), _Float16(dka[db][4 * a + 1] * scale),
+                                  _Float16(dka[db][4 * a + 2] * scale), _Float16(dka[db][4 * a + 3] * scale)};
+                const f16x4 v4 = {_Float16(dva[db][4 * a]), _Float16(dva[db][4 * a + 1]),
+                                  _Float16(dva[db][4 * a + 2]), _Float16(dva[db][4 * a + 3])};
+                *reinterpret_cast<f16x4*>(krow + 32 * db + 8 * a + 4 * h) = k4;
+                *reinterpret_cast<f16x4*>(vrow + 32 * db + 8 * a + 4 * h) = v4;
+            }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_attention_forward(void* out, void* lse, const void* q, const void* k,
+                                    const void* v, size_t batches, size_t length, float scale,
+                                    hipStream_t stream) {
+    const unsigned blocks = unsigned(batches * ((length + 127) / 128));
+    hipLaunchKernelGGL(attn_forward, dim3(blocks), dim3(kAttnThreads), 0, stream,
+                       static_cast<_Float16*>(out), static_cast<float*>(lse),
+                       static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
+                       static_cast<const _Float16*>(v), int(batches), int(length), scale * kLog2e);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_backward(void* dq, void* dk, void* dv, const void* dout, const void* q,
+                                     const void* k, const void* v, const void* o, const void* lse,
+                                     void* dsum, size_t batches, size_t length, float scale,
+                                     hipStream_t stream) {
+    const unsigned blocks = unsigned(batches * ((length + 127) / 128));
+    hipLaunchKernelGGL(attn_backward_dq, dim3(blocks), dim3(kAttnThreads), 0, stream,
+                       static_cast<_Float16*>(dq), static_cast<float*>(dsum),
+                       static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
+                       static_cast<const _Float16*>(v), static_cast<const _Float16*>(o),
+                       static_cast<const _Float16*>(dout), static_cast<const float*>(lse),
+                       int(batches), int(length), scale * kLog2e, scale);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_backward_dkdv, dim3(blocks), dim3(kAttnThreads), 0, stream,
+                       static_cast<_Float16*>(dk), static_cast<_Float16*>(dv),
+                       static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
+                       static_cast<const _Float16*>(v), static_cast<const _Float16*>(dout),
+                       static_cast<const float*>(lse), static_cast<const float*>(dsum),
+                       int(batches), int(length), scale * kLog2e, scale);
+    return hipGetLastError();
+}
+
+}  // namespace flint

@@ -75,6 +75,17 @@ hipError_t launch_gemm_tn_batched(void* y, const void* x, const void* w, size_t 
 // Whether a causal batched GEMM of this layout and shape takes the causal path
 // (the pipeline, with the square operand); otherwise it computes everything.
 bool gemm_batched_causal_taken(GemmLayout l, size_t m, size_t n, size_t k);
+// Fused causal attention (attention.hip), head width 64. D (batches x length
+// FP32) is the backward's workspace.
+constexpr size_t kAttentionMaxLength = size_t{1} << 20;
+constexpr size_t kAttentionMaxBatches = 65535;
+hipError_t launch_attention_forward(void* out, void* lse, const void* q, const void* k,
+                                    const void* v, size_t batches, size_t length, float scale,
+                                    hipStream_t stream);
+hipError_t launch_attention_backward(void* dq, void* dk, void* dv, const void* dout, const void* q,
+                                     const void* k, const void* v, const void* o, const void* lse,
+                                     void* dsum, size_t batches, size_t length, float scale,
+                                     hipStream_t stream);
 // Rows of a causal tile and the k-step both divide this: a causal softmax
 // writing its zeros up to the end of each such block covers what the causal
 // GEMMs read.

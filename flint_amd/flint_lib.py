@@ -20,6 +20,7 @@ ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "flint" / "flint.h"
 TRAIN_HEADER = ROOT / "include" / "flint" / "flint_train.h"
 NOALLOC_HEADER = ROOT / "include" / "flint" / "flint_noalloc.h"
+ATTENTION_HEADER = ROOT / "include" / "flint" / "flint_attention.h"
 LIBRARY = ROOT / "build" / "release" / "bin" / "libflint.so"
 
 OK = 0
@@ -90,6 +91,10 @@ SIGNATURES = {
     "flint_bias_gradient_workspace": (I, [Z, Z, ctypes.POINTER(Z)]),
     # flint_noalloc.h (no counterpart in the reference)
     "flint_bias_gradient_noalloc": (I, [P, P, Z, Z, I, P]),
+    # flint_attention.h (no counterpart in the reference's ABI)
+    "flint_attention_forward": (I, [P, P, P, P, P, Z, Z, Z, F, P]),
+    "flint_attention_backward_workspace": (I, [Z, Z, Z, ctypes.POINTER(Z)]),
+    "flint_attention_backward": (I, [P, P, P, P, P, P, P, P, P, Z, Z, Z, F, P, Z, P]),
     "flint_gemm_nt_batched": (I, [P, P, P, Z, Z, Z, Z, F, P]),
     "flint_gemm_nn_batched": (I, [P, P, P, Z, Z, Z, Z, P]),
     "flint_gemm_tn_batched": (I, [P, P, P, Z, Z, Z, Z, P]),
@@ -279,6 +284,32 @@ class Flint:
         out = Z(0)
         self.check(self.lib.flint_bias_gradient_workspace(rows, cols, ctypes.byref(out)))
         return out.value
+
+    def attention_forward(self, o, lse, q, k, v, batches, length, head_width, scale, stream=None):
+        self.check(self.lib.flint_attention_forward(pointer(o), pointer(lse), pointer(q), pointer(k),
+                                                    pointer(v), batches, length, head_width, scale,
+                                                    stream_handle(stream)))
+
+    def attention_backward_workspace(self, batches, length, head_width):
+        out = Z(0)
+        self.check(self.lib.flint_attention_backward_workspace(batches, length, head_width,
+                                                               ctypes.byref(out)))
+        return out.value
+
+    def attention_backward(self, dq, dk, dv, dout, q, k, v, o, lse, batches, length, head_width,
+                           scale, workspace=None, workspace_bytes=None, stream=None):
+        if workspace is None:
+            import torch
+
+            workspace = torch.empty(max(self.attention_backward_workspace(batches, length,
+                                                                          head_width), 16),
+                                    dtype=torch.uint8, device="cuda")
+        if workspace_bytes is None:
+            workspace_bytes = workspace.numel() * workspace.element_size()
+        self.check(self.lib.flint_attention_backward(
+            pointer(dq), pointer(dk), pointer(dv), pointer(dout), pointer(q), pointer(k),
+            pointer(v), pointer(o), pointer(lse), batches, length, head_width, scale,
+            pointer(workspace), workspace_bytes, stream_handle(stream)))
 
     def bias_gradient_noalloc(self, dbias, dy, rows, cols, accumulate=False, stream=None):
         """flint_bias_gradient with the library's own scratch array (no workspace)."""
@@ -473,6 +504,7 @@ def declared_functions(header=None):
     flint.h and of the training-step extension, flint_train.h."""
     import re
 
-    headers = [header] if header is not None else [HEADER, TRAIN_HEADER, NOALLOC_HEADER]
+    headers = ([header] if header is not None
+               else [HEADER, TRAIN_HEADER, NOALLOC_HEADER, ATTENTION_HEADER])
     text = "".join(Path(h).read_text() for h in headers)
     return re.findall(r"FLINT_API\s+[^;(]*?\b(flint_\w+)\s*\(", text)

@@ -18,6 +18,8 @@ def test_header_matches_signatures():
     assert len(flint_lib.declared_functions(flint_lib.TRAIN_HEADER)) == 4
     # flint_noalloc.h: one entry point for callers that cannot allocate.
     assert flint_lib.declared_functions(flint_lib.NOALLOC_HEADER) == ["flint_bias_gradient_noalloc"]
+    # flint_attention.h: the fused causal attention, additive.
+    assert len(flint_lib.declared_functions(flint_lib.ATTENTION_HEADER)) == 3
     declared = flint_lib.declared_functions()
     assert sorted(declared) == sorted(flint_lib.SIGNATURES)
 
@@ -125,3 +127,20 @@ def test_gpt2_config_validation(flint):
     assert flint.lib.flint_gpt2_bytes(ctypes.byref(bad), ctypes.byref(size)) == 1
     assert "heads (7) must split width (768) into multiples of 8" in flint.last_error()
     assert flint.lib.flint_gpt2_parameter_count(None) == 0
+
+
+def test_attention_checks_fail_before_any_device_work(flint):
+    from flint_amd.flint_lib import FlintError
+
+    with pytest.raises(FlintError, match="head_width \\(32\\) must be 64"):
+        flint.attention_forward(16, 32, 48, 64, 80, 2, 8, 32, 0.125, stream=0)
+    with pytest.raises(FlintError, match="scale .* must be finite"):
+        flint.attention_forward(16, 32, 48, 64, 80, 2, 8, 64, float("inf"), stream=0)
+    with pytest.raises(FlintError, match="q is null"):
+        flint.attention_forward(16, 1 << 20, None, 64, 80, 2, 8, 64, 0.125, stream=0)
+    assert flint.attention_backward_workspace(96, 1024, 64) == 96 * 1024 * 4
+    with pytest.raises(FlintError, match="needs 64 bytes of workspace, given 8"):
+        flint.attention_backward(16, 32, 48, 64, 80, 96, 112, 128, 144, 2, 8, 64, 0.125,
+                                 workspace=1 << 20, workspace_bytes=8, stream=0)
+    # Empty calls succeed without touching anything.
+    flint.attention_forward(None, None, None, None, None, 0, 8, 64, 0.125, stream=0)

@@ -128,6 +128,37 @@ def test_forward_and_backward_pass_the_gate(flint, cuda, cfg, sequences, length,
     _gate_case(flint, cfg, sequences, length, trained)
 
 
+# Head width 64: the model runs the fused causal attention (flint_attention_*);
+# FLINT_FLASH=0 runs the stored scores and probabilities instead. Both pass the
+# gate; the fused path keeps scores and probabilities in FP32 longer, so its
+# forward error is no larger.
+HEAD64 = dict(layers=2, heads=2, width=128, block_size=128, vocab=1000, padded_vocab=1024)
+
+
+@pytest.mark.parametrize("flash", ["1", "0"], ids=["fused", "stored"])
+@pytest.mark.parametrize("trained", [False, True], ids=["init", "trained"])
+def test_head64_passes_the_gate_fused_and_stored(flint, cuda, monkeypatch, flash, trained):
+    monkeypatch.setenv("FLINT_FLASH", flash)
+    _gate_case(flint, HEAD64, 2, 128, trained)
+
+
+def test_fused_attention_forward_error_is_no_larger(flint, cuda, monkeypatch):
+    cfg, sequences, length = HEAD64, 3, 96
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=21, trained=True)
+    params = {n: t.half().float() for n, t in params.items()}
+    idx, tgt = _tokens(cfg, sequences, length, 22)
+    ref = G.gradients(params, idx, tgt, cfg, 1.0)
+    errs = {}
+    for flash in ("1", "0"):
+        monkeypatch.setenv("FLINT_FLASH", flash)
+        out = _run(flint, cfg, sequences, length, params, idx, tgt, 1.0)
+        errs[flash] = _rel_l2(out[0][:, :cfg["vocab"]], ref[0])
+    print(f"logits rel L2: fused {errs['1']:.3e} stored {errs['0']:.3e}")
+    assert errs["1"] <= errs["0"] * 1.05
+
+
 # GPT-2 124M itself (configs[4]'s model), at the reference's gate shapes (ref
 # tests/test_gpt2.py:686, :712-715; gradients ref tests/test_gpt2_backward.py:651-653).
 GPT2 = dict(layers=12, heads=12, width=768, block_size=1024, vocab=50257, padded_vocab=50304)
@@ -235,6 +266,9 @@ def test_causal_attention_products_change_no_bits(flint, cuda, monkeypatch, leng
     idx, tgt = _tokens(cfg, sequences, length, 12)
     if force is not None:
         monkeypatch.setenv("FLINT_GEMM_PIPE", force)
+    # The stored scores and probabilities (head width 64 would take the fused
+    # attention, which has no causal-skip variant to compare).
+    monkeypatch.setenv("FLINT_FLASH", "0")
     monkeypatch.setenv("FLINT_ATTN_CAUSAL", "0")
     full = _run(flint, cfg, sequences, length, params, idx, tgt, 0.25)
     monkeypatch.delenv("FLINT_ATTN_CAUSAL")
