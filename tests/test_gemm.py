@@ -571,3 +571,120 @@ def test_nt_pingpong_forced(flint, cuda, monkeypatch, force, epilogue, m, n, k):
     got = y.cpu()
     assert bool(torch.isfinite(got).all())
     assert rel_err(got, ref) <= TOL
+
+
+# ---- exact-rounding contracts of the GELU and dGELU epilogues
+#
+# With sums made exact (a zero x for GELU, so s is the bias; a one-hot w for
+# dGELU, so the sum is dh), every output is one FP16 rounding of a known real
+# number. Within one FP16 ulp of the correctly rounded value everywhere, and
+# equal to it wherever the exact value lies farther from a rounding boundary
+# than the FP32 evaluation's error can move it. With t = s (c0 + c1 s^2) the
+# exponential's argument in log2 units, an FP32 error of about 2^-22 |t| ln 2
+# relative in exp2(t) reaches the result where the exponential dominates
+# (t > 0, i.e. s < 0); where it is small against 1 (s > 0) it does not. So
+# 2^-21 (2 + max(t, 0) ln 2), plus a few FP32 ulps, is taken as the bound.
+
+def _ordered(h):
+    """FP16 values to integers in value order, +0 and -0 both 0 (ulp distance)."""
+    u = np.asarray(h, dtype=np.float16).view(np.uint16).astype(np.int64)
+    return np.where(u & 0x8000, -(u & 0x7FFF), u)
+
+
+def _safe(v, rel, absolute=0.0):
+    """Whether float64 values v lie farther from the nearest FP16 rounding
+    boundary (the midpoint between the FP16 neighbours around v) than an
+    error of rel |v| + absolute can move them."""
+    v = np.asarray(v, dtype=np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        h = v.astype(np.float16)
+        up = np.nextafter(h, np.float16(np.inf)).astype(np.float64)
+        dn = np.nextafter(h, np.float16(-np.inf)).astype(np.float64)
+        hf = h.astype(np.float64)
+        d = np.minimum(np.abs(v - (hf + up) / 2), np.abs(v - (hf + dn) / 2))
+        d = np.where(np.isfinite(d), d, np.inf)
+        return d > rel * np.abs(v) + absolute
+
+
+def _exponent_arg(s):
+    s = np.asarray(s, dtype=np.float64)
+    return s * (-2.3022082 - 0.10294324 * s * s)
+
+
+def _gelu_sweep():
+    rng = np.random.default_rng(7)
+    grid = np.linspace(-12.0, 12.0, 32768)
+    rand = rng.random(16384) * 24 - 12
+    mags = [1e-40, 1e-30, 2.0**-25, 6e-8, 1e-5, 20.0, 30.0, 100.0, 1000.0, 1e4, 65000.0, 65504.0,
+            65519.0, 65520.0, 65536.0, 1e5, 1e30, 3.4028234e38]
+    ext = [0.0] + [sg * m for m in mags for sg in (1, -1)]
+    s = np.concatenate([grid, rand, ext]).astype(np.float32)
+    pad = (-len(s)) % 64
+    return np.concatenate([s, np.zeros(pad, np.float32)])
+
+
+def test_gelu_epilogue_is_the_correctly_rounded_gelu(flint, cuda):
+    from oracle import oracle
+
+    bias = _gelu_sweep()
+    n, m, k = len(bias), 2, 64
+    x = torch.zeros((m, k), dtype=torch.float16, device=cuda)
+    w = torch.ones((n, k), dtype=torch.float16, device=cuda)
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    pre = torch.empty_like(y)
+    flint.gemm_nt_bias_gelu(y, pre, x, w, torch.from_numpy(bias).to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    y, pre = y.cpu().numpy(), pre.cpu().numpy()
+    assert np.array_equal(pre[0].view(np.uint16), bias.astype(np.float16).view(np.uint16))
+    assert np.array_equal(y[0].view(np.uint16), y[1].view(np.uint16))
+    with np.errstate(all="ignore"):
+        exact64 = oracle.gelu64(bias.astype(np.float64))
+    exact = exact64.astype(np.float16)
+    dist = np.abs(_ordered(y[0]) - _ordered(exact))
+    assert dist.max() <= 1, (dist.max(), bias[dist.argmax()])
+    safe = _safe(exact64, 2.0**-21 * (2 + np.log(2) * np.maximum(_exponent_arg(bias), 0)))
+    assert safe.mean() > 0.95
+    wrong = safe & (_ordered(y[0]) != _ordered(exact))
+    assert not wrong.any(), (int(wrong.sum()), bias[wrong][:3])
+    # GELU of the FP32 sum, not of its FP16 rounding: at safe points the two
+    # differ often, so the bit-exact match above tells them apart.
+    with np.errstate(all="ignore"):
+        from_pre = oracle.gelu64(bias.astype(np.float16).astype(np.float64)).astype(np.float16)
+    assert (safe & (_ordered(from_pre) != _ordered(exact))).sum() > 1000
+
+
+def test_dgelu_epilogue_over_every_finite_fp16_pre(flint, cuda):
+    from oracle import oracle
+
+    allbits = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    s = allbits[np.isfinite(allbits)]
+    n = len(s)
+    assert n == 63488
+    dhs = [1.0, 1000.0, 2.0**-10, -1.0, -3.0, float(np.float16(0.1))]
+    m, k = len(dhs), 8
+    x = torch.zeros((m, k), dtype=torch.float16)
+    x[:, 0] = torch.tensor(dhs, dtype=torch.float16)
+    w = torch.zeros((k, n), dtype=torch.float16)
+    w[0] = 1
+    pre = torch.from_numpy(np.broadcast_to(s, (m, n)).copy())
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nn_dgelu(y, x.to(cuda), w.to(cuda), pre.to(cuda), m, n, k)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    with np.errstate(all="ignore"):
+        g = oracle.gelu_grad64(s.astype(np.float64))
+    v = np.asarray(dhs)[:, None] * g[None, :]
+    with np.errstate(over="ignore"):
+        exact = v.astype(np.float16)
+    root = -0.7517916243
+    near_root = np.abs(s.astype(np.float64) - root) < 0.25
+    dist = np.abs(_ordered(y) - _ordered(exact))
+    close = np.abs(y.astype(np.float64) - v) <= np.abs(np.asarray(dhs))[:, None] * 1e-7
+    bad = (dist > 1) & ~(near_root[None, :] & close)
+    assert not bad.any(), int(bad.sum())
+    rel = 2.0**-21 * (2 + np.log(2) * np.maximum(_exponent_arg(s), 0))
+    absb = np.where(near_root[None, :], np.abs(np.asarray(dhs))[:, None] * 1e-7, 0.0)
+    safe = _safe(v, rel[None, :], absb)
+    assert safe.mean() > 0.95
+    wrong = safe & (_ordered(y) != _ordered(exact))
+    assert not wrong.any(), int(wrong.sum())

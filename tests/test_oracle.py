@@ -202,3 +202,72 @@ def test_embedding_backward_against_golden():
 def test_rel_max_err_metric():
     assert oracle.rel_max_err(np.array([1.0, 2.0]), np.array([1.0, 2.002])) == pytest.approx(
         0.002 / 2.002)
+
+
+# ---- the shape-only summation orders against the reference's own emulations
+#
+# tests/golden/reference_orders.npz holds inputs and the outputs of the
+# reference's numpy emulations of its kernels' arithmetic (written by
+# tests/golden/make_reference_orders.py from the reference checkout). The C
+# oracle restates those orders independently; here it must reproduce every
+# output bit (values compared as integers, so -0/+0 and NaN payloads count).
+# The GPU kernels are checked against the C oracle bit for bit in
+# test_reductions.py and test_support.py, which closes the chain.
+
+REF_ORDERS = Path(__file__).resolve().parent / "golden" / "reference_orders.npz"
+
+
+def _bits_equal(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape and a.dtype == b.dtype, (a.shape, b.shape, a.dtype, b.dtype)
+    view = np.uint32 if a.dtype == np.float32 else np.uint16
+    return np.array_equal(a.view(view), b.view(view))
+
+
+@pytest.fixture(scope="module")
+def ref_orders():
+    return dict(np.load(REF_ORDERS))
+
+
+def test_bias_gradient_order_is_the_references(ref_orders):
+    r = ref_orders
+    assert _bits_equal(oracle.bias_gradient(r["bias_dy"]), r["bias_out"])
+    assert _bits_equal(oracle.bias_gradient(r["bias_dy"], r["bias_old"]), r["bias_out_acc"])
+    assert _bits_equal(oracle.bias_gradient(r["bias_dy2"]), r["bias_out2"])
+
+
+def test_layernorm_backward_order_is_the_references(ref_orders):
+    r = ref_orders
+    args = (r["ln_dy"], r["ln_x"], r["ln_mean"], r["ln_rstd"], r["ln_gamma"])
+    dx, dgamma, dbeta = oracle.layernorm_backward(*args)
+    assert _bits_equal(dx, r["ln_dx"])
+    assert _bits_equal(dgamma, r["ln_dgamma"])
+    # dbeta is the bias gradient of dy.
+    assert _bits_equal(dbeta, oracle.bias_gradient(r["ln_dy"]))
+    dx_acc, _, _ = oracle.layernorm_backward(*args, dx_old=r["ln_dx_old"])
+    assert _bits_equal(dx_acc, r["ln_dx_acc"])
+
+
+def test_softmax_backward_order_is_the_references(ref_orders):
+    r = ref_orders
+    t = r["sm_p"].shape[-1]
+    ds = oracle.softmax_backward(r["sm_p"], r["sm_dp"], t, 0.125).reshape(r["sm_ds"].shape)
+    assert _bits_equal(ds, r["sm_ds"])
+
+
+def test_embedding_backward_order_is_the_references(ref_orders):
+    r = ref_orders
+    vocab, width = r["emb_dwte"].shape
+    length = r["emb_dwpe"].shape[0]
+    seqs = r["emb_dx"].shape[0] // length
+    dwte, dwpe = oracle.embedding_backward(r["emb_dx"], r["emb_tokens"], seqs, length, vocab, width)
+    assert _bits_equal(dwte, r["emb_dwte"])
+    assert _bits_equal(dwpe, r["emb_dwpe"])
+
+
+def test_a_plain_sum_would_not_match_the_references_order(ref_orders):
+    """The fixtures can tell orders apart: plain FP32 column sums of the mixed
+    case differ from the reference's compensated chunked sums."""
+    r = ref_orders
+    plain = r["bias_dy2"].astype(np.float32).sum(axis=0, dtype=np.float32)
+    assert not _bits_equal(plain, r["bias_out2"])
