@@ -10,9 +10,13 @@ buffer sets rotated past the 256 MB Infinity Cache).
 
 Also reported, in the same JSON line:
   roofline      the dominant kernel's achieved TFLOP/s (algorithmic 2mnk over
-                its mean HIP-event duration on the launch stream) against
-                MI355X's dense FP16 MFMA peak (2,516.6 TFLOP/s);
-  cpu_baseline  PyTorch CPU FP32 of the same three ops on the host cores.
+                its mean HIP-event duration on the launch stream, in a window
+                of >= 100 ms of back-to-back launches) against MI355X's dense
+                FP16 MFMA peak (2,516.6 TFLOP/s); `traffic` is the HBM bytes
+                per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+                profile of this bench;
+  cpu_baseline  PyTorch CPU FP32 of the same three ops on every core the
+                process may run on.
 
 --suite PATH also times every GEMM shape and reduction of the hot path and
 writes them to PATH as JSON (one object per kernel).
@@ -43,6 +47,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--suite", type=str, default=None)
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--window-ms", type=float, default=100.0,
+                   help="length of each per-kernel roofline window (default 100 ms)")
     p.add_argument("--calibrate-copy", type=int, default=0,
                    help="only run flint_copy of this many bytes 5 times (PMC calibration)")
     return p.parse_args()
@@ -106,6 +112,19 @@ def launch(f, s, i):
         f.gemm_nt_bias_residual(s["y_pr"], s["x_pr"], s["w_pr"], s["b_pr"], s["r_pr"], M, C, C)
 
 
+def time_launches(torch, stream, body, reps):
+    """Mean ms per launch of `reps` back-to-back calls of body(i), from HIP
+    events recorded on the launch stream."""
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(reps):
+        body(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
 def set_bytes(s):
     return sum(t.numel() * t.element_size() for t in s.values())
 
@@ -130,7 +149,7 @@ def cpu_baseline(torch):
     median of 3 after a warm-up, scaled to TFLOPS."""
     from inputs import normal, uniform
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     M, C = 1024, 768
     x_up = uniform((M, C), 1).float()
@@ -209,26 +228,24 @@ def main():
 
     # Per-kernel durations (the roofline's denominator), as the reference's
     # per-kernel harness takes them: HIP events on the launch stream around a
-    # run of back-to-back launches of one kernel over the rotating sets.
-    reps = max(args.steps, 20)
-    ms = []
+    # window of back-to-back launches of one kernel over the rotating sets,
+    # the window sized to last at least --window-ms (20 launches at least).
+    ms, windows = [], []
     for k in range(3):
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for i in range(reps):
-            launch(f, sets[i % len(sets)], k)
-        b.record(stream)
-        torch.cuda.synchronize()
-        ms.append(a.elapsed_time(b) / reps)
+        probe = time_launches(torch, stream, lambda i: launch(f, sets[i % len(sets)], k), 10)
+        reps = max(20, int(1.25 * args.window_ms / probe) + 1)
+        t = time_launches(torch, stream, lambda i: launch(f, sets[i % len(sets)], k), reps)
+        ms.append(t)
+        windows.append((reps, reps * t))
 
     flops = [2 * m * n * k for _, m, n, k in KERNELS]
     step_flops = sum(flops)
     kernels = {}
-    for (name, m, n, k), fl, t in zip(KERNELS, flops, ms):
+    for (name, m, n, k), fl, t, (reps, total) in zip(KERNELS, flops, ms, windows):
         tf = fl / (t * 1e-3) / 1e12
         kernels[name] = {"ms": round(t, 5), "tflops": round(tf, 2),
-                         "frac_mfma": round(tf / PEAK_FP16_TFLOPS, 4)}
+                         "frac_mfma": round(tf / PEAK_FP16_TFLOPS, 4),
+                         "window": {"launches": reps, "ms": round(total, 1)}}
     dom = max(range(3), key=lambda k: ms[k])
     achieved = flops[dom] / (ms[dom] * 1e-3) / 1e12
     ms_step = wall / args.steps * 1e3
@@ -255,6 +272,9 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
                      "traffic": traffic_bytes(KERNELS[dom][0]),
+                     "traffic_source": f"profiles/{TRAFFIC.name}: rocprofv3 FETCH_SIZE + "
+                                       "WRITE_SIZE of this bench, scaled by a plain copy "
+                                       "(not measured in this run)",
                      "kernel": KERNELS[dom][0]},
         "kernels": kernels,
         "parity_max_rel_err": err,

@@ -18,7 +18,8 @@ Used by `bench.py --suite PATH`, or directly:
     python3 -m flint_amd.bench_suite --out suite.json [--only SUBSTRING]
 
 which writes one JSON object per kernel (`--only` keeps the kernels whose name
-contains SUBSTRING, e.g. for a rocprofv3 counter pass over one kernel).
+contains SUBSTRING, or any of a comma-separated list of them, e.g. for a
+rocprofv3 counter pass over a few kernels).
 """
 
 import json
@@ -74,13 +75,13 @@ def run(f, torch, dev, path, only=None):
     sys.path.insert(0, str(Path(__file__).resolve().parent.parent / "tests"))
     from inputs import normal, targets, uniform
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     F = torch.nn.functional
     out = []
 
     def want(name):
-        return not only or only in name
+        return not only or any(part in name for part in only.split(","))
 
     def record(name, kind, work, ms, cpu_s=None, cpu_work=None, peer_ms=None, note=""):
         if kind == "gemm":
@@ -515,7 +516,8 @@ def main():
 
     ap = argparse.ArgumentParser(description="Per-kernel measurement at the GPT-2 124M shapes.")
     ap.add_argument("--out", default="suite.json")
-    ap.add_argument("--only", default=None, help="keep kernels whose name contains this")
+    ap.add_argument("--only", default=None,
+                    help="keep kernels whose name contains this (or any of a comma-separated list)")
     a = ap.parse_args()
     if not torch.cuda.is_available():
         raise SystemExit("bench_suite needs a GPU")
