@@ -247,7 +247,7 @@ def run(f, torch, dev, path, only=None):
             st[1][1], dg, db, st[1][0], st[0][0], st[0][2], st[0][3], g, M, C, accumulate_dx=True,
             workspace=wsb), list(zip(sets, dsets)), per_round=64)
         record("flint_layernorm_backward 8192x768 (accumulate_dx)", "red", lnb_bytes, ms,
-               note="5 kernels: dbeta, dgamma (partials + finish each), dx")
+               note="2 kernels: dbeta + dgamma chunk partials; dx + their merge")
         bg_bytes = M * C * 2 + C * 4
         wsg = torch.empty(f.bias_gradient_workspace(M, 4 * C), dtype=torch.uint8, device=dev)
         dy3 = [normal((M, 4 * C), 30 + r, 1.0, torch.float16).to(dev) for r in range(4)]

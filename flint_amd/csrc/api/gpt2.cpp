@@ -532,10 +532,10 @@ flint_status bias_grad(const flint_gpt2& m, const Param& p, const void* dy, int 
     return flint_bias_gradient(p.grad, dy, m.rows, p.cols, acc, m.work, m.work_bytes, st);
 }
 
-// LayerNorm backward: dbeta and dgamma from one pass over dy and x (the
-// model's workspace holds both partial regions), bit-identical to
-// flint_layernorm_backward's separate passes, which FLINT_FUSED_SUMS=0 runs
-// instead (the tests compare the two), then dx.
+// LayerNorm backward: dx, with its FP16 copy written by the dx kernel, then
+// dbeta and dgamma from one pass over dy and x. FLINT_FUSED_SUMS=0 calls
+// flint_layernorm_backward instead and converts dx to FP16 after it (the
+// tests compare the two).
 bool fused_sums() {
     const char* e = std::getenv("FLINT_FUSED_SUMS");
     return e == nullptr || !(e[0] == '0' && e[1] == '\0');
@@ -551,12 +551,10 @@ flint_status norm_backward(const flint_gpt2& m, const Norm& n, const void* x, co
                                            m.work_bytes, st));
         return flint_fp32_to_fp16(m.dres_half, m.dres, m.rows * m.cfg.width, st);
     }
-    FLINT_HIP_CHECK(flint::launch_layernorm_param_grads(n.b->grad, n.w->grad, m.dh, x, mean, rstd,
-                                                        m.rows, m.cfg.width, acc != 0, m.work,
-                                                        m.work_bytes, flint::to_hip(st)));
-    FLINT_HIP_CHECK(flint::launch_layernorm_backward_dx(m.dres, m.dh, x, mean, rstd, n.w->data,
-                                                        m.rows, m.cfg.width, acc_dx != 0,
-                                                        flint::to_hip(st), m.dres_half));
+    FLINT_HIP_CHECK(flint::launch_layernorm_backward(m.dres, n.w->grad, n.b->grad, m.dh, x, mean,
+                                                     rstd, n.w->data, m.rows, m.cfg.width,
+                                                     acc_dx != 0, acc != 0, m.work,
+                                                     flint::to_hip(st), m.dres_half));
     return FLINT_OK;
 }
 

@@ -82,7 +82,7 @@ FLINT_API flint_status flint_layernorm_backward(void* dx, void* dgamma, void* db
                                                 size_t workspace_bytes, flint_stream stream) {
     Checker c("flint_layernorm_backward");
     if (!ln_backward_sizes(c, rows, cols).ok()) return c.status();
-    const size_t needed = flint::bias_gradient_workspace(rows, cols);
+    const size_t needed = flint::layernorm_backward_workspace(rows, cols);
     c.require(workspace_bytes >= needed, "needs %zu bytes of workspace, given %zu", needed,
               workspace_bytes)
         .buffers({{"dx", dx, rows * cols * 4},
@@ -108,7 +108,7 @@ FLINT_API flint_status flint_layernorm_backward_workspace(size_t rows, size_t co
     Checker c("flint_layernorm_backward_workspace");
     if (!ln_backward_sizes(c.require(bytes != nullptr, "bytes is null"), rows, cols).ok())
         return c.status();
-    *bytes = flint::bias_gradient_workspace(rows, cols);
+    *bytes = flint::layernorm_backward_workspace(rows, cols);
     return FLINT_OK;
 }
 

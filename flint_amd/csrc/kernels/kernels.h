@@ -108,14 +108,25 @@ constexpr size_t bias_gradient_workspace(size_t rows, size_t cols) {
     return (rows + kBiasGradientChunkRows - 1) / kBiasGradientChunkRows * cols * 8;
 }
 
+// Workspace of the LayerNorm backward: the dbeta and dgamma chunk partials,
+// one bias-gradient region each.
+constexpr size_t layernorm_backward_workspace(size_t rows, size_t cols) {
+    return 2 * bias_gradient_workspace(rows, cols);
+}
+
 hipError_t launch_layernorm_forward(void* y, void* mean, void* rstd, const void* x,
                                     const void* gamma, const void* beta, size_t rows, size_t cols,
                                     float eps, hipStream_t stream);
+// LayerNorm backward in two launches: the dbeta and dgamma chunk partials from
+// one pass over dy and x, then dx, whose kernel also merges the partials.
+// With dx_half, RN16 of every dx value written goes there too (the values
+// flint_fp32_to_fp16 of dx would give). workspace:
+// layernorm_backward_workspace(rows, cols) bytes.
 hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const void* dy,
                                      const void* x, const void* mean, const void* rstd,
                                      const void* gamma, size_t rows, size_t cols,
                                      bool accumulate_dx, bool accumulate_params, void* workspace,
-                                     hipStream_t stream);
+                                     hipStream_t stream, void* dx_half = nullptr);
 hipError_t launch_bias_gradient(void* dbias, const void* dy, size_t rows, size_t cols,
                                 bool accumulate, void* workspace, hipStream_t stream);
 // The same two passes with the partials in the library's per-device scratch
@@ -131,20 +142,6 @@ hipError_t launch_bias_gradient_finish(void* out, const void* workspace, size_t 
 // multiple of 8) writes the masked zeros only up to the end of the Z-column
 // block holding the diagonal, for consumers that read no further (the model's
 // causal GEMMs, whose tiles are at most 256 rows and k-steps divide 256).
-// LayerNorm's dbeta and dgamma in two launches (one pass over dy and x for
-// both sets of chunk partials, one finish for both), bit-identical to
-// flint_layernorm_backward's four; workspace holds both partial regions
-// (2 x chunks x 2 x cols floats).
-hipError_t launch_layernorm_param_grads(void* dbeta, void* dgamma, const void* dy, const void* x,
-                                        const void* mean, const void* rstd, size_t rows,
-                                        size_t cols, bool accumulate, void* workspace,
-                                        size_t workspace_bytes, hipStream_t stream);
-// LayerNorm dx alone; with dx_half, also RN16 of every dx value written (the
-// values flint_fp32_to_fp16 of dx would give).
-hipError_t launch_layernorm_backward_dx(void* dx, const void* dy, const void* x, const void* mean,
-                                       const void* rstd, const void* gamma, size_t rows,
-                                       size_t cols, bool accumulate_dx, hipStream_t stream,
-                                       void* dx_half = nullptr);
 hipError_t launch_causal_softmax_forward(void* p, const void* s, size_t rows, size_t length,
                                          hipStream_t stream, int zero_span = 0);
 hipError_t launch_causal_softmax_backward(void* ds, const void* p, const void* dp, size_t rows,

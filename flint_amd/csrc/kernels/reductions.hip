@@ -290,10 +290,10 @@ column_finish(float* __restrict__ out, const float* __restrict__ partial, size_t
     finish_quad(out, partial, chunks, cols, accumulate, quad, threadIdx.x & 31);
 }
 
-// LayerNorm's dbeta and dgamma partials in one pass over dy and x (the model's
-// own workspace holds both regions): per 256-row chunk and column, exactly the
-// sums of column_partials<false, 1> and column_partials<true, 1>, in their
-// order, into part0 and part1. column_finish2 then merges both.
+// LayerNorm's dbeta and dgamma partials in one pass over dy and x: per
+// 256-row chunk and column, exactly the sums of column_partials<false, 1> and
+// column_partials<true, 1>, in their order, into part0 and part1. The dx
+// kernel launched after it merges them (ColumnFinish).
 __global__ void __launch_bounds__(kPhases * 64)
 column_partials2(float* part0, float* part1, const _Float16* __restrict__ dy,
                  const float* __restrict__ x, const float* __restrict__ mean,
@@ -355,16 +355,6 @@ column_partials2(float* part0, float* part1, const _Float16* __restrict__ dy,
     }
 }
 
-// column_finish for two outputs at once (dbeta from part0, dgamma from part1).
-__global__ void __launch_bounds__(256)
-column_finish2(float* out0, float* out1, const float* part0, const float* part1, size_t chunks,
-               int cols, int accumulate) {
-    const int quad = blockIdx.x * 8 + (threadIdx.x >> 5);
-    if (quad >= cols / 4) return;   // whole half-waves leave together
-    finish_quad(out0, part0, chunks, cols, accumulate, quad, threadIdx.x & 31);
-    finish_quad(out1, part1, chunks, cols, accumulate, quad, threadIdx.x & 31);
-}
-
 hipError_t launch_partials(bool dgamma, float* partial, const void* dy, const void* x,
                            const void* mean, const void* rstd, size_t rows, size_t cols,
                            hipStream_t stream) {
@@ -395,6 +385,28 @@ hipError_t launch_partials(bool dgamma, float* partial, const void* dy, const vo
 
 // ------------------------------------------------------------ LayerNorm dx
 
+// The merge of dbeta's and dgamma's chunk partials (column_finish's, for two
+// outputs), done by the dx kernel's first half-waves before their rows: the
+// partials come from the launch before it, so the kernel boundary orders them.
+struct ColumnFinish {
+    float* out0;
+    float* out1;
+    const float* part0;
+    const float* part1;
+    size_t chunks;
+    int accumulate;
+};
+
+__device__ __forceinline__ void finish_columns(const ColumnFinish& f, int cols) {
+    const int quads = cols / 4;
+    for (int job = int(blockIdx.x) * 8 + int(threadIdx.x >> 5); job < 2 * quads;
+         job += int(gridDim.x) * 8) {
+        const bool second = job >= quads;
+        finish_quad(second ? f.out1 : f.out0, second ? f.part1 : f.part0, f.chunks, cols,
+                    f.accumulate, second ? job - quads : job, threadIdx.x & 31);
+    }
+}
+
 // One 32-lane half-wave per row: lane l takes pieces l, l + 32, ... (up to PPL
 // of them, 8 columns each), adds g = dy gamma and g xhat over them in order
 // with plain FP32 adds, and a 32-lane butterfly totals them. The second pass
@@ -405,7 +417,9 @@ __global__ void __launch_bounds__(256)
 layernorm_backward_dx(float* __restrict__ dx, const _Float16* __restrict__ dy,
                       const float* __restrict__ x, const float* __restrict__ mean,
                       const float* __restrict__ rstd, const float* __restrict__ gamma,
-                      size_t rows, int cols, int accumulate, _Float16* __restrict__ dx_half) {
+                      size_t rows, int cols, int accumulate, _Float16* __restrict__ dx_half,
+                      ColumnFinish finish) {
+    finish_columns(finish, cols);
     for (size_t row = size_t(blockIdx.x) * 8 + (threadIdx.x >> 5); row < rows;
          row += size_t(gridDim.x) * 8) {
     const int lane = threadIdx.x & 31;
@@ -472,7 +486,9 @@ __global__ void __launch_bounds__(256)
 layernorm_backward_dx_any(float* __restrict__ dx, const _Float16* __restrict__ dy,
                           const float* __restrict__ x, const float* __restrict__ mean,
                           const float* __restrict__ rstd, const float* __restrict__ gamma,
-                          size_t rows, int cols, int accumulate, _Float16* __restrict__ dx_half) {
+                          size_t rows, int cols, int accumulate, _Float16* __restrict__ dx_half,
+                          ColumnFinish finish) {
+    finish_columns(finish, cols);
     for (size_t row = size_t(blockIdx.x) * 8 + (threadIdx.x >> 5); row < rows;
          row += size_t(gridDim.x) * 8) {
     const int lane = threadIdx.x & 31;
@@ -864,70 +880,38 @@ hipError_t launch_bias_gradient(void* dbias, const void* dy, size_t rows, size_t
     return launch_bias_gradient_finish(dbias, workspace, rows, cols, accumulate, stream);
 }
 
-hipError_t launch_layernorm_param_grads(void* dbeta, void* dgamma, const void* dy, const void* x,
-                                        const void* mean, const void* rstd, size_t rows,
-                                        size_t cols, bool accumulate, void* workspace,
-                                        size_t workspace_bytes, hipStream_t stream) {
-    const size_t chunks = (rows + kChunkRows - 1) / kChunkRows;
-    const size_t region = chunks * 2 * cols;   // floats
-    if (cols % 8 != 0 || 2 * region * sizeof(float) > workspace_bytes) return hipErrorInvalidValue;
-    auto* part0 = static_cast<float*>(workspace);
-    auto* part1 = part0 + region;
-    const size_t blocks = chunks * ((cols + 63) / 64);
-    hipLaunchKernelGGL(column_partials2, dim3(unsigned(std::min<size_t>(blocks, kMaxBlocks))),
-                       dim3(kPhases * 64), 0, stream, part0, part1,
-                       static_cast<const _Float16*>(dy), static_cast<const float*>(x),
-                       static_cast<const float*>(mean), static_cast<const float*>(rstd), rows,
-                       int(cols), chunks, blocks);
-    hipLaunchKernelGGL(column_finish2, dim3(unsigned((cols / 4 + 7) / 8)), dim3(256), 0, stream,
-                       static_cast<float*>(dbeta), static_cast<float*>(dgamma), part0, part1,
-                       chunks, int(cols), accumulate ? 1 : 0);
-    return hipGetLastError();
-}
-
 hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const void* dy,
                                      const void* x, const void* mean, const void* rstd,
                                      const void* gamma, size_t rows, size_t cols,
                                      bool accumulate_dx, bool accumulate_params, void* workspace,
-                                     hipStream_t stream) {
-    // dbeta is the bias gradient of dy; dgamma reuses the workspace after it.
-    if (hipError_t e = launch_bias_gradient(dbeta, dy, rows, cols, accumulate_params, workspace,
-                                            stream);
-        e != hipSuccess) {
-        return e;
-    }
-    if (hipError_t e = launch_partials(true, static_cast<float*>(workspace), dy, x, mean, rstd,
-                                       rows, cols, stream);
-        e != hipSuccess) {
-        return e;
-    }
-    if (hipError_t e = launch_bias_gradient_finish(dgamma, workspace, rows, cols,
-                                                   accumulate_params, stream);
-        e != hipSuccess) {
-        return e;
-    }
-    return launch_layernorm_backward_dx(dx, dy, x, mean, rstd, gamma, rows, cols, accumulate_dx,
-                                        stream);
-}
-
-hipError_t launch_layernorm_backward_dx(void* dx, const void* dy, const void* x, const void* mean,
-                                       const void* rstd, const void* gamma, size_t rows,
-                                       size_t cols, bool accumulate_dx, hipStream_t stream,
-                                       void* dx_half) {
-    const unsigned blocks = unsigned(std::min<size_t>((rows + 7) / 8, kMaxBlocks));
-    auto* dxf = static_cast<float*>(dx);
+                                     hipStream_t stream, void* dx_half) {
+    if (cols == 0 || cols % 8 != 0 || rows == 0) return hipErrorInvalidValue;
+    const size_t chunks = (rows + kChunkRows - 1) / kChunkRows;
+    const size_t region = chunks * 2 * cols;   // floats
+    auto* part0 = static_cast<float*>(workspace);
+    auto* part1 = part0 + region;
     const auto* dyh = static_cast<const _Float16*>(dy);
     const auto* xf = static_cast<const float*>(x);
     const auto* mf = static_cast<const float*>(mean);
     const auto* rf = static_cast<const float*>(rstd);
-    const auto* gf = static_cast<const float*>(gamma);
     const int c = int(cols);
+    // dbeta and dgamma partials, one pass over dy and x.
+    const size_t items = chunks * ((cols + 63) / 64);
+    hipLaunchKernelGGL(column_partials2, dim3(unsigned(std::min<size_t>(items, kMaxBlocks))),
+                       dim3(kPhases * 64), 0, stream, part0, part1, dyh, xf, mf, rf, rows, c,
+                       chunks, items);
+    // dx, whose first half-waves also merge the partials.
+    const ColumnFinish finish{static_cast<float*>(dbeta), static_cast<float*>(dgamma), part0,
+                              part1, chunks, accumulate_params ? 1 : 0};
+    const unsigned blocks = unsigned(std::min<size_t>((rows + 7) / 8, kMaxBlocks));
+    auto* dxf = static_cast<float*>(dx);
+    const auto* gf = static_cast<const float*>(gamma);
     const int acc = accumulate_dx ? 1 : 0;
     auto* dxh = static_cast<_Float16*>(dx_half);
     const size_t pieces = cols / 8;
 #define FLINT_DX(PPL)                                                                        \
     hipLaunchKernelGGL(layernorm_backward_dx<PPL>, dim3(blocks), dim3(256), 0, stream, dxf, dyh, \
-                       xf, mf, rf, gf, rows, c, acc, dxh)
+                       xf, mf, rf, gf, rows, c, acc, dxh, finish)
     if (pieces <= 32) FLINT_DX(1);
     else if (pieces <= 64) FLINT_DX(2);
     else if (pieces <= 96) FLINT_DX(3);
@@ -935,7 +919,7 @@ hipError_t launch_layernorm_backward_dx(void* dx, const void* dy, const void* x,
     else if (pieces <= 256) FLINT_DX(8);
     else
         hipLaunchKernelGGL(layernorm_backward_dx_any, dim3(blocks), dim3(256), 0, stream, dxf,
-                           dyh, xf, mf, rf, gf, rows, c, acc, dxh);
+                           dyh, xf, mf, rf, gf, rows, c, acc, dxh, finish);
 #undef FLINT_DX
     return hipGetLastError();
 }

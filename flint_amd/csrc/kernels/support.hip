@@ -285,6 +285,34 @@ embedding_words(float* __restrict__ dwte, const float* __restrict__ dx,
     *out = r;
 }
 
+// The same sums when they add into dwte: only the rows of tokens that occur
+// are touched, so a workgroup per sorted position (256 columns of it) works
+// if the position starts a run of equal tokens and leaves at once otherwise;
+// the run's rows come in ascending order (the sort is stable).
+__global__ void __launch_bounds__(64)
+embedding_runs(float* __restrict__ dwte, const float* __restrict__ dx,
+               const uint16_t* __restrict__ sorted_tokens, const unsigned* __restrict__ sorted_rows,
+               size_t rows, size_t width) {
+    const size_t i = blockIdx.x;
+    const uint16_t v = sorted_tokens[i];
+    if (i > 0 && sorted_tokens[i - 1] == v) return;
+    const size_t col = (size_t(blockIdx.y) * 64 + threadIdx.x) * 4;
+    if (col >= width) return;
+    Comp s[4];
+    for (size_t k = i; k < rows && sorted_tokens[k] == v; ++k) {
+        const f4 d = *reinterpret_cast<const f4*>(dx + size_t(sorted_rows[k]) * width + col);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) comp_add(s[j], d[j]);
+    }
+    f4* out = reinterpret_cast<f4*>(dwte + size_t(v) * width + col);
+    const f4 old = *out;
+    f4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        r[j] = add_rn(old[j], __builtin_isfinite(s[j].sum) ? add_rn(s[j].sum, s[j].error) : s[j].sum);
+    *out = r;
+}
+
 struct EmbLayout {
     size_t partials, sorted_tokens, sorted_rows, offsets, pass_tokens, pass_rows, counts, bytes;
 };
@@ -316,6 +344,8 @@ EmbLayout emb_layout(size_t sequences, size_t length, size_t vocab, size_t width
     l.bytes = at;
     return l;
 }
+
+constexpr int kPhasesF32 = 8;   // row phases of the column-sum order
 
 // Column partials of an FP32 matrix (bias-gradient order), for dwpe.
 __global__ void __launch_bounds__(64)
@@ -358,6 +388,49 @@ column_partials_f32(float* __restrict__ partial, const float* __restrict__ dy, s
     s4[1] = f4{acc[4].sum, acc[5].sum, acc[6].sum, acc[7].sum};
     e4[0] = f4{acc[0].error, acc[1].error, acc[2].error, acc[3].error};
     e4[1] = f4{acc[4].error, acc[5].error, acc[6].error, acc[7].error};
+}
+
+// The same column sums for at most one chunk of rows (rows <= 256), merged and
+// finished in one launch: a thread owns 4 columns, runs the 8 row phases as
+// independent chains (row 8k + p to phase p), lets phase 0 merge phases 1..7
+// in order, and then applies what column_finish does to a single chunk -- lane
+// 0 merges it into an empty sum and the 32-lane butterfly merges five empty
+// lanes' sums into it.
+__global__ void __launch_bounds__(256)
+column_sums_one_chunk(float* __restrict__ out, const float* __restrict__ dy, int rows,
+                      size_t cols, int accumulate) {
+    const size_t quad = size_t(blockIdx.x) * 256 + threadIdx.x;
+    if (quad >= cols / 4) return;
+    Comp acc[kPhasesF32][4];
+    for (int k = 0; k < rows; k += kPhasesF32) {
+        f4 v[kPhasesF32];
+#pragma unroll
+        for (int p = 0; p < kPhasesF32; ++p)
+            if (k + p < rows) v[p] = reinterpret_cast<const f4*>(dy + size_t(k + p) * cols)[quad];
+#pragma unroll
+        for (int p = 0; p < kPhasesF32; ++p) {
+            if (k + p < rows) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) comp_add(acc[p][j], v[p][j]);
+            }
+        }
+    }
+    f4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        for (int p = 1; p < kPhasesF32; ++p) comp_merge(acc[0][j], acc[p][j].sum, acc[p][j].error);
+        Comp t;
+        comp_merge(t, acc[0][j].sum, acc[0][j].error);
+        for (int step = 0; step < 5; ++step) comp_merge(t, 0.0f, 0.0f);
+        r[j] = __builtin_isfinite(t.sum) ? add_rn(t.sum, t.error) : t.sum;
+    }
+    f4* o = reinterpret_cast<f4*>(out) + quad;
+    if (accumulate) {
+        const f4 old = *o;
+        r = f4{add_rn(old[0], r[0]), add_rn(old[1], r[1]), add_rn(old[2], r[2]),
+               add_rn(old[3], r[3])};
+    }
+    *o = r;
 }
 
 }  // namespace
@@ -473,15 +546,30 @@ hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, con
                            in_r, counts, rows, shift, tiles);
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(token_offsets, dim3(unsigned((vocab + 1 + 255) / 256)), dim3(256), 0,
-                       stream, offsets, sorted_tokens, rows, unsigned(vocab));
-    hipLaunchKernelGGL(embedding_words, dim3(unsigned(vocab), unsigned((width / 4 + 63) / 64)),
-                       dim3(64), 0, stream, static_cast<float*>(dwte),
-                       static_cast<const float*>(dx), sorted_rows, offsets, width,
-                       accumulate_wte ? 1 : 0);
+    // A grid dimension holds fewer than 2^32 work-items.
+    if (accumulate_wte && rows < (size_t{1} << 26)) {
+        hipLaunchKernelGGL(embedding_runs, dim3(unsigned(rows), unsigned((width / 4 + 63) / 64)),
+                           dim3(64), 0, stream, static_cast<float*>(dwte),
+                           static_cast<const float*>(dx), sorted_tokens, sorted_rows, rows,
+                           width);
+    } else {
+        hipLaunchKernelGGL(token_offsets, dim3(unsigned((vocab + 1 + 255) / 256)), dim3(256), 0,
+                           stream, offsets, sorted_tokens, rows, unsigned(vocab));
+        hipLaunchKernelGGL(embedding_words, dim3(unsigned(vocab), unsigned((width / 4 + 63) / 64)),
+                           dim3(64), 0, stream, static_cast<float*>(dwte),
+                           static_cast<const float*>(dx), sorted_rows, offsets, width,
+                           accumulate_wte ? 1 : 0);
+    }
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     // dwpe: column sums of dx viewed as sequences x (length * width).
     const size_t cols = length * width;
+    if (sequences <= 256) {
+        hipLaunchKernelGGL(column_sums_one_chunk, dim3(unsigned((cols / 4 + 255) / 256)),
+                           dim3(256), 0, stream, static_cast<float*>(dwpe),
+                           static_cast<const float*>(dx), int(sequences), cols,
+                           accumulate_wpe ? 1 : 0);
+        return hipGetLastError();
+    }
     const dim3 pgrid(unsigned((cols / 8 + 7) / 8), unsigned((sequences + 255) / 256));
     hipLaunchKernelGGL(column_partials_f32, pgrid, dim3(64), 0, stream,
                        reinterpret_cast<float*>(ws + l.partials), static_cast<const float*>(dx),

@@ -84,7 +84,10 @@ def test_bias_gradient_past_65535_chunks(flint, cuda):
     assert np.array_equal(out.cpu().numpy(), vals.sum(0).astype(np.float32))
 
 
-@pytest.mark.parametrize("rows,cols", [(3, 8), (300, 24), (8192, 768), (100, 4096)])
+# 1 to 4 pieces of 8 columns per lane of the dx kernel and past them (1,032 and
+# 4,096 columns); a last chunk whose phases 1..7 hold no row (257 rows).
+@pytest.mark.parametrize("rows,cols", [(3, 8), (300, 24), (257, 512), (8192, 768), (1000, 1024),
+                                       (9, 1032), (100, 4096)])
 @pytest.mark.parametrize("acc", [False, True])
 def test_layernorm_backward(flint, cuda, rows, cols, acc):
     x = normal((rows, cols), 8)

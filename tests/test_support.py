@@ -48,7 +48,8 @@ def test_embedding_forward_matches_pytorch_bitwise(flint, cuda, sequences, lengt
 
 @pytest.mark.parametrize("sequences,length,vocab,width,kind", [
     (2, 64, 1000, 64, "uniform"), (3, 40, 200, 24, "few"), (1, 2048, 50, 8, "one"),
-    (2, 1500, 5000, 16, "zipf"), (4, 256, 65536, 8, "uniform")])
+    (2, 1500, 5000, 16, "zipf"), (4, 256, 65536, 8, "uniform"), (9, 16, 300, 16, "zipf"),
+    (300, 8, 100, 8, "uniform")])
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_embedding_backward_matches_the_oracle_bitwise(flint, cuda, sequences, length, vocab,
                                                        width, kind, accumulate):
@@ -154,7 +155,8 @@ def test_fp32_to_fp16_edge_values_round_to_nearest_even(flint, cuda):
     flint.fp32_to_fp16(y, xs.to(cuda), len(bits))
     torch.cuda.synchronize()
     got = y.cpu().numpy()
-    expect = bits.view(np.float32).astype(f16)
+    with np.errstate(over="ignore"):   # values past FP16's range round to inf
+        expect = bits.view(np.float32).astype(f16)
     finite = ~np.isnan(expect)
     assert np.array_equal(got[finite].view(np.uint16), expect[finite].view(np.uint16))
     assert np.isnan(got[~finite]).all()
@@ -168,7 +170,8 @@ def test_fp32_to_fp16_matches_numpy_at_every_count(flint, cuda, count):
     y = torch.full((count + 8,), -1, dtype=torch.int16, device=cuda)
     flint.fp32_to_fp16(y, x.to(cuda), count)
     torch.cuda.synchronize()
-    expect = x.numpy().astype(np.float16).view(np.int16)
+    with np.errstate(over="ignore"):   # values past FP16's range round to inf
+        expect = x.numpy().astype(np.float16).view(np.int16)
     got = y.cpu().numpy()
     assert np.array_equal(got[:count], expect)
     assert (got[count:] == -1).all()
