@@ -73,7 +73,9 @@ struct Saved {
     void *x_in = nullptr, *x_mid = nullptr, *x_out = nullptr;
     void *h1 = nullptr, *mean1 = nullptr, *rstd1 = nullptr;
     void *q = nullptr, *k = nullptr, *v = nullptr, *p = nullptr;
-    void *o = nullptr, *lse = nullptr;   // fused attention: heads' output, log-sum-exp
+    // Fused attention: the qkv projection itself ([rows][3 width], whose
+    // heads the kernels read in place) and the log-sum-exp.
+    void *qkv = nullptr, *lse = nullptr;
     void* attn_out = nullptr;
     void *h2 = nullptr, *mean2 = nullptr, *rstd2 = nullptr;
     void *gelu = nullptr, *pre = nullptr;
@@ -290,13 +292,13 @@ flint_status plan(flint_gpt2& m) {
             req(&s.h1, half_rows);
             req(&s.mean1, rows * 4);
             req(&s.rstd1, rows * 4);
-            req(&s.q, heads);
-            req(&s.k, heads);
-            req(&s.v, heads);
             if (m.flash) {
-                req(&s.o, heads);
+                req(&s.qkv, rows * 3 * w * 2);
                 req(&s.lse, m.head_batches * c.length * 4);
             } else {
+                req(&s.q, heads);
+                req(&s.k, heads);
+                req(&s.v, heads);
                 req(&s.p, matrix);
             }
             req(&s.attn_out, half_rows);
@@ -310,17 +312,20 @@ flint_status plan(flint_gpt2& m) {
         req(&m.mean_f, rows * 4);
         req(&m.rstd_f, rows * 4);
         req(&m.qkv, rows * 3 * w * 2);
-        if (m.flash) req(&m.attn_work, m.head_batches * c.length * 4);
-        else req(&m.scores, matrix);
-        req(&m.heads_out, heads);
+        if (m.flash) {
+            req(&m.attn_work, m.head_batches * c.length * 4);
+        } else {
+            req(&m.scores, matrix);
+            req(&m.heads_out, heads);
+            req(&m.dq, heads);
+            req(&m.dk, heads);
+            req(&m.dv, heads);
+        }
         FLINT_TRY(size_workspaces(m));
         req(&m.dres, resid);
         req(&m.dres_half, half_rows);
         req(&m.dh, half_rows);
         req(&m.dpre, rows * 4 * w * 2);
-        req(&m.dq, heads);
-        req(&m.dk, heads);
-        req(&m.dv, heads);
         req(&m.work, m.work_bytes);
         req(&m.tn_work, m.tn_work_bytes);
     } else {
@@ -331,16 +336,16 @@ flint_status plan(flint_gpt2& m) {
         req(&s.mean1, rows * 4);
         req(&s.rstd1, rows * 4);
         req(&m.qkv, rows * 3 * w * 2);
-        req(&s.q, heads);
-        req(&s.k, heads);
-        req(&s.v, heads);
         if (m.flash) {
             req(&s.lse, m.head_batches * c.length * 4);
         } else {
+            req(&s.q, heads);
+            req(&s.k, heads);
+            req(&s.v, heads);
             req(&m.scores, matrix);
             req(&s.p, matrix);
+            req(&m.heads_out, heads);
         }
-        req(&m.heads_out, heads);
         req(&s.attn_out, half_rows);
         req(&s.gelu, rows * 4 * w * 2);
         req(&s.pre, rows * 4 * w * 2);
@@ -482,6 +487,18 @@ flint_status attn_softmax_backward(void* ds, const void* p, const void* dp, size
     return FLINT_OK;
 }
 
+// The fused attention's rows inside the model: head h of sequence n is batch
+// n * heads + h; q, k and v rows are the projection's ([rows][3 width]), o and
+// dO rows the width-wide ones, dq, dk and dv the projection gradient's.
+flint::AttnLayout attn_layout(const flint_gpt2& m) {
+    flint::AttnLayout l;
+    l.heads = int(m.cfg.heads);
+    l.qkv_stride = int(3 * m.cfg.width);
+    l.o_stride = int(m.cfg.width);
+    l.grad_stride = int(3 * m.cfg.width);
+    return l;
+}
+
 flint_status layer_norm(const flint_gpt2& m, const Norm& n, const void* x, void* y, void* mean,
                         void* rstd, flint_stream st) {
     return flint_layernorm_forward(y, mean, rstd, x, n.w->data, n.b->data, m.rows, m.cfg.width,
@@ -495,23 +512,26 @@ flint_status forward_layer(const flint_gpt2& m, const Layer& L, flint_stream st)
     const Saved& s = L.s;
     const size_t rows = m.rows, w = c.width, hw = m.head_width;
     FLINT_TRY(layer_norm(m, L.ln_1, s.x_in, s.h1, s.mean1, s.rstd1, st));
-    FLINT_TRY(flint_gemm_nt_bias(m.qkv, s.h1, L.attn.half, L.attn.b->data, rows, 3 * w, w, st));
-    void* const qkv_parts[] = {s.q, s.k, s.v};
-    FLINT_TRY(attn_heads3(m.qkv, qkv_parts, c.sequences, c.length, c.heads, hw, false, st));
-    // The heads' output: per layer (s.o) when the fused backward reads it.
-    void* heads_o = m.flash && c.backward ? s.o : m.heads_out;
     if (m.flash) {
-        FLINT_HIP_CHECK(flint::launch_attention_forward(heads_o, s.lse, s.q, s.k, s.v,
-                                                        m.head_batches, c.length, score_scale(hw),
-                                                        flint::to_hip(st)));
+        // The kernel reads each head's q, k and v rows inside the projection
+        // and writes its output rows straight into attn_out's columns.
+        auto* qkv = static_cast<_Float16*>(c.backward ? s.qkv : m.qkv);
+        FLINT_TRY(flint_gemm_nt_bias(qkv, s.h1, L.attn.half, L.attn.b->data, rows, 3 * w, w, st));
+        FLINT_HIP_CHECK(flint::launch_attention_forward(
+            s.attn_out, s.lse, qkv, qkv + w, qkv + 2 * w, m.head_batches, c.length,
+            score_scale(hw), flint::to_hip(st), attn_layout(m)));
     } else {
+        FLINT_TRY(flint_gemm_nt_bias(m.qkv, s.h1, L.attn.half, L.attn.b->data, rows, 3 * w, w,
+                                     st));
+        void* const qkv_parts[] = {s.q, s.k, s.v};
+        FLINT_TRY(attn_heads3(m.qkv, qkv_parts, c.sequences, c.length, c.heads, hw, false, st));
         FLINT_TRY(attn_nt(m.scores, s.q, s.k, m.head_batches, c.length, c.length, hw,
                           score_scale(hw), st));
         FLINT_TRY(attn_softmax_forward(s.p, m.scores, m.head_batches, c.length, hw, st));
-        FLINT_TRY(attn_nn(heads_o, s.p, s.v, m.head_batches, c.length, hw, c.length, st));
+        FLINT_TRY(attn_nn(m.heads_out, s.p, s.v, m.head_batches, c.length, hw, c.length, st));
+        FLINT_TRY(flint_heads_merge(s.attn_out, m.heads_out, c.sequences, c.length, c.heads, hw,
+                                    w, 0, st));
     }
-    FLINT_TRY(flint_heads_merge(s.attn_out, heads_o, c.sequences, c.length, c.heads, hw, w, 0,
-                                st));
     FLINT_TRY(flint_gemm_nt_bias_residual(s.x_mid, s.attn_out, L.attn_proj.half,
                                           L.attn_proj.b->data, s.x_in, rows, w, w, st));
     FLINT_TRY(layer_norm(m, L.ln_2, s.x_mid, s.h2, s.mean2, s.rstd2, st));
@@ -580,20 +600,24 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
     FLINT_TRY(weight_grad(m, *L.attn_proj.w, m.dres_half, s.attn_out, acc, st));
     FLINT_TRY(bias_grad(m, *L.attn_proj.b, m.dres_half, acc, st));
     FLINT_TRY(flint_gemm_nn(m.dh, m.dres_half, L.attn_proj.half, rows, w, w, st));
-    FLINT_TRY(flint_heads_split(m.heads_out, m.dh, c.sequences, len, c.heads, hw, w, 0, st));
     if (m.flash) {
-        FLINT_HIP_CHECK(flint::launch_attention_backward(m.dq, m.dk, m.dv, m.heads_out, s.q, s.k,
-                                                         s.v, s.o, s.lse, m.attn_work, nb, len,
-                                                         score_scale(hw), flint::to_hip(st)));
+        // dO rows in dh, O in attn_out, q, k, v in the saved projection; dq,
+        // dk and dv go straight into the qkv gradient's columns.
+        auto* g = static_cast<_Float16*>(m.qkv);
+        const auto* qkv = static_cast<const _Float16*>(s.qkv);
+        FLINT_HIP_CHECK(flint::launch_attention_backward(
+            g, g + w, g + 2 * w, m.dh, qkv, qkv + w, qkv + 2 * w, s.attn_out, s.lse,
+            m.attn_work, nb, len, score_scale(hw), flint::to_hip(st), attn_layout(m)));
     } else {
+        FLINT_TRY(flint_heads_split(m.heads_out, m.dh, c.sequences, len, c.heads, hw, w, 0, st));
         FLINT_TRY(attn_tn(m.dv, s.p, m.heads_out, nb, len, hw, len, st));
         FLINT_TRY(attn_nt(m.scores, m.heads_out, s.v, nb, len, len, hw, 1.0f, st));
         FLINT_TRY(attn_softmax_backward(m.scores, s.p, m.scores, nb, len, hw, st));
         FLINT_TRY(attn_nn(m.dq, m.scores, s.k, nb, len, hw, len, st));
         FLINT_TRY(attn_tn(m.dk, m.scores, s.q, nb, len, hw, len, st));
+        void* const parts[] = {m.dq, m.dk, m.dv};
+        FLINT_TRY(attn_heads3(m.qkv, parts, c.sequences, len, c.heads, hw, true, st));
     }
-    void* const parts[] = {m.dq, m.dk, m.dv};
-    FLINT_TRY(attn_heads3(m.qkv, parts, c.sequences, len, c.heads, hw, true, st));
     FLINT_TRY(weight_grad(m, *L.attn.w, m.qkv, s.h1, acc, st));
     FLINT_TRY(bias_grad(m, *L.attn.b, m.qkv, acc, st));
     FLINT_TRY(flint_gemm_nn(m.dh, m.qkv, L.attn.half, rows, w, 3 * w, st));

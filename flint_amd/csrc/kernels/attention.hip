@@ -3,8 +3,10 @@
 // backward pass to dQ, dK and dV, without materialising the length x length
 // scores or probabilities in HBM.
 //
-// Layout: q, k, v, o, dO, dQ, dK, dV are [batches][length][64] FP16; lse and
-// D (the backward's row sums of dO * O) are [batches][length] FP32.
+// Layout: q, k, v, o, dO, dQ, dK, dV hold 64-half rows of FP16 at a row
+// stride of their own (AttnLayout: [batches][length][64] for the C ABI, the
+// heads' slices of [tokens][width] rows inside the model); lse and D (the
+// backward's row sums of dO * O) are [batches][length] FP32.
 //
 // How the work maps to the hardware:
 //  * Scores come from v_mfma_f32_32x32x16_f16 computing S^T = K Q^T (keys as
@@ -74,16 +76,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* base, unsi
     return __builtin_amdgcn_make_buffer_rsrc(p, 0, bytes, 0x00020000);
 }
 
-// Rows r0 .. r0 + 63 of a [rows][64] FP16 matrix into a tile: 8 loads of 1 KB
-// (8 rows each), two per wave. Lane l writes row l / 8 at chunk position
-// l % 8, which holds global chunk (l % 8) ^ key(row).
+// Rows r0 .. r0 + 63 of a matrix of 64-half rows `stride` halves apart into a
+// tile: 8 loads of 1 KB (8 rows each), two per wave. Lane l writes row l / 8
+// at chunk position l % 8, which holds global chunk (l % 8) ^ key(row).
 __device__ __forceinline__ void load_tile(_Float16* tile, __amdgpu_buffer_rsrc_t rs, int r0,
-                                          int wave, int lane) {
+                                          int stride, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int u = wave + 4 * i;
         const int row = u * 8 + (lane >> 3);
-        const unsigned voff = unsigned(((r0 + row) * kHd + (((lane & 7) ^ akey(row)) * 8)) * 2);
+        const unsigned voff = unsigned(((r0 + row) * stride + (((lane & 7) ^ akey(row)) * 8)) * 2);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (__attribute__((address_space(3))) void*)(lds_half*)(tile + u * 512), 16, voff, 0, 0, 0);
     }
@@ -117,6 +119,19 @@ __device__ __forceinline__ TrPair frag_tr(const _Float16* tile, int k0, int db, 
     return f;
 }
 
+// Batch b's rows in a tensor of row stride `stride`: its first row, and the
+// bytes up to the end of its last one (the buffer resource's length, so that
+// rows at or past `length` read zeros).
+struct Rows {
+    int heads, length;
+    __device__ size_t first(int b, int stride) const {
+        return (size_t(b / heads) * length) * size_t(stride) + size_t(b % heads) * kHd;
+    }
+    __device__ unsigned bytes(int stride) const {
+        return unsigned((size_t(length - 1) * stride + kHd) * 2);
+    }
+};
+
 // The value of lane ^ 32 (the other half of the wave holds the same query).
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
 
@@ -131,7 +146,8 @@ __device__ __forceinline__ f16x8 to_half8(const f32x16& v, int base) {
 
 __global__ void __launch_bounds__(kAttnThreads)
 attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16* q,
-             const _Float16* k, const _Float16* v, int batches, int length, float c) {
+             const _Float16* k, const _Float16* v, int batches, int length, float c, int heads,
+             int in_stride, int o_stride) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[2 * 2 * kTile];   // [buf][K, V]
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -139,11 +155,12 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
     const int nqb = (length + 127) / 128;
     const int qb = nqb - 1 - int(blockIdx.x) / batches;      // longest blocks first
     const int b = int(blockIdx.x) % batches;
-    const size_t mat = size_t(length) * kHd;
-    const unsigned bytes = unsigned(mat * 2);
-    const auto rq = rsrc_of(q + b * mat, bytes);
-    const auto rk = rsrc_of(k + b * mat, bytes);
-    const auto rv = rsrc_of(v + b * mat, bytes);
+    const Rows rows{heads, length};
+    const size_t in_first = rows.first(b, in_stride);
+    const unsigned in_bytes = rows.bytes(in_stride);
+    const auto rq = rsrc_of(q + in_first, in_bytes);
+    const auto rk = rsrc_of(k + in_first, in_bytes);
+    const auto rv = rsrc_of(v + in_first, in_bytes);
     const int q0 = qb * 128 + wave * 32;
     const int qi = q0 + fr;
 
@@ -151,14 +168,15 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
         qf[kk] = __builtin_bit_cast(
-            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, unsigned((qi * kHd + 16 * kk + 8 * h) * 2), 0, 0));
+            f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                       rq, unsigned((qi * in_stride + 16 * kk + 8 * h) * 2), 0, 0));
 
     float m = -INFINITY, l = 0.0f;
     f32x16 oacc[2] = {f32x16{}, f32x16{}};
     const int q_last = min(qb * 128 + 127, length - 1);
     const int nkb = q_last / 64 + 1;
-    load_tile(lds, rk, 0, wave, lane);
-    load_tile(lds + kTile, rv, 0, wave, lane);
+    load_tile(lds, rk, 0, in_stride, wave, lane);
+    load_tile(lds + kTile, rv, 0, in_stride, wave, lane);
     for (int j = 0; j < nkb; ++j) {
         wait_vmcnt<0>();
         block_sync();
@@ -166,8 +184,8 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
         const _Float16* vt = kt + kTile;
         if (j + 1 < nkb) {
             _Float16* nt = lds + ((j + 1) & 1) * 2 * kTile;
-            load_tile(nt, rk, 64 * (j + 1), wave, lane);
-            load_tile(nt + kTile, rv, 64 * (j + 1), wave, lane);
+            load_tile(nt, rk, 64 * (j + 1), in_stride, wave, lane);
+            load_tile(nt + kTile, rv, 64 * (j + 1), in_stride, wave, lane);
         }
         const int kbase = 64 * j;
         if (kbase > q0 + 31) continue;          // every key above every query of the wave
@@ -223,7 +241,7 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
     wait_vmcnt<0>();
     if (qi < length) {
         const float inv = 1.0f / l;
-        _Float16* orow = out + b * mat + size_t(qi) * kHd;
+        _Float16* orow = out + rows.first(b, o_stride) + size_t(qi) * o_stride;
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -241,7 +259,8 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
 __global__ void __launch_bounds__(kAttnThreads)
 attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Float16* q,
                  const _Float16* k, const _Float16* v, const _Float16* o, const _Float16* dout,
-                 const float* lse, int batches, int length, float c, float scale) {
+                 const float* lse, int batches, int length, float c, float scale, int heads,
+                 int in_stride, int o_stride, int g_stride) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[2 * 2 * kTile];   // [buf][K, V]
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -249,29 +268,31 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
     const int nqb = (length + 127) / 128;
     const int qb = nqb - 1 - int(blockIdx.x) / batches;
     const int b = int(blockIdx.x) % batches;
-    const size_t mat = size_t(length) * kHd;
-    const unsigned bytes = unsigned(mat * 2);
-    const auto rq = rsrc_of(q + b * mat, bytes);
-    const auto rk = rsrc_of(k + b * mat, bytes);
-    const auto rv = rsrc_of(v + b * mat, bytes);
-    const auto ro = rsrc_of(o + b * mat, bytes);
-    const auto rdo = rsrc_of(dout + b * mat, bytes);
+    const Rows rows{heads, length};
+    const size_t in_first = rows.first(b, in_stride), o_first = rows.first(b, o_stride);
+    const unsigned in_bytes = rows.bytes(in_stride), o_bytes = rows.bytes(o_stride);
+    const auto rq = rsrc_of(q + in_first, in_bytes);
+    const auto rk = rsrc_of(k + in_first, in_bytes);
+    const auto rv = rsrc_of(v + in_first, in_bytes);
+    const auto ro = rsrc_of(o + o_first, o_bytes);
+    const auto rdo = rsrc_of(dout + o_first, o_bytes);
     const int q0 = qb * 128 + wave * 32;
     const int qi = q0 + fr;
 
     f16x8 qf[4], df[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-        const unsigned off = unsigned((qi * kHd + 16 * kk + 8 * h) * 2);
-        qf[kk] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
-        df[kk] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0));
+        const unsigned in_off = unsigned((qi * in_stride + 16 * kk + 8 * h) * 2);
+        const unsigned o_off = unsigned((qi * o_stride + 16 * kk + 8 * h) * 2);
+        qf[kk] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, in_off, 0, 0));
+        df[kk] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, o_off, 0, 0));
     }
     // D = sum_d dO * O for this lane's query: halves 32 h .. 32 h + 31 here,
     // the rest from lane ^ 32.
     float dd = 0.0f;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-        const unsigned off = unsigned((qi * kHd + 32 * h + 8 * kk) * 2);
+        const unsigned off = unsigned((qi * o_stride + 32 * h + 8 * kk) * 2);
         const f16x8 ov = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, 0));
         const f16x8 gv = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rdo, off, 0, 0));
 #pragma unroll
@@ -284,8 +305,8 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
     f32x16 acc[2] = {f32x16{}, f32x16{}};   // dQ^T[d][q]
     const int q_last = min(qb * 128 + 127, length - 1);
     const int nkb = q_last / 64 + 1;
-    load_tile(lds, rk, 0, wave, lane);
-    load_tile(lds + kTile, rv, 0, wave, lane);
+    load_tile(lds, rk, 0, in_stride, wave, lane);
+    load_tile(lds + kTile, rv, 0, in_stride, wave, lane);
     for (int j = 0; j < nkb; ++j) {
         wait_vmcnt<0>();
         block_sync();
@@ -293,8 +314,8 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
         const _Float16* vt = kt + kTile;
         if (j + 1 < nkb) {
             _Float16* nt = lds + ((j + 1) & 1) * 2 * kTile;
-            load_tile(nt, rk, 64 * (j + 1), wave, lane);
-            load_tile(nt + kTile, rv, 64 * (j + 1), wave, lane);
+            load_tile(nt, rk, 64 * (j + 1), in_stride, wave, lane);
+            load_tile(nt + kTile, rv, 64 * (j + 1), in_stride, wave, lane);
         }
         const int kbase = 64 * j;
         if (kbase > q0 + 31) continue;
@@ -333,7 +354,7 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
     }
     wait_vmcnt<0>();
     if (qi < length) {
-        _Float16* row = dq + b * mat + size_t(qi) * kHd;
+        _Float16* row = dq + rows.first(b, g_stride) + size_t(qi) * g_stride;
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -354,7 +375,8 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
 __global__ void __launch_bounds__(kAttnThreads)
 attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _Float16* q,
                    const _Float16* k, const _Float16* v, const _Float16* dout, const float* lse,
-                   const float* dsum, int batches, int length, float c, float scale) {
+                   const float* dsum, int batches, int length, float c, float scale, int heads,
+                   int in_stride, int o_stride, int g_stride) {
     // [buf][Q tile, dO tile] then [buf][lse2 64, D 64].
     __shared__ __attribute__((aligned(16))) _Float16 lds[2 * 2 * kTile];
     __shared__ __attribute__((aligned(16))) float rowstat[2][2][64];
@@ -364,12 +386,13 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
     const int nkb = (length + 127) / 128;
     const int kb = int(blockIdx.x) / batches;                // earliest keys have the most queries
     const int b = int(blockIdx.x) % batches;
-    const size_t mat = size_t(length) * kHd;
-    const unsigned bytes = unsigned(mat * 2);
-    const auto rq = rsrc_of(q + b * mat, bytes);
-    const auto rk = rsrc_of(k + b * mat, bytes);
-    const auto rv = rsrc_of(v + b * mat, bytes);
-    const auto rdo = rsrc_of(dout + b * mat, bytes);
+    const Rows rows{heads, length};
+    const size_t in_first = rows.first(b, in_stride);
+    const unsigned in_bytes = rows.bytes(in_stride);
+    const auto rq = rsrc_of(q + in_first, in_bytes);
+    const auto rk = rsrc_of(k + in_first, in_bytes);
+    const auto rv = rsrc_of(v + in_first, in_bytes);
+    const auto rdo = rsrc_of(dout + rows.first(b, o_stride), rows.bytes(o_stride));
     const float* lse_b = lse + size_t(b) * length;
     const float* d_b = dsum + size_t(b) * length;
     (void)nkb;
@@ -379,7 +402,7 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
     f16x8 kf[4], vf[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-        const unsigned off = unsigned((ki * kHd + 16 * kk + 8 * h) * 2);
+        const unsigned off = unsigned((ki * in_stride + 16 * kk + 8 * h) * 2);
         kf[kk] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
         vf[kk] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
     }
@@ -397,8 +420,8 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
             lv = lse_b[qq];
             dv0 = d_b[qq];
         }
-        load_tile(t, rq, 64 * qblk, wave, lane);
-        load_tile(t + kTile, rdo, 64 * qblk, wave, lane);
+        load_tile(t, rq, 64 * qblk, in_stride, wave, lane);
+        load_tile(t + kTile, rdo, 64 * qblk, o_stride, wave, lane);
         if (wave == 0) {
             rowstat[buf][0][lane] = lv * kLog2e;
             rowstat[buf][1][lane] = dv0;
@@ -467,8 +490,9 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
     }
     wait_vmcnt<0>();
     if (ki < length) {
-        _Float16* krow = dk + b * mat + size_t(ki) * kHd;
-        _Float16* vrow = dv + b * mat + size_t(ki) * kHd;
+        const size_t g_first = rows.first(b, g_stride);
+        _Float16* krow = dk + g_first + size_t(ki) * g_stride;
+        _Float16* vrow = dv + g_first + size_t(ki) * g_stride;
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -483,37 +507,51 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
     }
 }
 
+// Heads divide the batches, every stride holds a 64-half row, and buffer
+// offsets (32-bit bytes) reach every row.
+bool layout_fits(const AttnLayout& l, size_t batches, size_t length) {
+    if (l.heads < 1 || batches % size_t(l.heads) != 0 || length == 0) return false;
+    for (int s : {l.qkv_stride, l.o_stride, l.grad_stride})
+        if (s < kHd || length * size_t(s) >= (size_t{1} << 30)) return false;
+    return true;
+}
+
 }  // namespace
 
 hipError_t launch_attention_forward(void* out, void* lse, const void* q, const void* k,
                                     const void* v, size_t batches, size_t length, float scale,
-                                    hipStream_t stream) {
+                                    hipStream_t stream, AttnLayout layout) {
+    if (!layout_fits(layout, batches, length)) return hipErrorInvalidValue;
     const unsigned blocks = unsigned(batches * ((length + 127) / 128));
     hipLaunchKernelGGL(attn_forward, dim3(blocks), dim3(kAttnThreads), 0, stream,
                        static_cast<_Float16*>(out), static_cast<float*>(lse),
                        static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
-                       static_cast<const _Float16*>(v), int(batches), int(length), scale * kLog2e);
+                       static_cast<const _Float16*>(v), int(batches), int(length), scale * kLog2e,
+                       layout.heads, layout.qkv_stride, layout.o_stride);
     return hipGetLastError();
 }
 
 hipError_t launch_attention_backward(void* dq, void* dk, void* dv, const void* dout, const void* q,
                                      const void* k, const void* v, const void* o, const void* lse,
                                      void* dsum, size_t batches, size_t length, float scale,
-                                     hipStream_t stream) {
+                                     hipStream_t stream, AttnLayout layout) {
+    if (!layout_fits(layout, batches, length)) return hipErrorInvalidValue;
     const unsigned blocks = unsigned(batches * ((length + 127) / 128));
     hipLaunchKernelGGL(attn_backward_dq, dim3(blocks), dim3(kAttnThreads), 0, stream,
                        static_cast<_Float16*>(dq), static_cast<float*>(dsum),
                        static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
                        static_cast<const _Float16*>(v), static_cast<const _Float16*>(o),
                        static_cast<const _Float16*>(dout), static_cast<const float*>(lse),
-                       int(batches), int(length), scale * kLog2e, scale);
+                       int(batches), int(length), scale * kLog2e, scale, layout.heads,
+                       layout.qkv_stride, layout.o_stride, layout.grad_stride);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     hipLaunchKernelGGL(attn_backward_dkdv, dim3(blocks), dim3(kAttnThreads), 0, stream,
                        static_cast<_Float16*>(dk), static_cast<_Float16*>(dv),
                        static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
                        static_cast<const _Float16*>(v), static_cast<const _Float16*>(dout),
                        static_cast<const float*>(lse), static_cast<const float*>(dsum),
-                       int(batches), int(length), scale * kLog2e, scale);
+                       int(batches), int(length), scale * kLog2e, scale, layout.heads,
+                       layout.qkv_stride, layout.o_stride, layout.grad_stride);
     return hipGetLastError();
 }
 

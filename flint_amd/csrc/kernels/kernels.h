@@ -79,13 +79,25 @@ bool gemm_batched_causal_taken(GemmLayout l, size_t m, size_t n, size_t k);
 // FP32) is the backward's workspace.
 constexpr size_t kAttentionMaxLength = size_t{1} << 20;
 constexpr size_t kAttentionMaxBatches = 65535;
+// Where the rows of batch b live: head b % heads of sequence b / heads, its
+// row t at element (sequence * length + t) * stride + head * 64 of a tensor
+// (q, k, v: qkv_stride; o, dout: o_stride; dq, dk, dv: grad_stride). The
+// C ABI's [batches][length][64] tensors are heads 1, strides 64; the model
+// reads q, k and v straight from its [tokens][3 width] projection and writes
+// o into its [tokens][width] rows. length * stride stays below 2^30.
+struct AttnLayout {
+    int heads = 1;
+    int qkv_stride = 64;
+    int o_stride = 64;
+    int grad_stride = 64;
+};
 hipError_t launch_attention_forward(void* out, void* lse, const void* q, const void* k,
                                     const void* v, size_t batches, size_t length, float scale,
-                                    hipStream_t stream);
+                                    hipStream_t stream, AttnLayout layout = {});
 hipError_t launch_attention_backward(void* dq, void* dk, void* dv, const void* dout, const void* q,
                                      const void* k, const void* v, const void* o, const void* lse,
                                      void* dsum, size_t batches, size_t length, float scale,
-                                     hipStream_t stream);
+                                     hipStream_t stream, AttnLayout layout = {});
 // Rows of a causal tile and the k-step both divide this: a causal softmax
 // writing its zeros up to the end of each such block covers what the causal
 // GEMMs read.

@@ -159,22 +159,18 @@ constexpr int kPhases = 8;   // row phases per chunk: thread y adds rows y, y+8,
 // Partial (sum, error) pairs per 256-row chunk and column, in the reference's
 // order (ref bias_gradient.cu:1-25, layernorm_backward.cu:120-200): for each
 // column, row phase y (0..7) adds rows y, y + 8, ... of the chunk in order,
-// then phase 0 merges phases 1..7 in order. With DGAMMA the values are
-// dy * xhat, xhat = (x - mean) * rstd, the product's rounding error kept;
-// otherwise dy. The chunk's sums go to workspace row 2c, its errors to 2c + 1.
+// then phase 0 merges phases 1..7 in order, over the values of dy. The
+// chunk's sums go to workspace row 2c, its errors to 2c + 1.
 //
 // Workgroup = one chunk x 64 * CPL columns: wave y is phase y, lane l holds
-// CPL adjacent columns, so a wave reads 128 * CPL B of dy (twice that of x) per
-// row. A lane issues all of its (up to 32) row loads before the first add:
+// CPL adjacent columns, so a wave reads 128 * CPL B of dy per row. A lane issues all of its (up to 32) row loads before the first add:
 // every workgroup keeps its whole chunk slice in flight, which makes the pass
 // bandwidth- rather than latency-bound. Workgroup ids run over chunks first
 // (measured faster than tiles first on 8192 x 768 and 8192 x 3072).
-template <bool DGAMMA, int CPL>
+template <int CPL>
 __global__ void __launch_bounds__(kPhases * 64)
-column_partials(float* __restrict__ partial, const _Float16* __restrict__ dy,
-                const float* __restrict__ x, const float* __restrict__ mean,
-                const float* __restrict__ rstd, size_t rows, int cols, size_t chunks,
-                size_t blocks) {
+column_partials(float* __restrict__ partial, const _Float16* __restrict__ dy, size_t rows,
+                int cols, size_t chunks, size_t blocks) {
     constexpr int kPer = kChunkRows / kPhases;   // 32 rows per phase
     constexpr int kTile = 64 * CPL;
     typedef _Float16 hv __attribute__((ext_vector_type(CPL)));
@@ -197,30 +193,18 @@ column_partials(float* __restrict__ partial, const _Float16* __restrict__ dy,
         const size_t step = size_t(kPhases) * size_t(cols);
         size_t at = (first + ph) * size_t(cols) + col;
         hv d[kPer];
-        fv xv[kPer];
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const size_t use = k < n && live ? at : 0;
             d[k] = *reinterpret_cast<const hv*>(dy + use);
-            if (DGAMMA) xv[k] = *reinterpret_cast<const fv*>(x + use);
             at += step;
         }
         Comp acc[CPL];
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             if (k < n) {
-                if (DGAMMA) {
-                    const size_t r = first + ph + size_t(k) * kPhases;
-                    const float mu = mean[r];
-                    const float rs = rstd[r];
 #pragma unroll
-                    for (int j = 0; j < CPL; ++j)
-                        comp_add_product(acc[j], float(d[k][j]),
-                                         mul_rn(sub_rn(xv[k][j], mu), rs));
-                } else {
-#pragma unroll
-                    for (int j = 0; j < CPL; ++j) comp_add(acc[j], float(d[k][j]));
-                }
+                for (int j = 0; j < CPL; ++j) comp_add(acc[j], float(d[k][j]));
             }
         }
         if (ph > 0) {
@@ -355,30 +339,25 @@ column_partials2(float* part0, float* part1, const _Float16* __restrict__ dy,
     }
 }
 
-hipError_t launch_partials(bool dgamma, float* partial, const void* dy, const void* x,
-                           const void* mean, const void* rstd, size_t rows, size_t cols,
+hipError_t launch_partials(float* partial, const void* dy, size_t rows, size_t cols,
                            hipStream_t stream) {
     const size_t chunks = (rows + kChunkRows - 1) / kChunkRows;
-    // FLINT_PARTIALS_CPL=1|2 forces the columns per lane (tuning sweeps).
+    // FLINT_PARTIALS_CPL=1|2|4 forces the columns per lane (tuning sweeps).
     int cpl = 1;
-    if (const char* e = std::getenv("FLINT_PARTIALS_CPL")) cpl = std::atoi(e) == 2 ? 2 : 1;
+    if (const char* e = std::getenv("FLINT_PARTIALS_CPL")) {
+        const int v = std::atoi(e);
+        cpl = v == 2 || v == 4 ? v : 1;
+    }
     const int tiles = int((cols + 64 * cpl - 1) / (64 * cpl));
     const size_t blocks = chunks * size_t(tiles);
     const dim3 grid(unsigned(std::min<size_t>(blocks, kMaxBlocks)));
     const auto* dyh = static_cast<const _Float16*>(dy);
-    const auto* xf = static_cast<const float*>(x);
-    const auto* mf = static_cast<const float*>(mean);
-    const auto* rf = static_cast<const float*>(rstd);
-#define FLINT_PARTIALS(DG, CPL)                                                                 \
-    hipLaunchKernelGGL((column_partials<DG, CPL>), grid, dim3(kPhases * 64), 0, stream, partial, \
-                       dyh, xf, mf, rf, rows, int(cols), chunks, blocks)
-    if (dgamma) {
-        if (cpl == 1) FLINT_PARTIALS(true, 1);
-        else FLINT_PARTIALS(true, 2);
-    } else {
-        if (cpl == 1) FLINT_PARTIALS(false, 1);
-        else FLINT_PARTIALS(false, 2);
-    }
+#define FLINT_PARTIALS(CPL)                                                                    \
+    hipLaunchKernelGGL(column_partials<CPL>, grid, dim3(kPhases * 64), 0, stream, partial, dyh, \
+                       rows, int(cols), chunks, blocks)
+    if (cpl == 1) FLINT_PARTIALS(1);
+    else if (cpl == 2) FLINT_PARTIALS(2);
+    else FLINT_PARTIALS(4);
 #undef FLINT_PARTIALS
     return hipGetLastError();
 }
@@ -872,8 +851,7 @@ hipError_t launch_bias_gradient_finish(void* out, const void* workspace, size_t 
 
 hipError_t launch_bias_gradient(void* dbias, const void* dy, size_t rows, size_t cols,
                                 bool accumulate, void* workspace, hipStream_t stream) {
-    if (hipError_t e = launch_partials(false, static_cast<float*>(workspace), dy, nullptr, nullptr,
-                                       nullptr, rows, cols, stream);
+    if (hipError_t e = launch_partials(static_cast<float*>(workspace), dy, rows, cols, stream);
         e != hipSuccess) {
         return e;
     }
