@@ -372,7 +372,7 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
 // or after its first key. S[q][key] = Q K^T with queries as the MFMA's rows:
 // a lane holds one key (lane % 32) and 16 queries per 32-query block, whose
 // lse and D come from the block's LDS copy.
-__global__ void __launch_bounds__(kAttnThreads)
+__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _Float16* q,
                    const _Float16* k, const _Float16* v, const _Float16* dout, const float* lse,
                    const float* dsum, int batches, int length, float c, float scale, int heads,
@@ -450,12 +450,14 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
                                                                 dp[qh], 0, 0, 0);
             }
         const bool diag = qbase < k0 + 31;
-        f32x16 ds[2];
+        // P and dS = P (dP - D) go to FP16 as they are formed: 16-query
+        // slice cs (of the 64) is MFMA operand pf[cs] / sf[cs].
+        f16x8 pf[4], sf[4];
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
             for (int a = 0; a < 4; ++a) {
-                const int qr = 32 * qh + 8 * a + 4 * h;   // query row in the block, + b
+                const int qr = 32 * qh + 8 * a + 4 * h;   // query row in the block, + e
                 const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2 + qr);
                 const f32x4 d4 = *reinterpret_cast<const f32x4*>(dd + qr);
 #pragma unroll
@@ -464,27 +466,33 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
                     float p = __builtin_amdgcn_exp2f(s[qh][r] * c - l4[e]);
                     if (diag && ki > qbase + qr + e) p = 0.0f;
                     if (qbase + qr + e >= length) p = 0.0f;
-                    s[qh][r] = p;
-                    ds[qh][r] = p * (dp[qh][r] - d4[e]);
+                    const int cs = 2 * qh + (a >> 1), at = 4 * (a & 1) + e;
+                    pf[cs][at] = _Float16(p);
+                    sf[cs][at] = _Float16(p * (dp[qh][r] - d4[e]));
                 }
             }
-        TrPair gtr[4][2], qtr[4][2];
+        // dV^T += dO^T P^T and dK^T += Q^T dS^T, two 16-query slices at a time.
 #pragma unroll
-        for (int cs = 0; cs < 4; ++cs)
+        for (int half = 0; half < 2; ++half) {
+            TrPair gtr[2][2], qtr[2][2];
 #pragma unroll
-            for (int db = 0; db < 2; ++db) {
-                gtr[cs][db] = frag_tr(gt, 16 * cs, db, lane);
-                qtr[cs][db] = frag_tr(qt, 16 * cs, db, lane);
-            }
-        wait_lds();
+            for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-        for (int cs = 0; cs < 4; ++cs) {
-            const f16x8 pf = to_half8(s[cs >> 1], 8 * (cs & 1));
-            const f16x8 sf = to_half8(ds[cs >> 1], 8 * (cs & 1));
+                for (int db = 0; db < 2; ++db) {
+                    gtr[c2][db] = frag_tr(gt, 16 * (2 * half + c2), db, lane);
+                    qtr[c2][db] = frag_tr(qt, 16 * (2 * half + c2), db, lane);
+                }
+            wait_lds();
 #pragma unroll
-            for (int db = 0; db < 2; ++db) {
-                dva[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(gtr[cs][db]), pf, dva[db], 0, 0, 0);
-                dka[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(qtr[cs][db]), sf, dka[db], 0, 0, 0);
+            for (int c2 = 0; c2 < 2; ++c2) {
+                const int cs = 2 * half + c2;
+#pragma unroll
+                for (int db = 0; db < 2; ++db) {
+                    dva[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(gtr[c2][db]), pf[cs],
+                                                                     dva[db], 0, 0, 0);
+                    dka[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(qtr[c2][db]), sf[cs],
+                                                                     dka[db], 0, 0, 0);
+                }
             }
         }
     }
