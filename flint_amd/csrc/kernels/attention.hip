@@ -135,16 +135,9 @@ struct Rows {
 // The value of lane ^ 32 (the other half of the wave holds the same query).
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
 
-__device__ __forceinline__ f16x8 to_half8(const f32x16& v, int base) {
-    f16x8 h;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = _Float16(v[base + e]);
-    return h;
-}
-
 // ---------------------------------------------------------------- forward
 
-__global__ void __launch_bounds__(kAttnThreads)
+__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
 attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16* q,
              const _Float16* k, const _Float16* v, int batches, int length, float c, int heads,
              int in_stride, int o_stride) {
@@ -210,13 +203,15 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
         mx = fmaxf(mx, xor32(mx));
         const float m_new = fmaxf(m, mx);
         const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        // P goes to FP16 as it is formed: 16-key slice cs is pf[cs].
         float sum = 0.0f;
+        f16x8 pf[4];
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float p = __builtin_amdgcn_exp2f(s[hb][r] - m_new);
-                s[hb][r] = p;
+                pf[2 * hb + (r >> 3)][r & 7] = _Float16(p);
                 sum += p;
             }
         sum += xor32(sum);
@@ -224,18 +219,22 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
         m = m_new;
 #pragma unroll
         for (int db = 0; db < 2; ++db) oacc[db] *= alpha;
-        TrPair vf[4][2];
+        // O^T += V^T P^T, two 16-key slices at a time.
 #pragma unroll
-        for (int cs = 0; cs < 4; ++cs)
+        for (int half = 0; half < 2; ++half) {
+            TrPair vf[2][2];
 #pragma unroll
-            for (int db = 0; db < 2; ++db) vf[cs][db] = frag_tr(vt, 16 * cs, db, lane);
-        wait_lds();
+            for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-        for (int cs = 0; cs < 4; ++cs) {
-            const f16x8 pf = to_half8(s[cs >> 1], 8 * (cs & 1));
+                for (int db = 0; db < 2; ++db) vf[c2][db] = frag_tr(vt, 16 * (2 * half + c2), db, lane);
+            wait_lds();
 #pragma unroll
-            for (int db = 0; db < 2; ++db)
-                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(vf[cs][db]), pf, oacc[db], 0, 0, 0);
+            for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(vf[c2][db]),
+                                                                      pf[2 * half + c2], oacc[db], 0,
+                                                                      0, 0);
         }
     }
     wait_vmcnt<0>();
@@ -330,26 +329,32 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
                                                                 dp[hb], 0, 0, 0);
             }
         const bool diag = kbase + 63 > q0;
+        // dS^T = P (dP - D) goes to FP16 as it is formed: 16-key slice cs is sf[cs].
+        f16x8 sf[4];
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 float p = __builtin_amdgcn_exp2f(s[hb][r] * c - lse2);
                 if (diag && kbase + 32 * hb + 8 * (r >> 2) + 4 * h + (r & 3) > qi) p = 0.0f;
-                s[hb][r] = p * (dp[hb][r] - dd);       // dS^T
+                sf[2 * hb + (r >> 3)][r & 7] = _Float16(p * (dp[hb][r] - dd));
             }
-        TrPair kf[4][2];
+        // dQ^T += K^T dS^T, two 16-key slices at a time.
 #pragma unroll
-        for (int cs = 0; cs < 4; ++cs)
+        for (int half = 0; half < 2; ++half) {
+            TrPair kf[2][2];
 #pragma unroll
-            for (int db = 0; db < 2; ++db) kf[cs][db] = frag_tr(kt, 16 * cs, db, lane);
-        wait_lds();
+            for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-        for (int cs = 0; cs < 4; ++cs) {
-            const f16x8 sf = to_half8(s[cs >> 1], 8 * (cs & 1));
+                for (int db = 0; db < 2; ++db) kf[c2][db] = frag_tr(kt, 16 * (2 * half + c2), db, lane);
+            wait_lds();
 #pragma unroll
-            for (int db = 0; db < 2; ++db)
-                acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(kf[cs][db]), sf, acc[db], 0, 0, 0);
+            for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(kf[c2][db]),
+                                                                     sf[2 * half + c2], acc[db], 0,
+                                                                     0, 0);
         }
     }
     wait_vmcnt<0>();
