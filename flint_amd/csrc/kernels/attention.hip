@@ -35,6 +35,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "common/common.h"
 #include "kernels/gemm_common.h"
@@ -189,17 +190,23 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
             for (int hb = 0; hb < 2; ++hb)
                 s[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(kt, 32 * hb, kk, lane), qf[kk],
                                                                s[hb], 0, 0, 0);
-        const bool diag = kbase + 63 > q0;
+        // Scaled scores; keys above the query masked in the diagonal block
+        // only (a uniform branch: the other blocks skip the compares).
         float mx = -INFINITY;
+        auto scale_scores = [&](auto masked) {
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb)
+            for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float t = s[hb][r] * c;
-                if (diag && kbase + 32 * hb + 8 * (r >> 2) + 4 * h + (r & 3) > qi) t = -INFINITY;
-                s[hb][r] = t;
-                mx = fmaxf(mx, t);
-            }
+                for (int r = 0; r < 16; ++r) {
+                    float t = s[hb][r] * c;
+                    if constexpr (masked)
+                        if (kbase + 32 * hb + 8 * (r >> 2) + 4 * h + (r & 3) > qi) t = -INFINITY;
+                    s[hb][r] = t;
+                    mx = fmaxf(mx, t);
+                }
+        };
+        if (kbase + 63 > q0) scale_scores(std::true_type{});
+        else scale_scores(std::false_type{});
         mx = fmaxf(mx, xor32(mx));
         const float m_new = fmaxf(m, mx);
         const float alpha = __builtin_amdgcn_exp2f(m - m_new);
@@ -255,7 +262,7 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
 
 // ---------------------------------------------------------------- backward: dQ (and D)
 
-__global__ void __launch_bounds__(kAttnThreads)
+__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Float16* q,
                  const _Float16* k, const _Float16* v, const _Float16* o, const _Float16* dout,
                  const float* lse, int batches, int length, float c, float scale, int heads,
@@ -328,17 +335,22 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
                 dp[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(vt, 32 * hb, kk, lane), df[kk],
                                                                 dp[hb], 0, 0, 0);
             }
-        const bool diag = kbase + 63 > q0;
-        // dS^T = P (dP - D) goes to FP16 as it is formed: 16-key slice cs is sf[cs].
+        // dS^T = P (dP - D) goes to FP16 as it is formed: 16-key slice cs is
+        // sf[cs]. Keys above the query are masked in the diagonal block only.
         f16x8 sf[4];
+        auto form_ds = [&](auto masked) {
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb)
+            for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float p = __builtin_amdgcn_exp2f(s[hb][r] * c - lse2);
-                if (diag && kbase + 32 * hb + 8 * (r >> 2) + 4 * h + (r & 3) > qi) p = 0.0f;
-                sf[2 * hb + (r >> 3)][r & 7] = _Float16(p * (dp[hb][r] - dd));
-            }
+                for (int r = 0; r < 16; ++r) {
+                    float p = __builtin_amdgcn_exp2f(s[hb][r] * c - lse2);
+                    if constexpr (masked)
+                        if (kbase + 32 * hb + 8 * (r >> 2) + 4 * h + (r & 3) > qi) p = 0.0f;
+                    sf[2 * hb + (r >> 3)][r & 7] = _Float16(p * (dp[hb][r] - dd));
+                }
+        };
+        if (kbase + 63 > q0) form_ds(std::true_type{});
+        else form_ds(std::false_type{});
         // dQ^T += K^T dS^T, two 16-key slices at a time.
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
@@ -454,28 +466,35 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
                 dp[qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(gt, 32 * qh, kk, lane), vf[kk],
                                                                 dp[qh], 0, 0, 0);
             }
-        const bool diag = qbase < k0 + 31;
         // P and dS = P (dP - D) go to FP16 as they are formed: 16-query
-        // slice cs (of the 64) is MFMA operand pf[cs] / sf[cs].
+        // slice cs (of the 64) is MFMA operand pf[cs] / sf[cs]. Queries
+        // before the key, and past the sequence, are masked only in the
+        // blocks that hold any (a uniform branch).
         f16x8 pf[4], sf[4];
+        auto form_p_ds = [&](auto masked) {
 #pragma unroll
-        for (int qh = 0; qh < 2; ++qh)
+            for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const int qr = 32 * qh + 8 * a + 4 * h;   // query row in the block, + e
-                const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2 + qr);
-                const f32x4 d4 = *reinterpret_cast<const f32x4*>(dd + qr);
+                for (int a = 0; a < 4; ++a) {
+                    const int qr = 32 * qh + 8 * a + 4 * h;   // query row in the block, + e
+                    const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2 + qr);
+                    const f32x4 d4 = *reinterpret_cast<const f32x4*>(dd + qr);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * a + e;
-                    float p = __builtin_amdgcn_exp2f(s[qh][r] * c - l4[e]);
-                    if (diag && ki > qbase + qr + e) p = 0.0f;
-                    if (qbase + qr + e >= length) p = 0.0f;
-                    const int cs = 2 * qh + (a >> 1), at = 4 * (a & 1) + e;
-                    pf[cs][at] = _Float16(p);
-                    sf[cs][at] = _Float16(p * (dp[qh][r] - d4[e]));
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 4 * a + e;
+                        float p = __builtin_amdgcn_exp2f(s[qh][r] * c - l4[e]);
+                        if constexpr (masked) {
+                            if (ki > qbase + qr + e) p = 0.0f;
+                            if (qbase + qr + e >= length) p = 0.0f;
+                        }
+                        const int cs = 2 * qh + (a >> 1), at = 4 * (a & 1) + e;
+                        pf[cs][at] = _Float16(p);
+                        sf[cs][at] = _Float16(p * (dp[qh][r] - d4[e]));
+                    }
                 }
-            }
+        };
+        if (qbase < k0 + 31 || qbase + 63 >= length) form_p_ds(std::true_type{});
+        else form_p_ds(std::false_type{});
         // dV^T += dO^T P^T and dK^T += Q^T dS^T, two 16-query slices at a time.
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
