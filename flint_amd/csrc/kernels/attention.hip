@@ -456,24 +456,25 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
         if (qblk + 1 < nqb) stage_rows(buf ^ 1, qblk + 1);
         const int qbase = 64 * qblk;
         if (qbase + 63 < k0) continue;        // every query of the block precedes every key of the wave
-        f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+        // The block in two halves of 32 queries, each through all of its
+        // products before the next (fewer registers live at once).
+        const bool masked = qbase < k0 + 31 || qbase + 63 >= length;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
+        for (int qh = 0; qh < 2; ++qh) {
+            f32x16 s = {}, dp = {};
 #pragma unroll
-            for (int qh = 0; qh < 2; ++qh) {
-                s[qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(qt, 32 * qh, kk, lane), kf[kk],
-                                                               s[qh], 0, 0, 0);
-                dp[qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(gt, 32 * qh, kk, lane), vf[kk],
-                                                                dp[qh], 0, 0, 0);
+            for (int kk = 0; kk < 4; ++kk) {
+                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(qt, 32 * qh, kk, lane), kf[kk],
+                                                           s, 0, 0, 0);
+                dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(gt, 32 * qh, kk, lane), vf[kk],
+                                                            dp, 0, 0, 0);
             }
-        // P and dS = P (dP - D) go to FP16 as they are formed: 16-query
-        // slice cs (of the 64) is MFMA operand pf[cs] / sf[cs]. Queries
-        // before the key, and past the sequence, are masked only in the
-        // blocks that hold any (a uniform branch).
-        f16x8 pf[4], sf[4];
-        auto form_p_ds = [&](auto masked) {
-#pragma unroll
-            for (int qh = 0; qh < 2; ++qh)
+            // P and dS = P (dP - D) go to FP16 as they are formed: 16-query
+            // slice c2 of the half is MFMA operand pf[c2] / sf[c2]. Queries
+            // before the key, and past the sequence, are masked only in the
+            // blocks that hold any (a uniform branch).
+            f16x8 pf[2], sf[2];
+            auto form_p_ds = [&](auto mask) {
 #pragma unroll
                 for (int a = 0; a < 4; ++a) {
                     const int qr = 32 * qh + 8 * a + 4 * h;   // query row in the block, + e
@@ -482,42 +483,38 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int r = 4 * a + e;
-                        float p = __builtin_amdgcn_exp2f(s[qh][r] * c - l4[e]);
-                        if constexpr (masked) {
+                        float p = __builtin_amdgcn_exp2f(s[r] * c - l4[e]);
+                        if constexpr (mask) {
                             if (ki > qbase + qr + e) p = 0.0f;
                             if (qbase + qr + e >= length) p = 0.0f;
                         }
-                        const int cs = 2 * qh + (a >> 1), at = 4 * (a & 1) + e;
-                        pf[cs][at] = _Float16(p);
-                        sf[cs][at] = _Float16(p * (dp[qh][r] - d4[e]));
+                        const int c2 = a >> 1, at = 4 * (a & 1) + e;
+                        pf[c2][at] = _Float16(p);
+                        sf[c2][at] = _Float16(p * (dp[r] - d4[e]));
                     }
                 }
-        };
-        if (qbase < k0 + 31 || qbase + 63 >= length) form_p_ds(std::true_type{});
-        else form_p_ds(std::false_type{});
-        // dV^T += dO^T P^T and dK^T += Q^T dS^T, two 16-query slices at a time.
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
+            };
+            if (masked) form_p_ds(std::true_type{});
+            else form_p_ds(std::false_type{});
+            // dV^T += dO^T P^T and dK^T += Q^T dS^T over the half's 32 queries.
             TrPair gtr[2][2], qtr[2][2];
 #pragma unroll
             for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
                 for (int db = 0; db < 2; ++db) {
-                    gtr[c2][db] = frag_tr(gt, 16 * (2 * half + c2), db, lane);
-                    qtr[c2][db] = frag_tr(qt, 16 * (2 * half + c2), db, lane);
+                    gtr[c2][db] = frag_tr(gt, 16 * (2 * qh + c2), db, lane);
+                    qtr[c2][db] = frag_tr(qt, 16 * (2 * qh + c2), db, lane);
                 }
             wait_lds();
 #pragma unroll
-            for (int c2 = 0; c2 < 2; ++c2) {
-                const int cs = 2 * half + c2;
+            for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
                 for (int db = 0; db < 2; ++db) {
-                    dva[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(gtr[c2][db]), pf[cs],
+                    dva[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(gtr[c2][db]), pf[c2],
                                                                      dva[db], 0, 0, 0);
-                    dka[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(qtr[c2][db]), sf[cs],
+                    dka[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(qtr[c2][db]), sf[c2],
                                                                      dka[db], 0, 0, 0);
                 }
-            }
         }
     }
     wait_vmcnt<0>();
