@@ -92,32 +92,67 @@ __device__ __forceinline__ void load_tile(_Float16* tile, __amdgpu_buffer_rsrc_t
     }
 }
 
+// Per-lane byte offsets of the fragment reads inside a 64-row tile, computed
+// once per kernel and kept in registers (an empty asm makes them opaque, so
+// they are not recomputed per read): the row-major read of (32 hb, kk) is
+// rows[kk] + 4096 hb, the transposing reads of (16 cs, db) are tr[db][0 | 1]
+// + 2048 cs. The key (row >> 1) & 7 of the XOR swizzle is the same for rows
+// 32 or 16 apart, which is what lets hb and cs become immediate offsets.
+struct FragOff {
+    unsigned rows[4];
+    unsigned tr[2][2];
+};
+__device__ __forceinline__ FragOff frag_offsets(int lane) {
+    FragOff f;
+    const int fr = lane & 31, h = lane >> 5, j = lane & 15;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        f.rows[kk] = unsigned((fr * kHd + (((2 * kk + h) ^ akey(fr)) * 8)) * 2);
+        asm volatile("" : "+v"(f.rows[kk]));
+    }
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int row = 4 * h + (j >> 2) + 8 * t;
+            const int col = 32 * db + 16 * ((lane >> 4) & 1) + 4 * (j & 3);
+            f.tr[db][t] = unsigned((row * kHd + (((col >> 3) ^ akey(row)) * 8) + (col & 7)) * 2);
+            asm volatile("" : "+v"(f.tr[db][t]));
+        }
+    return f;
+}
+
 // An MFMA operand with tile rows as its rows and d as k: lane l gets row
-// r0 + l % 32, halves 16 kk + 8 (l / 32) .. + 8.
-__device__ __forceinline__ f16x8 frag_rows(const _Float16* tile, int r0, int kk, int lane) {
-    const int row = r0 + (lane & 31);
-    const int chunk = kk * 2 + (lane >> 5);
-    return *reinterpret_cast<const f16x8*>(tile + row * kHd + ((chunk ^ akey(row)) * 8));
+// 32 hb + l % 32, halves 16 kk + 8 (l / 32) .. + 8.
+__device__ __forceinline__ f16x8 frag_rows(const _Float16* tile, const FragOff& fo, int hb, int kk) {
+    return *reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(tile) + fo.rows[kk] +
+                                           4096 * hb);
 }
 
 // An MFMA operand with d as its rows and tile rows as k, in the permuted k
 // order of the register-held probabilities: lane l (d = 32 db + l % 32,
-// h = l / 32) gets tile rows k0 + 4h .. + 3 (k 0..3) and k0 + 8 + 4h .. + 3
-// (k 4..7) of column d. Within 16 lanes, lane j addresses 4 halves of row
-// base + j / 4 at column c0 + 4 (j % 4); lane i receives column c0 + i.
-__device__ __forceinline__ TrPair frag_tr(const _Float16* tile, int k0, int db, int lane) {
-    const int j = lane & 15;
-    const int c0 = 32 * db + 16 * ((lane >> 4) & 1);
-    const int base = k0 + 4 * (lane >> 5);
-    const int col = c0 + 4 * (j & 3);
-    auto addr = [&](int row) {
-        return unsigned(reinterpret_cast<uintptr_t>(
-            (lds_half*)(tile + row * kHd + (((col >> 3) ^ akey(row)) * 8) + (col & 7))));
-    };
+// h = l / 32) gets tile rows 16 cs + 4h .. + 3 (k 0..3) and 16 cs + 8 + 4h ..
+// + 3 (k 4..7) of column d. Within 16 lanes, lane j addresses 4 halves of row
+// 16 cs + 4h + j / 4 (+ 8) at column 32 db + 16 ((l / 16) % 2) + 4 (j % 4);
+// lane i receives column 32 db + 16 ((l / 16) % 2) + i.
+template <int CS>
+__device__ __forceinline__ TrPair frag_tr(const _Float16* tile, const FragOff& fo, int db) {
+    const unsigned base = unsigned(reinterpret_cast<uintptr_t>((lds_half*)tile));
     TrPair f;
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(f.lo) : "v"(addr(base + (j >> 2))));
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(f.hi) : "v"(addr(base + 8 + (j >> 2))));
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                 : "=v"(f.lo) : "v"(base + fo.tr[db][0]), "i"(2048 * CS));
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                 : "=v"(f.hi) : "v"(base + fo.tr[db][1]), "i"(2048 * CS));
     return f;
+}
+// frag_tr for a slice index known once the loops are unrolled.
+__device__ __forceinline__ TrPair frag_tr(const _Float16* tile, const FragOff& fo, int cs, int db) {
+    switch (cs) {
+    case 0: return frag_tr<0>(tile, fo, db);
+    case 1: return frag_tr<1>(tile, fo, db);
+    case 2: return frag_tr<2>(tile, fo, db);
+    default: return frag_tr<3>(tile, fo, db);
+    }
 }
 
 // Batch b's rows in a tensor of row stride `stride`: its first row, and the
@@ -146,6 +181,7 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int fr = lane & 31, h = lane >> 5;
+    const FragOff fo = frag_offsets(lane);
     const int nqb = (length + 127) / 128;
     const int qb = nqb - 1 - int(blockIdx.x) / batches;      // longest blocks first
     const int b = int(blockIdx.x) % batches;
@@ -188,7 +224,7 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
         for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb)
-                s[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(kt, 32 * hb, kk, lane), qf[kk],
+                s[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(kt, fo, hb, kk), qf[kk],
                                                                s[hb], 0, 0, 0);
         // Scaled scores; keys above the query masked in the diagonal block
         // only (a uniform branch: the other blocks skip the compares).
@@ -233,7 +269,7 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
 #pragma unroll
             for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-                for (int db = 0; db < 2; ++db) vf[c2][db] = frag_tr(vt, 16 * (2 * half + c2), db, lane);
+                for (int db = 0; db < 2; ++db) vf[c2][db] = frag_tr(vt, fo, 2 * half + c2, db);
             wait_lds();
 #pragma unroll
             for (int c2 = 0; c2 < 2; ++c2)
@@ -271,6 +307,7 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int fr = lane & 31, h = lane >> 5;
+    const FragOff fo = frag_offsets(lane);
     const int nqb = (length + 127) / 128;
     const int qb = nqb - 1 - int(blockIdx.x) / batches;
     const int b = int(blockIdx.x) % batches;
@@ -330,9 +367,9 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
         for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb) {
-                s[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(kt, 32 * hb, kk, lane), qf[kk],
+                s[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(kt, fo, hb, kk), qf[kk],
                                                                s[hb], 0, 0, 0);
-                dp[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(vt, 32 * hb, kk, lane), df[kk],
+                dp[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(vt, fo, hb, kk), df[kk],
                                                                 dp[hb], 0, 0, 0);
             }
         // dS^T = P (dP - D) goes to FP16 as it is formed: 16-key slice cs is
@@ -358,7 +395,7 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
 #pragma unroll
             for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-                for (int db = 0; db < 2; ++db) kf[c2][db] = frag_tr(kt, 16 * (2 * half + c2), db, lane);
+                for (int db = 0; db < 2; ++db) kf[c2][db] = frag_tr(kt, fo, 2 * half + c2, db);
             wait_lds();
 #pragma unroll
             for (int c2 = 0; c2 < 2; ++c2)
@@ -400,6 +437,7 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int fr = lane & 31, h = lane >> 5;
+    const FragOff fo = frag_offsets(lane);
     const int nkb = (length + 127) / 128;
     const int kb = int(blockIdx.x) / batches;                // earliest keys have the most queries
     const int b = int(blockIdx.x) % batches;
@@ -464,9 +502,9 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
             f32x16 s = {}, dp = {};
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(qt, 32 * qh, kk, lane), kf[kk],
+                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(qt, fo, qh, kk), kf[kk],
                                                            s, 0, 0, 0);
-                dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(gt, 32 * qh, kk, lane), vf[kk],
+                dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(gt, fo, qh, kk), vf[kk],
                                                             dp, 0, 0, 0);
             }
             // P and dS = P (dP - D) go to FP16 as they are formed: 16-query
@@ -502,8 +540,8 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
             for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
                 for (int db = 0; db < 2; ++db) {
-                    gtr[c2][db] = frag_tr(gt, 16 * (2 * qh + c2), db, lane);
-                    qtr[c2][db] = frag_tr(qt, 16 * (2 * qh + c2), db, lane);
+                    gtr[c2][db] = frag_tr(gt, fo, 2 * qh + c2, db);
+                    qtr[c2][db] = frag_tr(qt, fo, 2 * qh + c2, db);
                 }
             wait_lds();
 #pragma unroll
