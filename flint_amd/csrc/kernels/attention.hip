@@ -298,7 +298,7 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
 
 // ---------------------------------------------------------------- backward: dQ (and D)
 
-__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
 attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Float16* q,
                  const _Float16* k, const _Float16* v, const _Float16* o, const _Float16* dout,
                  const float* lse, int batches, int length, float c, float scale, int heads,
@@ -362,48 +362,47 @@ attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Flo
         }
         const int kbase = 64 * j;
         if (kbase > q0 + 31) continue;
-        f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+        // The block in two halves of 32 keys, each through all of its
+        // products before the next (fewer registers live at once).
+        const bool masked = kbase + 63 > q0;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
+        for (int hb = 0; hb < 2; ++hb) {
+            f32x16 s = {}, dp = {};
 #pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                s[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(kt, fo, hb, kk), qf[kk],
-                                                               s[hb], 0, 0, 0);
-                dp[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(vt, fo, hb, kk), df[kk],
-                                                                dp[hb], 0, 0, 0);
+            for (int kk = 0; kk < 4; ++kk) {
+                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(kt, fo, hb, kk), qf[kk], s, 0,
+                                                           0, 0);
+                dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(vt, fo, hb, kk), df[kk], dp,
+                                                            0, 0, 0);
             }
-        // dS^T = P (dP - D) goes to FP16 as it is formed: 16-key slice cs is
-        // sf[cs]. Keys above the query are masked in the diagonal block only.
-        f16x8 sf[4];
-        auto form_ds = [&](auto masked) {
-#pragma unroll
-            for (int hb = 0; hb < 2; ++hb)
+            // dS^T = P (dP - D) goes to FP16 as it is formed: 16-key slice c2
+            // of the half is sf[c2]. Keys above the query are masked in the
+            // diagonal block only.
+            f16x8 sf[2];
+            auto form_ds = [&](auto mask) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    float p = __builtin_amdgcn_exp2f(s[hb][r] * c - lse2);
-                    if constexpr (masked)
+                    float p = __builtin_amdgcn_exp2f(s[r] * c - lse2);
+                    if constexpr (mask)
                         if (kbase + 32 * hb + 8 * (r >> 2) + 4 * h + (r & 3) > qi) p = 0.0f;
-                    sf[2 * hb + (r >> 3)][r & 7] = _Float16(p * (dp[hb][r] - dd));
+                    sf[r >> 3][r & 7] = _Float16(p * (dp[r] - dd));
                 }
-        };
-        if (kbase + 63 > q0) form_ds(std::true_type{});
-        else form_ds(std::false_type{});
-        // dQ^T += K^T dS^T, two 16-key slices at a time.
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
+            };
+            if (masked) form_ds(std::true_type{});
+            else form_ds(std::false_type{});
+            // dQ^T += K^T dS^T over the half's 32 keys.
             TrPair kf[2][2];
 #pragma unroll
             for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-                for (int db = 0; db < 2; ++db) kf[c2][db] = frag_tr(kt, fo, 2 * half + c2, db);
+                for (int db = 0; db < 2; ++db) kf[c2][db] = frag_tr(kt, fo, 2 * hb + c2, db);
             wait_lds();
 #pragma unroll
             for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
                 for (int db = 0; db < 2; ++db)
-                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(kf[c2][db]),
-                                                                     sf[2 * half + c2], acc[db], 0,
-                                                                     0, 0);
+                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(join(kf[c2][db]), sf[c2],
+                                                                     acc[db], 0, 0, 0);
         }
     }
     wait_vmcnt<0>();
