@@ -307,13 +307,22 @@ column_partials2(float* part0, float* part1, const _Float16* __restrict__ dy,
             xv[k] = x[use];
             at += step;
         }
+        // The phase's rows' mean and rstd, lane k holding row k's, loaded with
+        // the rows (per-row scalar loads inside the chain below would each
+        // wait out a round trip) and taken lane by lane.
+        const size_t mrow = lane < n ? first + ph + size_t(lane) * kPhases : 0;
+        const float mean_l = mean[mrow];
+        const float rstd_l = rstd[mrow];
         Comp acc[2];
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             if (k < n) {
-                const size_t r = first + ph + size_t(k) * kPhases;
+                const float mu = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mean_l), k));
+                const float rs = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, rstd_l), k));
                 comp_add(acc[0], float(d[k]));
-                comp_add_product(acc[1], float(d[k]), mul_rn(sub_rn(xv[k], mean[r]), rstd[r]));
+                comp_add_product(acc[1], float(d[k]), mul_rn(sub_rn(xv[k], mu), rs));
             }
         }
         if (ph > 0) {
