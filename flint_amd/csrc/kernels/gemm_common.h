@@ -48,7 +48,10 @@ __device__ __forceinline__ float gelu(float s) {
 // d/ds [s sigma(2u)] = sigma + s sigma (1 - sigma) 2u', 2u' = 2 sqrt(2/pi)
 // (1 + 3 * 0.044715 s^2). 1 - sigma is taken as e sigma for s >= 0 (keeps
 // precision as sigma -> 1) and directly for s < 0 (e may overflow there).
-// Infinite s returns GELU's limits; NaN propagates.
+// Infinite s returns GELU's limits; NaN propagates. Every lane computes g and
+// then selects: the empty asm keeps the compiler from moving g's arithmetic
+// into a branch around the rare infinite case (per element, that branch cost
+// more than the arithmetic it skipped).
 __device__ __forceinline__ float gelu_grad(float s) {
     constexpr float c0 = -2.3022082f;
     constexpr float c1 = -0.10294324f;
@@ -56,7 +59,8 @@ __device__ __forceinline__ float gelu_grad(float s) {
     const float sigma = __builtin_amdgcn_rcpf(1.0f + e);
     const float one_minus = s < 0.0f ? 1.0f - sigma : e * sigma;
     const float q = s * one_minus * __builtin_fmaf(0.21406444860866706f, s * s, 1.5957691216057308f);
-    const float g = __builtin_fmaf(sigma, q, sigma);
+    float g = __builtin_fmaf(sigma, q, sigma);
+    asm volatile("" : "+v"(g));
     return __builtin_isinf(s) ? (s > 0.0f ? 1.0f : 0.0f) : g;
 }
 
