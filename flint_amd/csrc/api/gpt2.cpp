@@ -552,6 +552,31 @@ flint_status bias_grad(const flint_gpt2& m, const Param& p, const void* dy, int 
     return flint_bias_gradient(p.grad, dy, m.rows, p.cols, acc, m.work, m.work_bytes, st);
 }
 
+// A linear layer's weight and bias gradients from its output gradient dy
+// (FP16, rows x w.rows) and input x: the TN product into its k-split
+// partials, the bias's chunk partials, then one launch that sums the first
+// and merges the second, in place of flint_gemm_tn's and
+// flint_bias_gradient's two launches each (the same kernels' arithmetic, the
+// same bits). FLINT_FUSED_GRADS=0 calls the two entry points instead (the
+// tests compare the two).
+flint_status linear_grads(const flint_gpt2& m, const Param& w, const Param& b, const void* dy,
+                          const void* x, int acc, flint_stream st) {
+    const char* e = std::getenv("FLINT_FUSED_GRADS");
+    if (e != nullptr && e[0] == '0' && e[1] == '\0') {
+        FLINT_TRY(weight_grad(m, w, dy, x, acc, st));
+        return bias_grad(m, b, dy, acc, st);
+    }
+    const hipStream_t hs = flint::to_hip(st);
+    int splits = 1;
+    FLINT_HIP_CHECK(flint::launch_gemm_tn_split(w.grad, dy, x, w.rows, w.cols, m.rows, acc != 0,
+                                                m.tn_work, &splits, hs));
+    FLINT_HIP_CHECK(flint::launch_bias_partials(m.work, dy, m.rows, b.cols, hs));
+    FLINT_HIP_CHECK(flint::launch_linear_grads_finish(w.grad, m.tn_work, w.rows, w.cols, splits,
+                                                      acc != 0, b.grad, m.work, m.rows, b.cols,
+                                                      acc != 0, hs));
+    return FLINT_OK;
+}
+
 // LayerNorm backward: dx, with its FP16 copy written by the dx kernel, then
 // dbeta and dgamma from one pass over dy and x. FLINT_FUSED_SUMS=0 calls
 // flint_layernorm_backward instead and converts dx to FP16 after it (the
@@ -589,16 +614,13 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
 
     // dres_half = RN16(dres): written by the LayerNorm backward that produced
     // dres (norm_backward), in place of the reference's conversion here.
-    FLINT_TRY(weight_grad(m, *L.fc_proj.w, m.dres_half, s.gelu, acc, st));
-    FLINT_TRY(bias_grad(m, *L.fc_proj.b, m.dres_half, acc, st));
+    FLINT_TRY(linear_grads(m, *L.fc_proj.w, *L.fc_proj.b, m.dres_half, s.gelu, acc, st));
     FLINT_TRY(flint_gemm_nn_dgelu(m.dpre, m.dres_half, L.fc_proj.half, s.pre, rows, 4 * w, w, st));
-    FLINT_TRY(weight_grad(m, *L.fc.w, m.dpre, s.h2, acc, st));
-    FLINT_TRY(bias_grad(m, *L.fc.b, m.dpre, acc, st));
+    FLINT_TRY(linear_grads(m, *L.fc.w, *L.fc.b, m.dpre, s.h2, acc, st));
     FLINT_TRY(flint_gemm_nn(m.dh, m.dpre, L.fc.half, rows, w, 4 * w, st));
     FLINT_TRY(norm_backward(m, L.ln_2, s.x_mid, s.mean2, s.rstd2, 1, acc, st));
 
-    FLINT_TRY(weight_grad(m, *L.attn_proj.w, m.dres_half, s.attn_out, acc, st));
-    FLINT_TRY(bias_grad(m, *L.attn_proj.b, m.dres_half, acc, st));
+    FLINT_TRY(linear_grads(m, *L.attn_proj.w, *L.attn_proj.b, m.dres_half, s.attn_out, acc, st));
     FLINT_TRY(flint_gemm_nn(m.dh, m.dres_half, L.attn_proj.half, rows, w, w, st));
     if (m.flash) {
         // dO rows in dh, O in attn_out, q, k, v in the saved projection; dq,
@@ -618,8 +640,7 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
         void* const parts[] = {m.dq, m.dk, m.dv};
         FLINT_TRY(attn_heads3(m.qkv, parts, c.sequences, len, c.heads, hw, true, st));
     }
-    FLINT_TRY(weight_grad(m, *L.attn.w, m.qkv, s.h1, acc, st));
-    FLINT_TRY(bias_grad(m, *L.attn.b, m.qkv, acc, st));
+    FLINT_TRY(linear_grads(m, *L.attn.w, *L.attn.b, m.qkv, s.h1, acc, st));
     FLINT_TRY(flint_gemm_nn(m.dh, m.qkv, L.attn.half, rows, w, 3 * w, st));
     return norm_backward(m, L.ln_1, s.x_in, s.mean1, s.rstd1, 1, acc, st);
 }

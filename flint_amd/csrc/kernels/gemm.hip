@@ -40,6 +40,7 @@
 #include "common/common.h"
 #include "kernels/kernels.h"
 #include "kernels/gemm_common.h"
+#include "kernels/split_sum.h"
 
 namespace flint {
 namespace {
@@ -597,19 +598,13 @@ gemm_kernel(Operands op, TileArgs ta) {
 }
 
 // Adds a split TN's partials in split order: y = old + (p0 + p1 + ...), or
-// y = p0 + p1 + ... (ref src/kernels/gemm.cu:678-703 for the order).
+// y = p0 + p1 + ... (add_split_partials).
 __global__ void __launch_bounds__(256)
 tn_reduce(float* __restrict__ y, const float* __restrict__ partials, size_t quads, int splits,
           int accumulate) {
-    const f32x4* p = reinterpret_cast<const f32x4*>(partials);
-    f32x4* out = reinterpret_cast<f32x4*>(y);
-    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < quads;
-         i += size_t(gridDim.x) * blockDim.x) {
-        f32x4 sum = p[i];
-        for (int s = 1; s < splits; ++s) sum += p[size_t(s) * quads + i];
-        if (accumulate) sum = out[i] + sum;
-        out[i] = sum;
-    }
+    add_split_partials(y, partials, quads, splits, accumulate,
+                       size_t(blockIdx.x) * blockDim.x + threadIdx.x,
+                       size_t(gridDim.x) * blockDim.x);
 }
 
 struct Config {
@@ -870,8 +865,9 @@ hipError_t launch_gemm_nn(void* y, const void* x, const void* w, const void* aux
     }
 }
 
-hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_t n, size_t k,
-                          bool accumulate, void* workspace, hipStream_t stream) {
+hipError_t launch_gemm_tn_split(void* y, const void* x, const void* w, size_t m, size_t n,
+                                size_t k, bool accumulate, void* workspace, int* splits_used,
+                                hipStream_t stream) {
     int splits = 1, len = 0;
     if (hipError_t e = gemm_tn_splits(m, n, k, &splits, &len); e != hipSuccess) return e;
     Operands op = make_ops(y, x, w, m, n, k);
@@ -886,12 +882,28 @@ hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_
     } else {
         err = run<Layout::kTN, Store::kTn>(op, size_t(splits), len, stream);
     }
-    if (err != hipSuccess || splits == 1) return err;
+    *splits_used = splits;
+    return err;
+}
+
+hipError_t launch_tn_reduce(void* y, const void* partials, size_t m, size_t n, int splits,
+                            bool accumulate, hipStream_t stream) {
     const size_t quads = m * n / 4;
     const unsigned blocks = unsigned(std::clamp<size_t>((quads + 255) / 256, 1, 8192));
     hipLaunchKernelGGL(tn_reduce, dim3(blocks), dim3(256), 0, stream, static_cast<float*>(y),
-                       op.partials, quads, splits, op.accumulate);
+                       static_cast<const float*>(partials), quads, splits, accumulate ? 1 : 0);
     return hipGetLastError();
+}
+
+hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_t n, size_t k,
+                          bool accumulate, void* workspace, hipStream_t stream) {
+    int splits = 1;
+    if (hipError_t e = launch_gemm_tn_split(y, x, w, m, n, k, accumulate, workspace, &splits,
+                                            stream);
+        e != hipSuccess || splits == 1) {
+        return e;
+    }
+    return launch_tn_reduce(y, workspace, m, n, splits, accumulate, stream);
 }
 
 hipError_t launch_gemm_nt_batched(void* y, const void* x, const void* w, size_t batches,

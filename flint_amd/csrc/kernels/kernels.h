@@ -58,6 +58,13 @@ hipError_t gemm_tn_splits(size_t m, size_t n, size_t k, int* splits, int* split_
 hipError_t gemm_tn_workspace(size_t m, size_t n, size_t k, size_t* bytes);
 hipError_t launch_gemm_tn(void* y, const void* x, const void* w, size_t m, size_t n, size_t k,
                           bool accumulate, void* workspace, hipStream_t stream);
+// launch_gemm_tn's two halves: the product, then (when *splits_used > 1, the
+// partials being in workspace and y untouched) the sum of the partials.
+hipError_t launch_gemm_tn_split(void* y, const void* x, const void* w, size_t m, size_t n,
+                                size_t k, bool accumulate, void* workspace, int* splits_used,
+                                hipStream_t stream);
+hipError_t launch_tn_reduce(void* y, const void* partials, size_t m, size_t n, int splits,
+                            bool accumulate, hipStream_t stream);
 // The batched GEMMs. causal (attention inside the GPT-2 model only): x (NN,
 // TN) is zero above its diagonal per slice, or (NT) only y's entries at or
 // below the diagonal are wanted; the pipeline then skips the rest, which
@@ -150,6 +157,17 @@ hipError_t launch_bias_gradient_noalloc(void* dbias, const void* dy, size_t rows
 // Merges per-chunk (sum, error) partials left in workspace into out (cols FP32).
 hipError_t launch_bias_gradient_finish(void* out, const void* workspace, size_t rows,
                                        size_t cols, bool accumulate, hipStream_t stream);
+// launch_bias_gradient's first pass alone: the chunk partials into workspace.
+hipError_t launch_bias_partials(void* workspace, const void* dy, size_t rows, size_t cols,
+                                hipStream_t stream);
+// One linear layer's gradients finished in one launch (the GPT-2 model's
+// backward): dw's k-split partials summed as launch_tn_reduce sums them (none
+// when splits == 1) and db's chunk partials merged as
+// launch_bias_gradient_finish merges them; the same bits as the two launches.
+hipError_t launch_linear_grads_finish(void* dw, const void* dw_partials, size_t m, size_t n,
+                                      int splits, bool accumulate_w, void* db,
+                                      const void* db_workspace, size_t rows, size_t cols,
+                                      bool accumulate_b, hipStream_t stream);
 // zero_span 0 writes every chunk of a row (the ABI functions); Z > 0 (a
 // multiple of 8) writes the masked zeros only up to the end of the Z-column
 // block holding the diagonal, for consumers that read no further (the model's

@@ -26,6 +26,7 @@
 #include "common/common.h"
 #include "kernels/kernels.h"
 #include "kernels/reduce_common.h"
+#include "kernels/split_sum.h"
 
 #pragma clang fp contract(off)
 
@@ -272,6 +273,24 @@ column_finish(float* __restrict__ out, const float* __restrict__ partial, size_t
     const int quad = blockIdx.x * 8 + (threadIdx.x >> 5);
     if (quad >= cols / 4) return;   // whole half-waves leave together
     finish_quad(out, partial, chunks, cols, accumulate, quad, threadIdx.x & 31);
+}
+
+// One linear layer's gradients in one launch: workgroups [0, reduce_blocks)
+// sum the weight gradient's k-split partials (tn_reduce's loop), the rest
+// merge the bias gradient's chunk partials (column_finish's).
+__global__ void __launch_bounds__(256)
+linear_grads_finish(float* __restrict__ dw, const float* __restrict__ dw_partials, size_t quads,
+                    int splits, int accumulate_w, unsigned reduce_blocks, float* __restrict__ db,
+                    const float* __restrict__ db_partial, size_t chunks, int cols,
+                    int accumulate_b) {
+    if (blockIdx.x < reduce_blocks) {
+        add_split_partials(dw, dw_partials, quads, splits, accumulate_w,
+                           size_t(blockIdx.x) * 256 + threadIdx.x, size_t(reduce_blocks) * 256);
+        return;
+    }
+    const int quad = int(blockIdx.x - reduce_blocks) * 8 + (threadIdx.x >> 5);
+    if (quad >= cols / 4) return;   // whole half-waves leave together
+    finish_quad(db, db_partial, chunks, cols, accumulate_b, quad, threadIdx.x & 31);
 }
 
 // LayerNorm's dbeta and dgamma partials in one pass over dy and x: per
@@ -852,6 +871,28 @@ hipError_t launch_bias_gradient_finish(void* out, const void* workspace, size_t 
     hipLaunchKernelGGL(column_finish, dim3(blocks), dim3(256), 0, stream,
                        static_cast<float*>(out), static_cast<const float*>(workspace), chunks,
                        int(cols), accumulate ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_bias_partials(void* workspace, const void* dy, size_t rows, size_t cols,
+                                hipStream_t stream) {
+    return launch_partials(static_cast<float*>(workspace), dy, rows, cols, stream);
+}
+
+hipError_t launch_linear_grads_finish(void* dw, const void* dw_partials, size_t m, size_t n,
+                                      int splits, bool accumulate_w, void* db,
+                                      const void* db_workspace, size_t rows, size_t cols,
+                                      bool accumulate_b, hipStream_t stream) {
+    const size_t quads = m * n / 4;
+    const unsigned reduce_blocks =
+        splits > 1 ? unsigned(std::clamp<size_t>((quads + 255) / 256, 1, 8192)) : 0u;
+    const size_t chunks = (rows + kChunkRows - 1) / kChunkRows;
+    const unsigned finish_blocks = unsigned((cols / 4 + 7) / 8);
+    hipLaunchKernelGGL(linear_grads_finish, dim3(reduce_blocks + finish_blocks), dim3(256), 0,
+                       stream, static_cast<float*>(dw), static_cast<const float*>(dw_partials),
+                       quads, splits, accumulate_w ? 1 : 0, reduce_blocks,
+                       static_cast<float*>(db), static_cast<const float*>(db_workspace), chunks,
+                       int(cols), accumulate_b ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -304,6 +304,42 @@ def test_fused_column_sums_change_no_bits(flint, cuda, monkeypatch, cfg, sequenc
     assert plain[4] == fused[4]
 
 
+@pytest.mark.parametrize("cfg,sequences,length", [(TINY, 8, 64), (ODD, 2, 48), (WIDE, 2, 520)],
+                         ids=["tiny-8x64", "odd-2x48", "wide-2x520"])
+def test_fused_linear_grads_change_no_bits(flint, cuda, monkeypatch, cfg, sequences, length):
+    """The model finishes each linear layer's weight and bias gradients in one
+    launch (FLINT_FUSED_GRADS unset); flint_gemm_tn and flint_bias_gradient
+    called one after the other (=0) must give the same bits, after a fresh
+    backward and after a second, accumulating one."""
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=15, trained=True)
+    idx, tgt = _tokens(cfg, sequences, length, 16)
+
+    def grads_twice():
+        with _make(flint, cfg, sequences, length) as model:
+            _load(model, params)
+            tok, trg = _dev16(idx), _dev16(tgt)
+            model.forward(tok, trg, 0.5)
+            model.backward(tok)
+            fresh = {n: model.read(a, (r, c), torch.float32).cpu()
+                     for n, a, r, c in model.gradients()}
+            model.backward(tok, accumulate=True)
+            twice = {n: model.read(a, (r, c), torch.float32).cpu()
+                     for n, a, r, c in model.gradients()}
+            torch.cuda.synchronize()
+        return fresh, twice
+
+    monkeypatch.setenv("FLINT_FUSED_GRADS", "0")
+    plain = grads_twice()
+    monkeypatch.delenv("FLINT_FUSED_GRADS")
+    fused = grads_twice()
+    for a, b in zip(plain, fused):
+        assert a.keys() == b.keys()
+        for n in a:
+            assert torch.equal(a[n].view(torch.int32), b[n].view(torch.int32)), n
+
+
 def test_backward_accumulate_adds_one_pass(flint, cuda):
     """accumulate: every gradient gets this pass's added with one FP32 add, wte
     with two (old + output layer's part) + the embedding's part, so only wte may
