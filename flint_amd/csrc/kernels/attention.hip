@@ -49,6 +49,9 @@ constexpr int kTile = 64 * kHd;          // halves in a 64-row tile (8 KB)
 constexpr int kAttnThreads = 256;        // 4 waves
 constexpr float kLn2 = 0.69314718055994531f;
 constexpr float kLog2e = 1.4426950408889634f;
+// How far (log2 units) a query's scores may rise above the forward's running
+// max before O and l are rescaled: P = 2^(c s - m) <= 2^8 until then.
+constexpr float kRescale = 8.0f;
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
@@ -173,6 +176,7 @@ __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
 
 // ---------------------------------------------------------------- forward
 
+template <bool NEG>
 __global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
 attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16* q,
              const _Float16* k, const _Float16* v, int batches, int length, float c, int heads,
@@ -226,26 +230,50 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
             for (int hb = 0; hb < 2; ++hb)
                 s[hb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag_rows(kt, fo, hb, kk), qf[kk],
                                                                s[hb], 0, 0, 0);
-        // Scaled scores; keys above the query masked in the diagonal block
-        // only (a uniform branch: the other blocks skip the compares).
+        // The block's largest scaled score c s. The diagonal block scales
+        // first and masks keys above the query (a uniform branch: the other
+        // blocks skip the compares); the others take c max(s) (c min(s) for
+        // c < 0: the max of -s, the negation a free source modifier), the
+        // same value since rounding is monotonic, and scale inside the
+        // exponent's FMA below.
         float mx = -INFINITY;
-        auto scale_scores = [&](auto masked) {
+        float ce = c;   // what the exponent multiplies s by
+        auto max_scores = [&](auto masked) {
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    float t = s[hb][r] * c;
-                    if constexpr (masked)
+                    if constexpr (masked) {
+                        float t = s[hb][r] * c;
                         if (kbase + 32 * hb + 8 * (r >> 2) + 4 * h + (r & 3) > qi) t = -INFINITY;
-                    s[hb][r] = t;
-                    mx = fmaxf(mx, t);
+                        s[hb][r] = t;
+                        mx = fmaxf(mx, t);
+                    } else {
+                        mx = fmaxf(mx, NEG ? -s[hb][r] : s[hb][r]);
+                    }
                 }
         };
-        if (kbase + 63 > q0) scale_scores(std::true_type{});
-        else scale_scores(std::false_type{});
+        if (kbase + 63 > q0) {
+            max_scores(std::true_type{});
+            ce = 1.0f;
+        } else {
+            max_scores(std::false_type{});
+            mx *= NEG ? -c : c;
+        }
         mx = fmaxf(mx, xor32(mx));
-        const float m_new = fmaxf(m, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        // The running max m moves only when some lane's block max passes it
+        // by more than kRescale (log2 units). Until then P = 2^(c s - m)
+        // stays below 2^kRescale, well inside FP16, and O and l keep their
+        // scale (the final O / l and lse = m + log2 l are the same quotient
+        // and sum); the rescale of O and l is skipped.
+        const float m_cand = fmaxf(m, mx);
+        if (__any(m_cand > m + kRescale)) {
+            const float alpha = __builtin_amdgcn_exp2f(m - m_cand);
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < 2; ++db) oacc[db] *= alpha;
+            m = m_cand;
+        }
         // P goes to FP16 as it is formed: 16-key slice cs is pf[cs].
         float sum = 0.0f;
         f16x8 pf[4];
@@ -253,15 +281,12 @@ attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16
         for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = __builtin_amdgcn_exp2f(s[hb][r] - m_new);
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hb][r], ce, -m));
                 pf[2 * hb + (r >> 3)][r & 7] = _Float16(p);
                 sum += p;
             }
         sum += xor32(sum);
-        l = l * alpha + sum;
-        m = m_new;
-#pragma unroll
-        for (int db = 0; db < 2; ++db) oacc[db] *= alpha;
+        l += sum;
         // O^T += V^T P^T, two 16-key slices at a time.
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
@@ -589,7 +614,8 @@ hipError_t launch_attention_forward(void* out, void* lse, const void* q, const v
                                     hipStream_t stream, AttnLayout layout) {
     if (!layout_fits(layout, batches, length)) return hipErrorInvalidValue;
     const unsigned blocks = unsigned(batches * ((length + 127) / 128));
-    hipLaunchKernelGGL(attn_forward, dim3(blocks), dim3(kAttnThreads), 0, stream,
+    auto* const kernel = scale < 0.0f ? attn_forward<true> : attn_forward<false>;
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kAttnThreads), 0, stream,
                        static_cast<_Float16*>(out), static_cast<float*>(lse),
                        static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
                        static_cast<const _Float16*>(v), int(batches), int(length), scale * kLog2e,

@@ -73,6 +73,20 @@ def test_matches_float64(flint, cuda, batches, length):
         assert err <= tol, (name, err)
 
 
+@pytest.mark.parametrize("batches,length,scale", [(3, 200, -0.125), (2, 100, -1.0), (2, 64, 0.0)])
+def test_any_finite_scale(flint, cuda, batches, length, scale):
+    """The forward takes the block max of c s as c max(s) (c min(s) for a
+    negative scale): negative and zero scales against float64."""
+    q, k, v, dout = inputs(batches, length, 70 + length)
+    got = run(flint, cuda, q, k, v, dout, scale)
+    ref = reference(q, k, v, dout, scale)
+    for name, g, r in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+        assert bool(torch.isfinite(g).all()), name
+        err = rel_err(g, r)
+        print(f"{batches}x{length} scale {scale} {name}: {err:.2e}")
+        assert err <= (1e-3 if name == "lse" else TOL), (name, err)
+
+
 def test_gpt2_shape_sampled(flint, cuda):
     """96 x 1024 (GPT-2 124M: 8 sequences x 12 heads), the first and last 4
     batches checked against float64."""
