@@ -714,6 +714,7 @@ gemm_pipe(Operands op, TileArgs ta) {
                                        rs, chunk_at(j, h, q, 2, &r, &cc), 0, 0));
                     }
                 }
+                f16x4 ykeep[ST == Store::kBiasGelu ? FN : 1][4];
 #pragma unroll
                 for (int pass = 0; pass < E::kPasses; ++pass) {
                     // GELU: pass 0 writes pre = RN16(s), pass 1 y = RN16(gelu(s)).
@@ -726,17 +727,25 @@ gemm_pipe(Operands op, TileArgs ta) {
                         for (int ii = 0; ii < FN; ++ii) {
 #pragma unroll
                             for (int g4 = 0; g4 < 4; ++g4) {
+                                const int at = srow * E::kLdw + ii * 32 + g4 * 8 + fc * 4;
+                                if (gelu_pass) {
+                                    // Formed with pre in pass 0.
+                                    *reinterpret_cast<f16x4*>(cst + at) = ykeep[ii][g4];
+                                    continue;
+                                }
                                 f32x4 v = {acc[ii][j][g4 * 4 + 0], acc[ii][j][g4 * 4 + 1],
                                            acc[ii][j][g4 * 4 + 2], acc[ii][j][g4 * 4 + 3]};
                                 if constexpr (kBias) v += bias_of(ii, g4);
                                 if constexpr (ST == Store::kScale) v *= op.scale;
-                                const int at = srow * E::kLdw + ii * 32 + g4 * 8 + fc * 4;
                                 if constexpr (E::kF32) {
                                     *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(cst) + at) = v;
                                 } else {
-                                    if (gelu_pass) {
-#pragma unroll
-                                        for (int e = 0; e < 4; ++e) v[e] = gelu(v[e]);
+                                    if constexpr (ST == Store::kBiasGelu) {
+                                        // y = RN16(gelu(v)) from the same biased sum, kept in
+                                        // registers for pass 1 (the accumulator is read and
+                                        // biased once).
+                                        ykeep[ii][g4] = f16x4{_Float16(gelu(v[0])), _Float16(gelu(v[1])),
+                                                              _Float16(gelu(v[2])), _Float16(gelu(v[3]))};
                                     }
                                     const f16x4 hv = {_Float16(v[0]), _Float16(v[1]),
                                                       _Float16(v[2]), _Float16(v[3])};
