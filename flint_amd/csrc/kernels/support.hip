@@ -236,6 +236,96 @@ sort_scatter(uint16_t* __restrict__ out_tokens, unsigned* __restrict__ out_rows,
     }
 }
 
+// Both 8-bit passes of the stable token sort in one workgroup, in LDS, for up
+// to kBlockSortRows rows: the order sort_count / scan_exclusive /
+// sort_scatter give (stable by token, rows ascending within a token), in one
+// launch instead of six. Wave w owns rows [w p, (w + 1) p), p a multiple of
+// 64; per pass it counts its digits, one scan over (digit, wave) in
+// digit-major order gives each its base, and the wave scatters its rows in
+// order, 64 at a time, ranked among equal digits by ballots.
+constexpr int kBlockSortRows = 8192;
+
+__global__ void __launch_bounds__(1024)
+sort_tokens_block(uint16_t* __restrict__ out_tokens, unsigned* __restrict__ out_rows,
+                  const uint16_t* __restrict__ tokens, int rows) {
+    __shared__ uint16_t key[2][kBlockSortRows];
+    __shared__ unsigned idx[2][kBlockSortRows];
+    __shared__ unsigned cnt[16][kDigits];
+    __shared__ unsigned wsum[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int per_wave = ((rows + 15) / 16 + 63) / 64 * 64;
+    const int lo = wave * per_wave, hi = min(rows, lo + per_wave);
+    for (int i = tid; i < rows; i += 1024) {
+        key[0][i] = tokens[i];
+        idx[0][i] = unsigned(i);
+    }
+    for (int pass = 0; pass < 2; ++pass) {
+        const int src = pass, dst = pass ^ 1, shift = 8 * pass;
+        for (int i = tid; i < 16 * kDigits; i += 1024) cnt[i / kDigits][i % kDigits] = 0;
+        __syncthreads();
+        for (int r = lo + lane; r < hi; r += 64) atomicAdd(&cnt[wave][(key[src][r] >> shift) & 255], 1u);
+        __syncthreads();
+        {
+            // Thread t holds entries 4t .. 4t + 3 of the digit-major order:
+            // digit t / 4, waves 4 (t % 4) .. + 3.
+            const int d = tid >> 2, w0 = (tid & 3) * 4;
+            unsigned c[4], own = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                c[k] = cnt[w0 + k][d];
+                own += c[k];
+            }
+            unsigned v = own;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const unsigned t = __shfl_up(v, o, 64);
+                if (lane >= o) v += t;
+            }
+            if (lane == 63) wsum[wave] = v;
+            __syncthreads();
+            unsigned run = v - own;
+            for (int w = 0; w < wave; ++w) run += wsum[w];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                cnt[w0 + k][d] = run;
+                run += c[k];
+            }
+        }
+        __syncthreads();
+        for (int base = lo; base < lo + per_wave; base += 64) {
+            const int r = base + lane;
+            const bool valid = r < hi;
+            const uint16_t tok = valid ? key[src][r] : 0;
+            const unsigned row_id = valid ? idx[src][r] : 0u;
+            const int digit = (tok >> shift) & 255;
+            unsigned long long match = __ballot(valid);
+#pragma unroll
+            for (int bit = 0; bit < 8; ++bit) {
+                const bool set = (digit >> bit) & 1;
+                const unsigned long long b = __ballot(set);
+                match &= set ? b : ~b;
+            }
+            const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+            const unsigned rank = unsigned(__popcll(match & below));
+            if (valid) {
+                const unsigned pos = cnt[wave][digit] + rank;
+                key[dst][pos] = tok;
+                idx[dst][pos] = row_id;
+            }
+            // The group's last lane advances the digit's base.
+            const bool last = valid && (match >> lane) == 1ull;
+            __builtin_amdgcn_wave_barrier();
+            if (last) cnt[wave][digit] += unsigned(__popcll(match));
+            __builtin_amdgcn_wave_barrier();
+        }
+        __syncthreads();
+    }
+    for (int i = tid; i < rows; i += 1024) {
+        out_tokens[i] = key[0][i];
+        out_rows[i] = idx[0][i];
+    }
+}
+
 // offsets[v] = number of sorted tokens below v, v = 0..vocab (binary search).
 __global__ void __launch_bounds__(256)
 token_offsets(unsigned* __restrict__ offsets, const uint16_t* __restrict__ sorted, size_t rows,
@@ -531,8 +621,12 @@ hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, con
     const auto* tok = static_cast<const uint16_t*>(tokens);
 
     // Two stable passes of 8 bits: low byte into the pass buffers, high byte
-    // into the sorted buffers.
-    for (int pass = 0; pass < 2; ++pass) {
+    // into the sorted buffers; in one workgroup's LDS when the rows fit.
+    if (rows <= size_t(kBlockSortRows)) {
+        hipLaunchKernelGGL(sort_tokens_block, dim3(1), dim3(1024), 0, stream, sorted_tokens,
+                           sorted_rows, tok, int(rows));
+    }
+    for (int pass = 0; pass < (rows <= size_t(kBlockSortRows) ? 0 : 2); ++pass) {
         const int shift = pass * 8;
         const uint16_t* in_t = pass == 0 ? tok : pass_tokens;
         const unsigned* in_r = pass == 0 ? nullptr : pass_rows;

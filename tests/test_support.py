@@ -49,7 +49,7 @@ def test_embedding_forward_matches_pytorch_bitwise(flint, cuda, sequences, lengt
 @pytest.mark.parametrize("sequences,length,vocab,width,kind", [
     (2, 64, 1000, 64, "uniform"), (3, 40, 200, 24, "few"), (1, 2048, 50, 8, "one"),
     (2, 1500, 5000, 16, "zipf"), (4, 256, 65536, 8, "uniform"), (9, 16, 300, 16, "zipf"),
-    (300, 8, 100, 8, "uniform")])
+    (300, 8, 100, 8, "uniform"), (3, 4000, 65536, 8, "uniform"), (5, 1700, 3000, 8, "zipf")])
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_embedding_backward_matches_the_oracle_bitwise(flint, cuda, sequences, length, vocab,
                                                        width, kind, accumulate):
