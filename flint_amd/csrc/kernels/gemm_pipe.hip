@@ -251,7 +251,12 @@ gemm_pipe(Operands op, TileArgs ta) {
     // 128 VGPRs (128 x 192: 96), so that its latency hides under the k-loop.
     constexpr int kResAll = FM * E::kSubs * E::kPerLane;
     constexpr bool kResEarly = ST == Store::kBiasResidual && kResAll <= 32;
-    constexpr int kEarlyLoads = kBiasLoads + (kResEarly ? kResAll : 0);
+    // dGELU's pre: the first staged block's chunks load at tile start, and
+    // each later block's while the block before it is stored, so that no
+    // block waits out a load's full latency.
+    constexpr bool kPreEarly = ST == Store::kDGelu;
+    constexpr int kEarlyLoads =
+        kBiasLoads + (kResEarly ? kResAll : 0) + (kPreEarly ? E::kPerLane : 0);
     // One LDS object for everything: with a second one, the compiler's LDS-DMA
     // alias tracking put a vmcnt(0) in front of every fragment read.
     __shared__ __attribute__((aligned(16)))
@@ -566,6 +571,22 @@ gemm_pipe(Operands op, TileArgs ta) {
                                        rs, chunk_at(j, h, q, 4, &r, &cc), 0, 0));
                     }
         }
+        // Block (j, h)'s pre chunks, 8 FP16 each.
+        auto load_pre = [&](int j, int h, f16x8 (&dst)[E::kPerLane]) {
+            const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<void*>(static_cast<const void*>(
+                    static_cast<const _Float16*>(op.aux) + t.y_off)),
+                0, out_bytes, 0x00020000);
+#pragma unroll
+            for (int q = 0; q < E::kPerLane; ++q) {
+                int r, cc;
+                dst[q] = __builtin_bit_cast(
+                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, chunk_at(j, h, q, 2, &r, &cc),
+                                                                 0, 0));
+            }
+        };
+        f16x8 pre_next[kPreEarly ? E::kPerLane : 1];
+        if constexpr (kPreEarly) load_pre(0, 0, pre_next);
         const int steps = (t.k_end - t.k_begin) / BK;
         for (int s = 0; s < steps; ++s) {
             Issue nxt = cur;
@@ -671,48 +692,53 @@ gemm_pipe(Operands op, TileArgs ta) {
                 return bias[ii][g4];
         };
         const bool accumulate = ST == Store::kTn && !split && op.accumulate;
+        // FP32 values the store pass reads back: the residual (where it was
+        // not loaded at tile start) and the old y of an accumulating TN. Block
+        // (j, h)'s go out while the block before it is stored; the first
+        // block's at the epilogue's start. Every one of them is used within
+        // this epilogue, so the k-loop's wait counts do not see them.
+        constexpr bool kReadsAhead =
+            (ST == Store::kBiasResidual && !kResEarly) || ST == Store::kTn;
+        auto load_rd = [&](int j, int h, f32x4 (&dst)[E::kPerLane]) {
+            const float* src = ST == Store::kTn ? static_cast<const float*>(op.y)
+                                                : static_cast<const float*>(op.aux);
+            const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src + t.y_off),
+                                                              0, out_bytes, 0x00020000);
+#pragma unroll
+            for (int q = 0; q < E::kPerLane; ++q) {
+                int r, cc;
+                if (ST == Store::kTn && !accumulate) {
+                    dst[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                } else {
+                    dst[q] = __builtin_bit_cast(
+                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                   rs, chunk_at(j, h, q, 4, &r, &cc), 0, 0));
+                }
+            }
+        };
+        f32x4 rd_next[kReadsAhead ? E::kPerLane : 1];
+        if constexpr (kReadsAhead) load_rd(0, 0, rd_next);
 #pragma unroll
         for (int j = 0; j < FM; ++j) {
 #pragma unroll
             for (int h = 0; h < E::kSubs; ++h) {
-                // Values the store pass reads back, loaded first so that their
-                // latency overlaps the staging writes: the residual, the old y
-                // of an accumulating TN, dGELU's pre.
                 constexpr bool kReads = ST == Store::kBiasResidual || ST == Store::kTn;
                 f32x4 rd[kReads ? E::kPerLane : 1];
                 if constexpr (kResEarly) {
 #pragma unroll
                     for (int q = 0; q < E::kPerLane; ++q) rd[q] = res_all[j][h][q];
-                } else if constexpr (ST == Store::kBiasResidual || ST == Store::kTn) {
-                    const float* src = ST == Store::kTn ? static_cast<const float*>(op.y)
-                                                        : static_cast<const float*>(op.aux);
-                    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
-                        const_cast<float*>(src + t.y_off), 0, out_bytes, 0x00020000);
+                } else if constexpr (kReadsAhead) {
 #pragma unroll
-                    for (int q = 0; q < E::kPerLane; ++q) {
-                        int r, cc;
-                        if (ST == Store::kTn && !accumulate) {
-                            rd[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                        } else {
-                            rd[q] = __builtin_bit_cast(
-                                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                           rs, chunk_at(j, h, q, 4, &r, &cc), 0, 0));
-                        }
-                    }
+                    for (int q = 0; q < E::kPerLane; ++q) rd[q] = rd_next[q];
+                    const int nb = j * E::kSubs + h + 1;
+                    if (nb < FM * E::kSubs) load_rd(nb / E::kSubs, nb % E::kSubs, rd_next);
                 }
                 f16x8 pre8[ST == Store::kDGelu ? E::kPerLane : 1];
                 if constexpr (ST == Store::kDGelu) {
-                    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
-                        const_cast<void*>(static_cast<const void*>(
-                            static_cast<const _Float16*>(op.aux) + t.y_off)),
-                        0, out_bytes, 0x00020000);
 #pragma unroll
-                    for (int q = 0; q < E::kPerLane; ++q) {
-                        int r, cc;
-                        pre8[q] = __builtin_bit_cast(
-                            f16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                                       rs, chunk_at(j, h, q, 2, &r, &cc), 0, 0));
-                    }
+                    for (int q = 0; q < E::kPerLane; ++q) pre8[q] = pre_next[q];
+                    const int nb = j * E::kSubs + h + 1;
+                    if (nb < FM * E::kSubs) load_pre(nb / E::kSubs, nb % E::kSubs, pre_next);
                 }
                 f16x4 ykeep[ST == Store::kBiasGelu ? FN : 1][4];
 #pragma unroll

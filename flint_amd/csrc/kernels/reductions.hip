@@ -547,6 +547,9 @@ __device__ __forceinline__ int written_chunks(int t, int chunks, int zero_span) 
 
 // One wave per row of length L <= 1024: lane l holds chunks l and l + 64.
 // Row t sees columns 0..t; masked chunks are written as zeros and never read.
+// The zeros go out with the row's values, after its reductions: stored first,
+// under the loads, they made the pass slower (60.5 -> 64.7 us at 96 x 1024,
+// and 74.2 -> 76.5 for the backward pass).
 // A wave takes R consecutive rows and loads all of them before the first
 // reduction, so R times the bytes are in flight; each row's arithmetic is
 // the one-row order.
@@ -805,7 +808,9 @@ softmax_cross_entropy(h8* __restrict__ dlogits, float* __restrict__ row_loss,
         const int c = tid + i * THREADS;
         if (c >= vocab_chunks) continue;
         // An empty asm on the chunk keeps the compiler from carrying pass 2's
-        // FP32 gaps (8 VGPRs a chunk) over to here instead of the FP16 chunk.
+        // FP32 gaps (8 VGPRs a chunk) over to here instead of the FP16 chunk
+        // (holding pass 2's e instead, 154 VGPRs, one workgroup per CU, ran
+        // no faster).
         asm volatile("" : "+v"(raw[i]));
         float e[8];
 #pragma unroll
