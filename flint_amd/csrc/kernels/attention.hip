@@ -35,6 +35,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common/common.h"
@@ -70,6 +71,20 @@ __device__ __forceinline__ void wait_lds() {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_sched_barrier(0);
+}
+
+// The work item (in longest-first order) that workgroup `bid` takes. The
+// kernels' grids are about what the GPU holds at once, so dispatch does little
+// balancing, and workgroups bid, bid + CUs, bid + 2 CUs, ... tend to share a
+// CU. With round > 0 (the CU count) every other run of `round` workgroups
+// takes its items in reverse, so that a CU's workgroups pair long items with
+// short ones.
+__device__ __forceinline__ int work_rank(int bid, int round, int total) {
+    if (round <= 0) return bid;
+    const int r = bid / round, pos = bid - r * round;
+    if ((r & 1) == 0) return bid;
+    const int n = min(round, total - r * round);
+    return r * round + (n - 1 - pos);
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* base, unsigned bytes) {
@@ -180,15 +195,16 @@ template <bool NEG>
 __global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
 attn_forward(_Float16* __restrict__ out, float* __restrict__ lse, const _Float16* q,
              const _Float16* k, const _Float16* v, int batches, int length, float c, int heads,
-             int in_stride, int o_stride) {
+             int in_stride, int o_stride, int round) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[2 * 2 * kTile];   // [buf][K, V]
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int fr = lane & 31, h = lane >> 5;
     const FragOff fo = frag_offsets(lane);
     const int nqb = (length + 127) / 128;
-    const int qb = nqb - 1 - int(blockIdx.x) / batches;      // longest blocks first
-    const int b = int(blockIdx.x) % batches;
+    const int rank = work_rank(int(blockIdx.x), round, int(gridDim.x));
+    const int qb = nqb - 1 - rank / batches;      // longest blocks first
+    const int b = rank % batches;
     const Rows rows{heads, length};
     const size_t in_first = rows.first(b, in_stride);
     const unsigned in_bytes = rows.bytes(in_stride);
@@ -327,15 +343,16 @@ __global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_
 attn_backward_dq(_Float16* __restrict__ dq, float* __restrict__ dsum, const _Float16* q,
                  const _Float16* k, const _Float16* v, const _Float16* o, const _Float16* dout,
                  const float* lse, int batches, int length, float c, float scale, int heads,
-                 int in_stride, int o_stride, int g_stride) {
+                 int in_stride, int o_stride, int g_stride, int round) {
     __shared__ __attribute__((aligned(16))) _Float16 lds[2 * 2 * kTile];   // [buf][K, V]
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int fr = lane & 31, h = lane >> 5;
     const FragOff fo = frag_offsets(lane);
     const int nqb = (length + 127) / 128;
-    const int qb = nqb - 1 - int(blockIdx.x) / batches;
-    const int b = int(blockIdx.x) % batches;
+    const int rank = work_rank(int(blockIdx.x), round, int(gridDim.x));
+    const int qb = nqb - 1 - rank / batches;
+    const int b = rank % batches;
     const Rows rows{heads, length};
     const size_t in_first = rows.first(b, in_stride), o_first = rows.first(b, o_stride);
     const unsigned in_bytes = rows.bytes(in_stride), o_bytes = rows.bytes(o_stride);
@@ -454,7 +471,7 @@ __global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_
 attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _Float16* q,
                    const _Float16* k, const _Float16* v, const _Float16* dout, const float* lse,
                    const float* dsum, int batches, int length, float c, float scale, int heads,
-                   int in_stride, int o_stride, int g_stride) {
+                   int in_stride, int o_stride, int g_stride, int round) {
     // [buf][Q tile, dO tile] then [buf][lse2 64, D 64].
     __shared__ __attribute__((aligned(16))) _Float16 lds[2 * 2 * kTile];
     __shared__ __attribute__((aligned(16))) float rowstat[2][2][64];
@@ -463,8 +480,9 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
     const int fr = lane & 31, h = lane >> 5;
     const FragOff fo = frag_offsets(lane);
     const int nkb = (length + 127) / 128;
-    const int kb = int(blockIdx.x) / batches;                // earliest keys have the most queries
-    const int b = int(blockIdx.x) % batches;
+    const int rank = work_rank(int(blockIdx.x), round, int(gridDim.x));
+    const int kb = rank / batches;                // earliest keys have the most queries
+    const int b = rank % batches;
     const Rows rows{heads, length};
     const size_t in_first = rows.first(b, in_stride);
     const unsigned in_bytes = rows.bytes(in_stride);
@@ -600,6 +618,16 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
 
 // Heads divide the batches, every stride holds a 64-half row, and buffer
 // offsets (32-bit bytes) reach every row.
+// work_rank's run: the CU count; FLINT_ATTN_ORDER=0 keeps plain
+// longest-first order (A/B runs).
+int order_round() {
+    const char* e = std::getenv("FLINT_ATTN_ORDER");
+    if (e != nullptr && e[0] == '0' && e[1] == '\0') return 0;
+    int cus = 0;
+    if (device_cus(&cus) != hipSuccess || cus <= 0) return 0;
+    return cus;
+}
+
 bool layout_fits(const AttnLayout& l, size_t batches, size_t length) {
     if (l.heads < 1 || batches % size_t(l.heads) != 0 || length == 0) return false;
     for (int s : {l.qkv_stride, l.o_stride, l.grad_stride})
@@ -619,7 +647,7 @@ hipError_t launch_attention_forward(void* out, void* lse, const void* q, const v
                        static_cast<_Float16*>(out), static_cast<float*>(lse),
                        static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
                        static_cast<const _Float16*>(v), int(batches), int(length), scale * kLog2e,
-                       layout.heads, layout.qkv_stride, layout.o_stride);
+                       layout.heads, layout.qkv_stride, layout.o_stride, order_round());
     return hipGetLastError();
 }
 
@@ -635,7 +663,7 @@ hipError_t launch_attention_backward(void* dq, void* dk, void* dv, const void* d
                        static_cast<const _Float16*>(v), static_cast<const _Float16*>(o),
                        static_cast<const _Float16*>(dout), static_cast<const float*>(lse),
                        int(batches), int(length), scale * kLog2e, scale, layout.heads,
-                       layout.qkv_stride, layout.o_stride, layout.grad_stride);
+                       layout.qkv_stride, layout.o_stride, layout.grad_stride, order_round());
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     hipLaunchKernelGGL(attn_backward_dkdv, dim3(blocks), dim3(kAttnThreads), 0, stream,
                        static_cast<_Float16*>(dk), static_cast<_Float16*>(dv),
@@ -643,7 +671,7 @@ hipError_t launch_attention_backward(void* dq, void* dk, void* dv, const void* d
                        static_cast<const _Float16*>(v), static_cast<const _Float16*>(dout),
                        static_cast<const float*>(lse), static_cast<const float*>(dsum),
                        int(batches), int(length), scale * kLog2e, scale, layout.heads,
-                       layout.qkv_stride, layout.o_stride, layout.grad_stride);
+                       layout.qkv_stride, layout.o_stride, layout.grad_stride, order_round());
     return hipGetLastError();
 }
 
