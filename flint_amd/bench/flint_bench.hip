@@ -96,6 +96,10 @@ void roc_check(rocblas_status s, const char* what) {
 constexpr double kMiB = 1024.0 * 1024.0;
 constexpr unsigned long long kInfinityCache = 256ull << 20;   // MI355X's last-level cache
 constexpr double kRatedBandwidthGBs = 8000.0;                 // MI355X HBM3E, published
+// HBM3E transfers per reported memory clock: the device reports 2,000 MHz on
+// an 8,192-bit bus, and 4 x 2,000 MHz x 1,024 B = 8.19 TB/s is the part's
+// published 8 TB/s (the reference's GDDR formula takes 2).
+constexpr double kTransfersPerMemClock = 4.0;
 constexpr double kPeakFlopPerCuPerClock = 4096.0;             // dense FP16 MFMA, gfx950
 
 struct DeviceInfo {
@@ -248,7 +252,7 @@ struct Side {
     long long launches_per_sample = 0;
     double min_sample_ms = 0, ms_per_launch = 0, gbs = 0, rated_fraction = 0, tflops = 0,
            rated_compute_fraction = 0;
-    std::optional<double> clock_adjusted_compute_fraction;
+    std::optional<double> clock_adjusted_fraction, clock_adjusted_compute_fraction;
     std::optional<WindowStats> stats;   // the valid samples' windows, merged by time
 };
 
@@ -336,6 +340,11 @@ Side summarize(long long launches, const std::vector<const Sample*>& samples, co
     if (spec.bytes_moved > 0) {
         side.gbs = spec.bytes_moved / (side.ms_per_launch * 1e-3) / 1e9;
         side.rated_fraction = side.gbs / kRatedBandwidthGBs;
+        // Against the bandwidth at the memory clock the monitor read (ref
+        // bench/harness.cpp:80-85).
+        if (side.stats && side.stats->mem_mhz > 0 && d.bus_width > 0)
+            side.clock_adjusted_fraction =
+                side.gbs / (kTransfersPerMemClock * side.stats->mem_mhz * 1e6 * (d.bus_width / 8) / 1e9);
     }
     if (spec.flops > 0) {
         side.tflops = spec.flops / (side.ms_per_launch * 1e-3) / 1e12;
@@ -917,7 +926,8 @@ void write_side(Json& j, const char* k, const Side& s) {
     j.num("ms_per_launch", s.ms_per_launch);
     j.num("gbs", s.gbs);
     j.num("rated_fraction", s.rated_fraction);
-    j.null("clock_adjusted_fraction");
+    if (s.clock_adjusted_fraction) j.num("clock_adjusted_fraction", *s.clock_adjusted_fraction);
+    else j.null("clock_adjusted_fraction");
     j.num("tflops", s.tflops);
     j.num("rated_compute_fraction", s.rated_compute_fraction);
     if (s.clock_adjusted_compute_fraction) j.num("clock_adjusted_compute_fraction", *s.clock_adjusted_compute_fraction);

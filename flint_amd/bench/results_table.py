@@ -82,6 +82,8 @@ def table(log):
     head = ["Case", "Flint ms", f"Flint {unit}", peak]
     if monitored and compute:
         head += ["SCLK MHz", "of peak at SCLK", "power-capped"]
+    elif monitored:
+        head += ["MCLK MHz", "of HBM peak at MCLK"]
     if has_baseline:
         head += ["Baseline", f"Baseline {unit}", "Ratio (median)", "Ratio range"]
     if has_algo:
@@ -97,6 +99,10 @@ def table(log):
             adj = c["flint"].get("clock_adjusted_compute_fraction")
             row += [f"{st['sm_mhz']:.0f}" if st else "-", pct(adj) if adj else "-",
                     pct(st["power_cap_share"]) if st else "-"]
+        elif monitored:
+            st = c["flint"].get("stats")
+            adj = c["flint"].get("clock_adjusted_fraction")
+            row += [f"{st['mem_mhz']:.0f}" if st else "-", pct(adj) if adj else "-"]
         if has_baseline:
             if c["one_sided"]:
                 row += ["-", "-", "-", "-"]

@@ -267,6 +267,14 @@ def test_quick_copy(exe, tmp_path):
             side = case[name]
             assert 0 < side["gbs"] <= 1.1 * device["rated_bandwidth_gbs"]
             assert side["gbs"] == pytest.approx(case["bytes_moved"] / (side["ms_per_launch"] * 1e-3) / 1e9)
+            # Against the bandwidth at the monitored memory clock: HBM3E moves
+            # four transfers per reported clock over the bus.
+            st = side["stats"]
+            if st is not None and st["samples"] > 0 and st["mem_mhz"] > 0:
+                at_clock = 4 * st["mem_mhz"] * 1e6 * device["bus_width_bits"] / 8 / 1e9
+                assert side["clock_adjusted_fraction"] == pytest.approx(side["gbs"] / at_clock)
+            else:
+                assert side["clock_adjusted_fraction"] is None
         stride = (case["size_bytes"] + 255) // 256 * 256
         assert case["rotation_sets"] * 2 * stride > 4 * device["l2_bytes"]
 
@@ -409,6 +417,23 @@ def test_results_table_rows():
     assert cells[12:] == ["10/10", "ok, rel L2 1.0e-06"]
     # Without monitor statistics the clock columns are left out.
     assert "SCLK" not in table(synthetic_log(stats=False))
+
+
+def test_results_table_bandwidth_at_the_memory_clock():
+    from flint_amd.bench.results_table import table
+
+    log = synthetic_log()
+    case = log["cases"][0]
+    case.update(benchmark="copy", label="1 GiB", layout=None, epilogue=None, flops=0)
+    for name in ("flint", "baseline"):
+        case[name] = dict(case[name], gbs=6000.0, rated_fraction=0.75, tflops=0,
+                          clock_adjusted_fraction=6000 / 8192, clock_adjusted_compute_fraction=None)
+    text = table(log)
+    head = [line for line in text.splitlines() if line.startswith("| Case")][0]
+    assert "MCLK MHz" in head and "SCLK" not in head
+    (row,) = [line for line in text.splitlines() if line.startswith("| copy 1 GiB")]
+    cells = [c.strip() for c in row.strip("|").split("|")]
+    assert cells[1:6] == ["0.5000", "6000.0", "75.0%", "2000", "73.2%"]
 
 
 @pytest.mark.parametrize("kwargs, reason", [
