@@ -297,17 +297,21 @@ linear_grads_finish(float* __restrict__ dw, const float* __restrict__ dw_partial
 // 256-row chunk and column, exactly the sums of column_partials<false, 1> and
 // column_partials<true, 1>, in their order, into part0 and part1. The dx
 // kernel launched after it merges them (ColumnFinish).
-__global__ void __launch_bounds__(kPhases * 64)
-column_partials2(float* part0, float* part1, const _Float16* __restrict__ dy,
-                 const float* __restrict__ x, const float* __restrict__ mean,
-                 const float* __restrict__ rstd, size_t rows, int cols, size_t chunks,
-                 size_t blocks) {
+// Units b = first, first + stride, ... < blocks (chunk x 64 columns each) of a
+// kPhases * 64-thread workgroup.
+__device__ __forceinline__ void partials2_units(float* part0, float* part1,
+                                                const _Float16* __restrict__ dy,
+                                                const float* __restrict__ x,
+                                                const float* __restrict__ mean,
+                                                const float* __restrict__ rstd, size_t rows,
+                                                int cols, size_t chunks, size_t blocks,
+                                                size_t first, size_t stride_b) {
     constexpr int kPer = kChunkRows / kPhases;
     __shared__ float sums[2][kPhases - 1][64];
     __shared__ float errs[2][kPhases - 1][64];
     const int lane = threadIdx.x & 63;
     const int ph = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
-    for (size_t b = blockIdx.x; b < blocks; b += gridDim.x) {
+    for (size_t b = first; b < blocks; b += stride_b) {
         const int tile = int(b / chunks);
         const size_t chunk = b - size_t(tile) * chunks;
         const size_t first = chunk * kChunkRows;
@@ -367,6 +371,15 @@ column_partials2(float* part0, float* part1, const _Float16* __restrict__ dy,
     }
 }
 
+__global__ void __launch_bounds__(kPhases * 64)
+column_partials2(float* part0, float* part1, const _Float16* __restrict__ dy,
+                 const float* __restrict__ x, const float* __restrict__ mean,
+                 const float* __restrict__ rstd, size_t rows, int cols, size_t chunks,
+                 size_t blocks) {
+    partials2_units(part0, part1, dy, x, mean, rstd, rows, cols, chunks, blocks, blockIdx.x,
+                    gridDim.x);
+}
+
 hipError_t launch_partials(float* partial, const void* dy, size_t rows, size_t cols,
                            hipStream_t stream) {
     const size_t chunks = (rows + kChunkRows - 1) / kChunkRows;
@@ -419,16 +432,16 @@ __device__ __forceinline__ void finish_columns(const ColumnFinish& f, int cols) 
 // with plain FP32 adds, and a 32-lane butterfly totals them. The second pass
 // reuses the registers. With dx_half, RN16 of every dx value written goes
 // there too (the model's FP16 copy of the residual gradient).
-template <int PPL>
-__global__ void __launch_bounds__(256)
-layernorm_backward_dx(float* __restrict__ dx, const _Float16* __restrict__ dy,
-                      const float* __restrict__ x, const float* __restrict__ mean,
-                      const float* __restrict__ rstd, const float* __restrict__ gamma,
-                      size_t rows, int cols, int accumulate, _Float16* __restrict__ dx_half,
-                      ColumnFinish finish) {
-    finish_columns(finish, cols);
-    for (size_t row = size_t(blockIdx.x) * 8 + (threadIdx.x >> 5); row < rows;
-         row += size_t(gridDim.x) * 8) {
+// Rows of workgroup `block` of `blocks` (RPB rows, one per half-wave, each).
+template <int PPL, int RPB>
+__device__ __forceinline__ void dx_rows(float* __restrict__ dx, const _Float16* __restrict__ dy,
+                                        const float* __restrict__ x,
+                                        const float* __restrict__ mean,
+                                        const float* __restrict__ rstd,
+                                        const float* __restrict__ gamma, size_t rows, int cols,
+                                        int accumulate, _Float16* __restrict__ dx_half,
+                                        size_t block, size_t blocks) {
+    for (size_t row = block * RPB + (threadIdx.x >> 5); row < rows; row += blocks * RPB) {
     const int lane = threadIdx.x & 31;
     const int pieces = cols / 8;
     const float mu = mean[row];
@@ -486,6 +499,44 @@ layernorm_backward_dx(float* __restrict__ dx, const _Float16* __restrict__ dy,
         }
     }
     }
+}
+
+template <int PPL>
+__global__ void __launch_bounds__(256)
+layernorm_backward_dx(float* __restrict__ dx, const _Float16* __restrict__ dy,
+                      const float* __restrict__ x, const float* __restrict__ mean,
+                      const float* __restrict__ rstd, const float* __restrict__ gamma,
+                      size_t rows, int cols, int accumulate, _Float16* __restrict__ dx_half,
+                      ColumnFinish finish) {
+    finish_columns(finish, cols);
+    dx_rows<PPL, 8>(dx, dy, x, mean, rstd, gamma, rows, cols, accumulate, dx_half, blockIdx.x,
+                    gridDim.x);
+}
+
+// LayerNorm backward's two passes in one launch: workgroups [0, units) take
+// the dbeta / dgamma chunk partials (column_partials2's), the rest dx one row
+// per half-wave (layernorm_backward_dx's), so that the latency-bound partials
+// overlap the bandwidth-bound rows; ln_params_finish merges the partials
+// after it. The same arithmetic in the same order as the two-launch path.
+template <int PPL>
+__global__ void __launch_bounds__(kPhases * 64)
+layernorm_backward_fused(float* part0, float* part1, float* __restrict__ dx,
+                         const _Float16* __restrict__ dy, const float* __restrict__ x,
+                         const float* __restrict__ mean, const float* __restrict__ rstd,
+                         const float* __restrict__ gamma, size_t rows, int cols, size_t chunks,
+                         size_t items, unsigned units, int accumulate,
+                         _Float16* __restrict__ dx_half) {
+    if (blockIdx.x < units) {
+        partials2_units(part0, part1, dy, x, mean, rstd, rows, cols, chunks, items, blockIdx.x,
+                        units);
+        return;
+    }
+    dx_rows<PPL, kPhases * 2>(dx, dy, x, mean, rstd, gamma, rows, cols, accumulate, dx_half,
+                              blockIdx.x - units, gridDim.x - units);
+}
+
+__global__ void __launch_bounds__(256) ln_params_finish(ColumnFinish finish, int cols) {
+    finish_columns(finish, cols);
 }
 
 // Any cols (multiple of 8): the same order, two passes over memory.
@@ -925,20 +976,42 @@ hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const 
     const auto* mf = static_cast<const float*>(mean);
     const auto* rf = static_cast<const float*>(rstd);
     const int c = int(cols);
-    // dbeta and dgamma partials, one pass over dy and x.
     const size_t items = chunks * ((cols + 63) / 64);
-    hipLaunchKernelGGL(column_partials2, dim3(unsigned(std::min<size_t>(items, kMaxBlocks))),
-                       dim3(kPhases * 64), 0, stream, part0, part1, dyh, xf, mf, rf, rows, c,
-                       chunks, items);
-    // dx, whose first half-waves also merge the partials.
     const ColumnFinish finish{static_cast<float*>(dbeta), static_cast<float*>(dgamma), part0,
                               part1, chunks, accumulate_params ? 1 : 0};
-    const unsigned blocks = unsigned(std::min<size_t>((rows + 7) / 8, kMaxBlocks));
     auto* dxf = static_cast<float*>(dx);
     const auto* gf = static_cast<const float*>(gamma);
     const int acc = accumulate_dx ? 1 : 0;
     auto* dxh = static_cast<_Float16*>(dx_half);
     const size_t pieces = cols / 8;
+    // One launch for the partials and dx, then the merge (FLINT_LN_FUSED=0:
+    // the partials, then dx with the merge; the same bits).
+    const char* fe = std::getenv("FLINT_LN_FUSED");
+    const bool fused = pieces <= 256 && !(fe != nullptr && fe[0] == '0' && fe[1] == '\0');
+    if (fused) {
+        const size_t units = std::min<size_t>(items, 1u << 20);
+        const size_t row_blocks = std::min<size_t>((rows + 15) / 16, kMaxBlocks);
+        const dim3 grid(unsigned(units + row_blocks));
+#define FLINT_LNF(PPL)                                                                         \
+    hipLaunchKernelGGL(layernorm_backward_fused<PPL>, grid, dim3(kPhases * 64), 0, stream,     \
+                       part0, part1, dxf, dyh, xf, mf, rf, gf, rows, c, chunks, items,         \
+                       unsigned(units), acc, dxh)
+        if (pieces <= 32) FLINT_LNF(1);
+        else if (pieces <= 64) FLINT_LNF(2);
+        else if (pieces <= 96) FLINT_LNF(3);
+        else if (pieces <= 128) FLINT_LNF(4);
+        else FLINT_LNF(8);
+#undef FLINT_LNF
+        const unsigned fin = unsigned(std::min<size_t>((2 * (cols / 4) + 7) / 8, kMaxBlocks));
+        hipLaunchKernelGGL(ln_params_finish, dim3(fin), dim3(256), 0, stream, finish, c);
+        return hipGetLastError();
+    }
+    // dbeta and dgamma partials, one pass over dy and x.
+    hipLaunchKernelGGL(column_partials2, dim3(unsigned(std::min<size_t>(items, kMaxBlocks))),
+                       dim3(kPhases * 64), 0, stream, part0, part1, dyh, xf, mf, rf, rows, c,
+                       chunks, items);
+    // dx, whose first half-waves also merge the partials.
+    const unsigned blocks = unsigned(std::min<size_t>((rows + 7) / 8, kMaxBlocks));
 #define FLINT_DX(PPL)                                                                        \
     hipLaunchKernelGGL(layernorm_backward_dx<PPL>, dim3(blocks), dim3(256), 0, stream, dxf, dyh, \
                        xf, mf, rf, gf, rows, c, acc, dxh, finish)

@@ -85,11 +85,16 @@ def test_bias_gradient_past_65535_chunks(flint, cuda):
 
 
 # 1 to 4 pieces of 8 columns per lane of the dx kernel and past them (1,032 and
-# 4,096 columns); a last chunk whose phases 1..7 hold no row (257 rows).
+# 4,096 columns); a last chunk whose phases 1..7 hold no row (257 rows). Both
+# launch plans: partials and dx in one launch then the merge (default), and
+# partials then dx with the merge (FLINT_LN_FUSED=0); 4,096 columns take the
+# second either way.
 @pytest.mark.parametrize("rows,cols", [(3, 8), (300, 24), (257, 512), (8192, 768), (1000, 1024),
                                        (9, 1032), (100, 4096)])
 @pytest.mark.parametrize("acc", [False, True])
-def test_layernorm_backward(flint, cuda, rows, cols, acc):
+@pytest.mark.parametrize("fused", ["1", "0"])
+def test_layernorm_backward(flint, cuda, monkeypatch, rows, cols, acc, fused):
+    monkeypatch.setenv("FLINT_LN_FUSED", fused)
     x = normal((rows, cols), 8)
     gamma = 1 + normal((cols,), 9, 0.1)
     beta = normal((cols,), 10, 0.1)
