@@ -120,6 +120,12 @@ struct flint_gpt2 {
     size_t work_bytes = 0;
     void* tn_work = nullptr;
     size_t tn_work_bytes = 0;
+    // LayerNorm backward's chunk partials, apart from `work`: their merge is
+    // deferred to the next linear layer's gradient finish (after that
+    // layer's bias partials have used `work`); `pending` describes it.
+    void* ln_work = nullptr;
+    size_t ln_work_bytes = 0;
+    mutable flint::ParamsMerge pending{};
     std::vector<Request> requests;
     std::vector<void*> blocks;   // hipMalloc'd allocations
     std::vector<float> host_loss;
@@ -216,6 +222,7 @@ flint_status size_workspaces(flint_gpt2& m) {
     }
     FLINT_TRY(flint_layernorm_backward_workspace(m.rows, w, &b));
     need = std::max(need, b);
+    m.ln_work_bytes = b;
     FLINT_TRY(flint_embedding_backward_workspace(c.sequences, c.length, c.padded_vocab, w, &b));
     m.work_bytes = std::max(need, b);
     const size_t shapes[][2] = {{c.padded_vocab, w}, {3 * w, w}, {w, w}, {4 * w, w}, {w, 4 * w}};
@@ -328,6 +335,7 @@ flint_status plan(flint_gpt2& m) {
         req(&m.dpre, rows * 4 * w * 2);
         req(&m.work, m.work_bytes);
         req(&m.tn_work, m.tn_work_bytes);
+        req(&m.ln_work, m.ln_work_bytes);
     } else {
         Saved& s = m.layers[0].s;
         req(&s.x_in, resid);
@@ -541,6 +549,16 @@ flint_status forward_layer(const flint_gpt2& m, const Layer& L, flint_stream st)
                                        s.x_mid, rows, w, 4 * w, st);
 }
 
+// Runs a deferred LayerNorm merge on its own (before its workspace is used
+// again, or at the end of the backward).
+flint_status flush_merge(const flint_gpt2& m, flint_stream st) {
+    if (m.pending.cols > 0) {
+        FLINT_HIP_CHECK(flint::launch_params_merge(m.pending, flint::to_hip(st)));
+        m.pending = flint::ParamsMerge{};
+    }
+    return FLINT_OK;
+}
+
 flint_status weight_grad(const flint_gpt2& m, const Param& p, const void* x, const void* w,
                          int acc, flint_stream st) {
     return flint_gemm_tn(p.grad, x, w, p.rows, p.cols, m.rows, acc, m.tn_work, m.tn_work_bytes,
@@ -561,19 +579,22 @@ flint_status bias_grad(const flint_gpt2& m, const Param& p, const void* dy, int 
 // tests compare the two).
 flint_status linear_grads(const flint_gpt2& m, const Param& w, const Param& b, const void* dy,
                           const void* x, int acc, flint_stream st) {
+    const hipStream_t hs = flint::to_hip(st);
     const char* e = std::getenv("FLINT_FUSED_GRADS");
     if (e != nullptr && e[0] == '0' && e[1] == '\0') {
+        FLINT_TRY(flush_merge(m, st));
         FLINT_TRY(weight_grad(m, w, dy, x, acc, st));
         return bias_grad(m, b, dy, acc, st);
     }
-    const hipStream_t hs = flint::to_hip(st);
     int splits = 1;
     FLINT_HIP_CHECK(flint::launch_gemm_tn_split(w.grad, dy, x, w.rows, w.cols, m.rows, acc != 0,
                                                 m.tn_work, &splits, hs));
     FLINT_HIP_CHECK(flint::launch_bias_partials(m.work, dy, m.rows, b.cols, hs));
+    // The finish also carries a LayerNorm backward's deferred merge.
     FLINT_HIP_CHECK(flint::launch_linear_grads_finish(w.grad, m.tn_work, w.rows, w.cols, splits,
                                                       acc != 0, b.grad, m.work, m.rows, b.cols,
-                                                      acc != 0, hs));
+                                                      acc != 0, hs, &m.pending));
+    m.pending = flint::ParamsMerge{};
     return FLINT_OK;
 }
 
@@ -596,10 +617,16 @@ flint_status norm_backward(const flint_gpt2& m, const Norm& n, const void* x, co
                                            m.work_bytes, st));
         return flint_fp32_to_fp16(m.dres_half, m.dres, m.rows * m.cfg.width, st);
     }
+    // Its dbeta / dgamma merge is left to the next linear layer's finish
+    // (FLINT_LN_DEFER=0: merged here).
+    FLINT_TRY(flush_merge(m, st));
+    const char* d = std::getenv("FLINT_LN_DEFER");
+    const bool defer = !(d != nullptr && d[0] == '0' && d[1] == '\0');
     FLINT_HIP_CHECK(flint::launch_layernorm_backward(m.dres, n.w->grad, n.b->grad, m.dh, x, mean,
                                                      rstd, n.w->data, m.rows, m.cfg.width,
-                                                     acc_dx != 0, acc != 0, m.work,
-                                                     flint::to_hip(st), m.dres_half));
+                                                     acc_dx != 0, acc != 0, m.ln_work,
+                                                     flint::to_hip(st), m.dres_half,
+                                                     defer ? &m.pending : nullptr));
     return FLINT_OK;
 }
 
@@ -785,12 +812,14 @@ FLINT_API flint_status flint_gpt2_backward(flint_gpt2* model, const void* tokens
         check.require(!tok.meets({"grad", p.grad, p.rows * p.cols * 4}),
                       "tokens and the gradient of %s overlap", p.name.c_str());
     FLINT_TRY(check.status());
+    m.pending = flint::ParamsMerge{};   // nothing carries over from an earlier call
     // Output layer (tied to wte): dwte (+)= dlogits^T h_f; dh = dlogits wte.
     FLINT_TRY(weight_grad(m, *m.wte, m.dlogits, m.h_f, accumulate, stream));
     FLINT_TRY(flint_gemm_nn(m.dh, m.dlogits, m.wte_half, rows, w, c.padded_vocab, stream));
     FLINT_TRY(norm_backward(m, m.ln_f, m.x_final, m.mean_f, m.rstd_f, 0, accumulate, stream));
     for (auto L = m.layers.rbegin(); L != m.layers.rend(); ++L)
         FLINT_TRY(backward_layer(m, *L, accumulate, stream));
+    FLINT_TRY(flush_merge(m, stream));
     // The embedding always adds into wte's gradient: (old + output layer) + embedding.
     FLINT_TRY(flint_embedding_backward(m.wte->grad, m.wpe->grad, m.dres, tokens, c.sequences,
                                        c.length, c.padded_vocab, w, 1, accumulate, m.work,

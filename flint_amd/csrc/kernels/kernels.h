@@ -141,11 +141,28 @@ hipError_t launch_layernorm_forward(void* y, void* mean, void* rstd, const void*
 // With dx_half, RN16 of every dx value written goes there too (the values
 // flint_fp32_to_fp16 of dx would give). workspace:
 // layernorm_backward_workspace(rows, cols) bytes.
+// LayerNorm backward's last step, the merge of its dbeta and dgamma chunk
+// partials, as a description another launch can carry (cols == 0: none).
+struct ParamsMerge {
+    float* dbeta = nullptr;
+    float* dgamma = nullptr;
+    const float* part0 = nullptr;   // dbeta's chunk partials
+    const float* part1 = nullptr;   // dgamma's
+    size_t chunks = 0;
+    int cols = 0;
+    int accumulate = 0;
+};
+// With `deferred`, a plan that ends in a separate merge launch leaves that
+// launch out and describes it in *deferred instead (cols = 0 when the merge
+// was done); the caller then runs it with launch_params_merge or passes it to
+// launch_linear_grads_finish, before the workspace is used again.
 hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const void* dy,
                                      const void* x, const void* mean, const void* rstd,
                                      const void* gamma, size_t rows, size_t cols,
                                      bool accumulate_dx, bool accumulate_params, void* workspace,
-                                     hipStream_t stream, void* dx_half = nullptr);
+                                     hipStream_t stream, void* dx_half = nullptr,
+                                     ParamsMerge* deferred = nullptr);
+hipError_t launch_params_merge(const ParamsMerge& merge, hipStream_t stream);
 hipError_t launch_bias_gradient(void* dbias, const void* dy, size_t rows, size_t cols,
                                 bool accumulate, void* workspace, hipStream_t stream);
 // The same two passes with the partials in the library's per-device scratch
@@ -167,7 +184,8 @@ hipError_t launch_bias_partials(void* workspace, const void* dy, size_t rows, si
 hipError_t launch_linear_grads_finish(void* dw, const void* dw_partials, size_t m, size_t n,
                                       int splits, bool accumulate_w, void* db,
                                       const void* db_workspace, size_t rows, size_t cols,
-                                      bool accumulate_b, hipStream_t stream);
+                                      bool accumulate_b, hipStream_t stream,
+                                      const ParamsMerge* also = nullptr);
 // zero_span 0 writes every chunk of a row (the ABI functions); Z > 0 (a
 // multiple of 8) writes the masked zeros only up to the end of the Z-column
 // block holding the diagonal, for consumers that read no further (the model's

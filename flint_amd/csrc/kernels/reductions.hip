@@ -275,6 +275,17 @@ column_finish(float* __restrict__ out, const float* __restrict__ partial, size_t
     finish_quad(out, partial, chunks, cols, accumulate, quad, threadIdx.x & 31);
 }
 
+// A merge of two column-partial sets (a LayerNorm's dbeta into out0, dgamma
+// into out1).
+struct ColumnFinish {
+    float* out0;
+    float* out1;
+    const float* part0;
+    const float* part1;
+    size_t chunks;
+    int accumulate;
+};
+
 // One linear layer's gradients in one launch: workgroups [0, reduce_blocks)
 // sum the weight gradient's k-split partials (tn_reduce's loop), the rest
 // merge the bias gradient's chunk partials (column_finish's).
@@ -282,10 +293,20 @@ __global__ void __launch_bounds__(256)
 linear_grads_finish(float* __restrict__ dw, const float* __restrict__ dw_partials, size_t quads,
                     int splits, int accumulate_w, unsigned reduce_blocks, float* __restrict__ db,
                     const float* __restrict__ db_partial, size_t chunks, int cols,
-                    int accumulate_b) {
+                    int accumulate_b, unsigned finish_blocks, ColumnFinish ln, int ln_cols) {
     if (blockIdx.x < reduce_blocks) {
         add_split_partials(dw, dw_partials, quads, splits, accumulate_w,
                            size_t(blockIdx.x) * 256 + threadIdx.x, size_t(reduce_blocks) * 256);
+        return;
+    }
+    if (blockIdx.x >= reduce_blocks + finish_blocks) {
+        // A LayerNorm backward's deferred dbeta / dgamma merge.
+        const int ln_quads = ln_cols / 4;
+        const int job = int(blockIdx.x - reduce_blocks - finish_blocks) * 8 + (threadIdx.x >> 5);
+        if (job >= 2 * ln_quads) return;   // whole half-waves leave together
+        const bool second = job >= ln_quads;
+        finish_quad(second ? ln.out1 : ln.out0, second ? ln.part1 : ln.part0, ln.chunks, ln_cols,
+                    ln.accumulate, second ? job - ln_quads : job, threadIdx.x & 31);
         return;
     }
     const int quad = int(blockIdx.x - reduce_blocks) * 8 + (threadIdx.x >> 5);
@@ -406,16 +427,9 @@ hipError_t launch_partials(float* partial, const void* dy, size_t rows, size_t c
 // ------------------------------------------------------------ LayerNorm dx
 
 // The merge of dbeta's and dgamma's chunk partials (column_finish's, for two
-// outputs), done by the dx kernel's first half-waves before their rows: the
-// partials come from the launch before it, so the kernel boundary orders them.
-struct ColumnFinish {
-    float* out0;
-    float* out1;
-    const float* part0;
-    const float* part1;
-    size_t chunks;
-    int accumulate;
-};
+// outputs): by the dx kernel's first half-waves before their rows when the
+// partials come from the launch before it (the kernel boundary orders them),
+// or by ln_params_finish / linear_grads_finish after the one-launch plan.
 
 __device__ __forceinline__ void finish_columns(const ColumnFinish& f, int cols) {
     const int quads = cols / 4;
@@ -938,17 +952,38 @@ hipError_t launch_bias_partials(void* workspace, const void* dy, size_t rows, si
 hipError_t launch_linear_grads_finish(void* dw, const void* dw_partials, size_t m, size_t n,
                                       int splits, bool accumulate_w, void* db,
                                       const void* db_workspace, size_t rows, size_t cols,
-                                      bool accumulate_b, hipStream_t stream) {
+                                      bool accumulate_b, hipStream_t stream,
+                                      const ParamsMerge* also) {
     const size_t quads = m * n / 4;
     const unsigned reduce_blocks =
         splits > 1 ? unsigned(std::clamp<size_t>((quads + 255) / 256, 1, 8192)) : 0u;
     const size_t chunks = (rows + kChunkRows - 1) / kChunkRows;
     const unsigned finish_blocks = unsigned((cols / 4 + 7) / 8);
-    hipLaunchKernelGGL(linear_grads_finish, dim3(reduce_blocks + finish_blocks), dim3(256), 0,
-                       stream, static_cast<float*>(dw), static_cast<const float*>(dw_partials),
-                       quads, splits, accumulate_w ? 1 : 0, reduce_blocks,
-                       static_cast<float*>(db), static_cast<const float*>(db_workspace), chunks,
-                       int(cols), accumulate_b ? 1 : 0);
+    ColumnFinish ln{};
+    int ln_cols = 0;
+    unsigned ln_blocks = 0;
+    if (also != nullptr && also->cols > 0) {
+        ln = ColumnFinish{also->dbeta, also->dgamma, also->part0, also->part1, also->chunks,
+                          also->accumulate};
+        ln_cols = also->cols;
+        ln_blocks = unsigned((2 * (ln_cols / 4) + 7) / 8);
+    }
+    hipLaunchKernelGGL(linear_grads_finish, dim3(reduce_blocks + finish_blocks + ln_blocks),
+                       dim3(256), 0, stream, static_cast<float*>(dw),
+                       static_cast<const float*>(dw_partials), quads, splits,
+                       accumulate_w ? 1 : 0, reduce_blocks, static_cast<float*>(db),
+                       static_cast<const float*>(db_workspace), chunks, int(cols),
+                       accumulate_b ? 1 : 0, finish_blocks, ln, ln_cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_params_merge(const ParamsMerge& merge, hipStream_t stream) {
+    if (merge.cols <= 0) return hipSuccess;
+    const ColumnFinish finish{merge.dbeta, merge.dgamma, merge.part0, merge.part1, merge.chunks,
+                              merge.accumulate};
+    const unsigned fin = unsigned(std::min<size_t>((2 * (size_t(merge.cols) / 4) + 7) / 8,
+                                                   kMaxBlocks));
+    hipLaunchKernelGGL(ln_params_finish, dim3(fin), dim3(256), 0, stream, finish, merge.cols);
     return hipGetLastError();
 }
 
@@ -965,7 +1000,8 @@ hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const 
                                      const void* x, const void* mean, const void* rstd,
                                      const void* gamma, size_t rows, size_t cols,
                                      bool accumulate_dx, bool accumulate_params, void* workspace,
-                                     hipStream_t stream, void* dx_half) {
+                                     hipStream_t stream, void* dx_half, ParamsMerge* deferred) {
+    if (deferred != nullptr) *deferred = ParamsMerge{};
     if (cols == 0 || cols % 8 != 0 || rows == 0) return hipErrorInvalidValue;
     const size_t chunks = (rows + kChunkRows - 1) / kChunkRows;
     const size_t region = chunks * 2 * cols;   // floats
@@ -1002,9 +1038,14 @@ hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const 
         else if (pieces <= 128) FLINT_LNF(4);
         else FLINT_LNF(8);
 #undef FLINT_LNF
-        const unsigned fin = unsigned(std::min<size_t>((2 * (cols / 4) + 7) / 8, kMaxBlocks));
-        hipLaunchKernelGGL(ln_params_finish, dim3(fin), dim3(256), 0, stream, finish, c);
-        return hipGetLastError();
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+        const ParamsMerge merge{static_cast<float*>(dbeta), static_cast<float*>(dgamma), part0,
+                                part1, chunks, c, accumulate_params ? 1 : 0};
+        if (deferred != nullptr) {
+            *deferred = merge;
+            return hipSuccess;
+        }
+        return launch_params_merge(merge, stream);
     }
     // dbeta and dgamma partials, one pass over dy and x.
     hipLaunchKernelGGL(column_partials2, dim3(unsigned(std::min<size_t>(items, kMaxBlocks))),
