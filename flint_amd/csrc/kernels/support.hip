@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 
 #include "common/common.h"
 #include "kernels/kernels.h"
@@ -245,9 +246,9 @@ sort_scatter(uint16_t* __restrict__ out_tokens, unsigned* __restrict__ out_rows,
 // order, 64 at a time, ranked among equal digits by ballots.
 constexpr int kBlockSortRows = 8192;
 
-__global__ void __launch_bounds__(1024)
-sort_tokens_block(uint16_t* __restrict__ out_tokens, unsigned* __restrict__ out_rows,
-                  const uint16_t* __restrict__ tokens, int rows) {
+__device__ __forceinline__ void sort_block_body(uint16_t* __restrict__ out_tokens,
+                                                unsigned* __restrict__ out_rows,
+                                                const uint16_t* __restrict__ tokens, int rows) {
     __shared__ uint16_t key[2][kBlockSortRows];
     __shared__ unsigned idx[2][kBlockSortRows];
     __shared__ unsigned cnt[16][kDigits];
@@ -325,6 +326,13 @@ sort_tokens_block(uint16_t* __restrict__ out_tokens, unsigned* __restrict__ out_
         out_rows[i] = idx[0][i];
     }
 }
+
+__global__ void __launch_bounds__(1024)
+sort_tokens_block(uint16_t* __restrict__ out_tokens, unsigned* __restrict__ out_rows,
+                  const uint16_t* __restrict__ tokens, int rows) {
+    sort_block_body(out_tokens, out_rows, tokens, rows);
+}
+
 
 // offsets[v] = number of sorted tokens below v, v = 0..vocab (binary search).
 __global__ void __launch_bounds__(256)
@@ -486,10 +494,9 @@ column_partials_f32(float* __restrict__ partial, const float* __restrict__ dy, s
 // in order, and then applies what column_finish does to a single chunk -- lane
 // 0 merges it into an empty sum and the 32-lane butterfly merges five empty
 // lanes' sums into it.
-__global__ void __launch_bounds__(256)
-column_sums_one_chunk(float* __restrict__ out, const float* __restrict__ dy, int rows,
-                      size_t cols, int accumulate) {
-    const size_t quad = size_t(blockIdx.x) * 256 + threadIdx.x;
+__device__ __forceinline__ void column_sums_quad(float* __restrict__ out,
+                                                 const float* __restrict__ dy, int rows,
+                                                 size_t cols, int accumulate, size_t quad) {
     if (quad >= cols / 4) return;
     Comp acc[kPhasesF32][4];
     for (int k = 0; k < rows; k += kPhasesF32) {
@@ -521,6 +528,30 @@ column_sums_one_chunk(float* __restrict__ out, const float* __restrict__ dy, int
                add_rn(old[3], r[3])};
     }
     *o = r;
+}
+
+__global__ void __launch_bounds__(256)
+column_sums_one_chunk(float* __restrict__ out, const float* __restrict__ dy, int rows,
+                      size_t cols, int accumulate) {
+    column_sums_quad(out, dy, rows, cols, accumulate, size_t(blockIdx.x) * 256 + threadIdx.x);
+}
+
+// The block sort and the position gradient in one launch: they are
+// independent, and the sort's one workgroup leaves the other CUs idle.
+// Workgroup 0 sorts; workgroup b > 0 takes column quads (b - 1) * 1024 + t of
+// column_sums_one_chunk's sums (the same arithmetic; the sort's LDS makes
+// these one workgroup per CU, 1,024 threads each).
+__global__ void __launch_bounds__(1024)
+sort_tokens_and_positions(uint16_t* __restrict__ out_tokens, unsigned* __restrict__ out_rows,
+                          const uint16_t* __restrict__ tokens, int rows,
+                          float* __restrict__ dwpe, const float* __restrict__ dx,
+                          int sequences, size_t cols, int accumulate) {
+    if (blockIdx.x == 0) {
+        sort_block_body(out_tokens, out_rows, tokens, rows);
+        return;
+    }
+    column_sums_quad(dwpe, dx, sequences, cols, accumulate,
+                     size_t(blockIdx.x - 1) * 1024 + threadIdx.x);
 }
 
 }  // namespace
@@ -622,7 +653,19 @@ hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, con
 
     // Two stable passes of 8 bits: low byte into the pass buffers, high byte
     // into the sorted buffers; in one workgroup's LDS when the rows fit.
-    if (rows <= size_t(kBlockSortRows)) {
+    const size_t cols = length * width;   // dwpe: column sums of dx as sequences x cols
+    // With one chunk of sequences the position gradient rides in the sort's
+    // launch (FLINT_EMB_TOGETHER=0: its own launch after the token rows).
+    const char* te = std::getenv("FLINT_EMB_TOGETHER");
+    const bool together = rows <= size_t(kBlockSortRows) && sequences <= 256 &&
+                          (cols / 4 + 1023) / 1024 < (size_t{1} << 30) &&
+                          !(te != nullptr && te[0] == '0' && te[1] == '\0');
+    if (together) {
+        hipLaunchKernelGGL(sort_tokens_and_positions, dim3(unsigned(1 + (cols / 4 + 1023) / 1024)),
+                           dim3(1024), 0, stream, sorted_tokens, sorted_rows, tok, int(rows),
+                           static_cast<float*>(dwpe), static_cast<const float*>(dx),
+                           int(sequences), cols, accumulate_wpe ? 1 : 0);
+    } else if (rows <= size_t(kBlockSortRows)) {
         hipLaunchKernelGGL(sort_tokens_block, dim3(1), dim3(1024), 0, stream, sorted_tokens,
                            sorted_rows, tok, int(rows));
     }
@@ -656,7 +699,7 @@ hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, con
     }
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     // dwpe: column sums of dx viewed as sequences x (length * width).
-    const size_t cols = length * width;
+    if (together) return hipSuccess;
     if (sequences <= 256) {
         hipLaunchKernelGGL(column_sums_one_chunk, dim3(unsigned((cols / 4 + 255) / 256)),
                            dim3(256), 0, stream, static_cast<float*>(dwpe),

@@ -51,8 +51,11 @@ def test_embedding_forward_matches_pytorch_bitwise(flint, cuda, sequences, lengt
     (2, 1500, 5000, 16, "zipf"), (4, 256, 65536, 8, "uniform"), (9, 16, 300, 16, "zipf"),
     (300, 8, 100, 8, "uniform"), (3, 4000, 65536, 8, "uniform"), (5, 1700, 3000, 8, "zipf")])
 @pytest.mark.parametrize("accumulate", [False, True])
-def test_embedding_backward_matches_the_oracle_bitwise(flint, cuda, sequences, length, vocab,
+@pytest.mark.parametrize("together", ["1", "0"])   # position sums in the sort's launch, or after
+def test_embedding_backward_matches_the_oracle_bitwise(flint, cuda, monkeypatch, together,
+                                                       sequences, length, vocab,
                                                        width, kind, accumulate):
+    monkeypatch.setenv("FLINT_EMB_TOGETHER", together)
     rows = sequences * length
     g = torch.Generator().manual_seed(4)
     if kind == "uniform":
