@@ -288,9 +288,11 @@ WIDE = dict(layers=1, heads=4, width=256, block_size=1024, vocab=1000, padded_vo
 @pytest.mark.parametrize("cfg,sequences,length", [(TINY, 8, 64), (ODD, 2, 48), (WIDE, 2, 520)],
                          ids=["tiny-8x64", "odd-2x48", "wide-2x520"])
 def test_fused_column_sums_change_no_bits(flint, cuda, monkeypatch, cfg, sequences, length):
-    """The model's LayerNorm dbeta and dgamma come from one partials pass and
-    one finish (FLINT_FUSED_SUMS unset); flint_layernorm_backward's separate
-    passes (=0) must give the same bits."""
+    """The model's LayerNorm backward runs its chunk partials and dx rows in
+    one launch and leaves the dbeta / dgamma merge to the next linear layer's
+    finish (FLINT_FUSED_SUMS and FLINT_LN_DEFER unset); the merge in a launch
+    of its own (FLINT_LN_DEFER=0) and flint_layernorm_backward plus a
+    conversion (FLINT_FUSED_SUMS=0) must give the same bits."""
     shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
                                 cfg["padded_vocab"])
     params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=13, trained=True)
@@ -298,10 +300,14 @@ def test_fused_column_sums_change_no_bits(flint, cuda, monkeypatch, cfg, sequenc
     monkeypatch.setenv("FLINT_FUSED_SUMS", "0")
     plain = _run(flint, cfg, sequences, length, params, idx, tgt, 0.5)
     monkeypatch.delenv("FLINT_FUSED_SUMS")
+    monkeypatch.setenv("FLINT_LN_DEFER", "0")
+    in_place = _run(flint, cfg, sequences, length, params, idx, tgt, 0.5)
+    monkeypatch.delenv("FLINT_LN_DEFER")
     fused = _run(flint, cfg, sequences, length, params, idx, tgt, 0.5)
-    for n in plain[3]:
-        assert torch.equal(plain[3][n].view(torch.int32), fused[3][n].view(torch.int32)), n
-    assert plain[4] == fused[4]
+    for other in (in_place, fused):
+        for n in plain[3]:
+            assert torch.equal(plain[3][n].view(torch.int32), other[3][n].view(torch.int32)), n
+        assert plain[4] == other[4]
 
 
 @pytest.mark.parametrize("cfg,sequences,length", [(TINY, 8, 64), (ODD, 2, 48), (WIDE, 2, 520)],
