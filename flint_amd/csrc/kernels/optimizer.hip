@@ -28,6 +28,7 @@ namespace flint {
 namespace {
 
 constexpr int kThreads = 256;
+static_assert(kAdamwChunk % (4 * kThreads * 4) == 0, "whole float4 rounds per chunk");
 
 struct Decision {
     float inv_scale;   // 1 / loss scale used for this step's gradients
@@ -65,6 +66,24 @@ __global__ void __launch_bounds__(kThreads) adamw_sumsq(AdamwGroup group, double
     const unsigned long long end = begin + kAdamwChunk < t.n ? begin + kAdamwChunk : t.n;
     const float inv = float(1.0 / double(state->loss_scale));
     double acc = 0;
+    constexpr int kPer = int(kAdamwChunk / (4 * kThreads));   // float4s per thread in a chunk
+    if (end - begin == kAdamwChunk) {
+        // A whole chunk: every load issued before the first add, the adds in
+        // the order of the loop below (the same sum).
+        float4 gv[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
+            gv[k] = *reinterpret_cast<const float4*>(t.g + begin + 4ull * threadIdx.x +
+                                                     4ull * kThreads * k);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const float a = gv[k].x * inv, bb = gv[k].y * inv, c = gv[k].z * inv, d = gv[k].w * inv;
+            acc += double(a) * a + double(bb) * bb + double(c) * c + double(d) * d;
+        }
+        const double sum = block_sum(acc, lds);
+        if (threadIdx.x == 0) partials[group.partial_offset + b] = sum;
+        return;
+    }
     for (unsigned long long e = begin + 4ull * threadIdx.x; e < end; e += 4ull * kThreads) {
         if (e + 3 < end) {
             const float4 g = *reinterpret_cast<const float4*>(t.g + e);
@@ -88,7 +107,16 @@ __global__ void __launch_bounds__(kThreads) adamw_decide(const double* partials,
                                                           float backoff_factor, int growth_interval) {
     __shared__ double lds[kThreads];
     double acc = 0;
-    for (int k = threadIdx.x; k < count; k += kThreads) acc += partials[k];
+    // Eight loads in flight per thread, added in order (the same sum).
+    int k = threadIdx.x;
+    for (; k + 7 * kThreads < count; k += 8 * kThreads) {
+        double v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = partials[k + j * kThreads];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += v[j];
+    }
+    for (; k < count; k += kThreads) acc += partials[k];
     const double sumsq = block_sum(acc, lds);
     if (threadIdx.x != 0) return;
     flint_train_state s = *state;
@@ -147,6 +175,40 @@ __global__ void __launch_bounds__(kThreads) adamw_update(AdamwGroup group, const
     const AdamwTensorArgs& t = group.t[i];
     const unsigned long long begin = (unsigned long long)(b - group.block_start[i]) * kAdamwChunk;
     const unsigned long long end = begin + kAdamwChunk < t.n ? begin + kAdamwChunk : t.n;
+    if (end - begin == kAdamwChunk) {
+        // A whole chunk in rounds of 4 float4s a thread, each round's loads
+        // issued before its arithmetic.
+        constexpr int kPer = int(kAdamwChunk / (4 * kThreads)), kRound = 4;
+#pragma unroll
+        for (int r0 = 0; r0 < kPer; r0 += kRound) {
+            float4 p[kRound], g[kRound], m[kRound], v[kRound];
+#pragma unroll
+            for (int k = 0; k < kRound; ++k) {
+                const unsigned long long e = begin + 4ull * threadIdx.x + 4ull * kThreads * (r0 + k);
+                p[k] = *reinterpret_cast<const float4*>(t.p + e);
+                g[k] = *reinterpret_cast<const float4*>(t.g + e);
+                m[k] = *reinterpret_cast<const float4*>(t.m + e);
+                v[k] = *reinterpret_cast<const float4*>(t.v + e);
+            }
+#pragma unroll
+            for (int k = 0; k < kRound; ++k) {
+                const unsigned long long e = begin + 4ull * threadIdx.x + 4ull * kThreads * (r0 + k);
+                adamw_element(p[k].x, g[k].x, m[k].x, v[k].x, t.decay, d, mo);
+                adamw_element(p[k].y, g[k].y, m[k].y, v[k].y, t.decay, d, mo);
+                adamw_element(p[k].z, g[k].z, m[k].z, v[k].z, t.decay, d, mo);
+                adamw_element(p[k].w, g[k].w, m[k].w, v[k].w, t.decay, d, mo);
+                *reinterpret_cast<float4*>(t.p + e) = p[k];
+                *reinterpret_cast<float4*>(t.m + e) = m[k];
+                *reinterpret_cast<float4*>(t.v + e) = v[k];
+                if (t.h) {
+                    __half2* h = reinterpret_cast<__half2*>(t.h + e);
+                    h[0] = __floats2half2_rn(p[k].x, p[k].y);
+                    h[1] = __floats2half2_rn(p[k].z, p[k].w);
+                }
+            }
+        }
+        return;
+    }
     for (unsigned long long e = begin + 4ull * threadIdx.x; e < end; e += 4ull * kThreads) {
         if (e + 3 < end) {
             float4 p = *reinterpret_cast<const float4*>(t.p + e);
