@@ -53,6 +53,10 @@
 namespace fb {
 namespace {
 
+// flint.h declares its stream type as the reference does; the value is this
+// harness's hipStream_t.
+inline flint_stream as_flint(hipStream_t s) { return reinterpret_cast<flint_stream>(s); }
+
 // ---------------------------------------------------------------- errors
 
 struct Failure : std::runtime_error {
@@ -482,7 +486,7 @@ CaseResult copy_case(unsigned long long bytes, const DeviceInfo& d, const Option
     spec.flint = [&, stride, sets, bytes](hipStream_t st, long long first, long long count) {
         for (long long i = first; i < first + count; ++i) {
             const size_t off = stride * size_t(i % sets);
-            flint_check(flint_copy(dst.at(off), src.at(off), bytes, st), "flint_copy");
+            flint_check(flint_copy(dst.at(off), src.at(off), bytes, as_flint(st)), "flint_copy");
         }
     };
     spec.reference = [&, stride, sets, bytes](hipStream_t st, long long first, long long count) {
@@ -500,7 +504,7 @@ CaseResult copy_case(unsigned long long bytes, const DeviceInfo& d, const Option
     bool match = true;
     for (int side = 0; side < 2; ++side) {
         hip_check(hipMemsetAsync(dst.ptr, 0xA5 + side, bytes, s), "hipMemsetAsync");
-        if (side == 0) flint_check(flint_copy(dst.ptr, src.ptr, bytes, s), "flint_copy");
+        if (side == 0) flint_check(flint_copy(dst.ptr, src.ptr, bytes, as_flint(s)), "flint_copy");
         else hip_check(hipMemcpyAsync(dst.ptr, src.ptr, bytes, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync");
         hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
         hip_check(hipMemcpy(got.data(), dst.ptr, bytes, hipMemcpyDeviceToHost), "hipMemcpy");
@@ -654,25 +658,25 @@ CaseResult gemm_case(const Shape& sh, Layout layout, Epilogue ep, const DeviceIn
         const void* bias = B.at(sb * i);
         switch (layout) {
         case Layout::TN:
-            flint_check(flint_gemm_tn(y, x, w, m, n, k, accumulate ? 1 : 0, tn_workspace.ptr, tn_ws, st),
+            flint_check(flint_gemm_tn(y, x, w, m, n, k, accumulate ? 1 : 0, tn_workspace.ptr, tn_ws, as_flint(st)),
                         "flint_gemm_tn");
             return;
         case Layout::NN:
-            if (ep == Epilogue::DGelu) flint_check(flint_gemm_nn_dgelu(y, x, w, pre, m, n, k, st), "flint_gemm_nn_dgelu");
-            else flint_check(flint_gemm_nn(y, x, w, m, n, k, st), "flint_gemm_nn");
+            if (ep == Epilogue::DGelu) flint_check(flint_gemm_nn_dgelu(y, x, w, pre, m, n, k, as_flint(st)), "flint_gemm_nn_dgelu");
+            else flint_check(flint_gemm_nn(y, x, w, m, n, k, as_flint(st)), "flint_gemm_nn");
             return;
         case Layout::NT: break;
         }
         switch (ep) {
-        case Epilogue::Bias: flint_check(flint_gemm_nt_bias(y, x, w, bias, m, n, k, st), "flint_gemm_nt_bias"); return;
+        case Epilogue::Bias: flint_check(flint_gemm_nt_bias(y, x, w, bias, m, n, k, as_flint(st)), "flint_gemm_nt_bias"); return;
         case Epilogue::BiasGelu:
-            flint_check(flint_gemm_nt_bias_gelu(y, pre, x, w, bias, m, n, k, st), "flint_gemm_nt_bias_gelu");
+            flint_check(flint_gemm_nt_bias_gelu(y, pre, x, w, bias, m, n, k, as_flint(st)), "flint_gemm_nt_bias_gelu");
             return;
         case Epilogue::BiasResidual:
-            flint_check(flint_gemm_nt_bias_residual(y, x, w, bias, R.at(sr * i), m, n, k, st),
+            flint_check(flint_gemm_nt_bias_residual(y, x, w, bias, R.at(sr * i), m, n, k, as_flint(st)),
                         "flint_gemm_nt_bias_residual");
             return;
-        default: flint_check(flint_gemm_nt(y, x, w, m, n, k, st), "flint_gemm_nt"); return;
+        default: flint_check(flint_gemm_nt(y, x, w, m, n, k, as_flint(st)), "flint_gemm_nt"); return;
         }
     };
 

@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "common/args.h"
+#include "common/tuning.h"
 #include "kernels/kernels.h"
 
 using flint::fail;
@@ -102,7 +103,7 @@ struct flint_gpt2 {
     flint_gpt2_config cfg{};
     size_t rows = 0, head_width = 0, head_batches = 0;
     // Fused attention (attention.hip) in place of the stored scores and
-    // probabilities; decided at creation (head width 64, FLINT_FLASH not "0").
+    // probabilities: chosen at creation (flint_gpt2_create_fused), head width 64.
     bool flash = false;
     void* attn_work = nullptr;   // the fused backward's D
     std::deque<Param> params;   // stable addresses
@@ -120,11 +121,13 @@ struct flint_gpt2 {
     size_t work_bytes = 0;
     void* tn_work = nullptr;
     size_t tn_work_bytes = 0;
-    // LayerNorm backward's chunk partials, apart from `work`: their merge is
-    // deferred to the next linear layer's gradient finish (after that
-    // layer's bias partials have used `work`); `pending` describes it.
-    void* ln_work = nullptr;
-    size_t ln_work_bytes = 0;
+    // LayerNorm backward's chunk partials sit in `work` past the first
+    // ln_offset bytes, where a linear layer's bias partials of up to
+    // ln_offset bytes leave them alone: their merge is then deferred to the
+    // next linear layer's gradient finish; `pending` describes it. ln_offset
+    // is 0 when the two do not fit side by side in `work` (the merge then
+    // runs at once).
+    size_t ln_offset = 0;
     mutable flint::ParamsMerge pending{};
     std::vector<Request> requests;
     std::vector<void*> blocks;   // hipMalloc'd allocations
@@ -141,66 +144,45 @@ struct flint_gpt2 {
 
 namespace {
 
+// The configuration's limits, in the order and words the reference reports
+// them (ref src/api/gpt2.cpp:187-243). A link's condition is evaluated even
+// after an earlier one failed (only the first failure is reported), so each
+// guards its own divisions.
 flint_status check_config(const char* name, const flint_gpt2_config* config) {
-    if (config == nullptr) return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: config is null", name);
+    flint::Checker ck(name);
+    if (!ck.require(config != nullptr, "config is null").ok()) return ck.status();
     const flint_gpt2_config& c = *config;
-    if (c.layers == 0 || c.layers > kMaxLayers) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: layers (%zu) must be from 1 to %zu", name,
-                    c.layers, kMaxLayers);
-    }
-    if (c.width == 0 || c.width % 8 != 0 || c.width > kMaxWidth) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: width (%zu) must be a multiple of 8 from 8 to %zu", name, c.width,
-                    kMaxWidth);
-    }
-    if (c.heads == 0 || c.width % c.heads != 0 || (c.width / c.heads) % 8 != 0) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: heads (%zu) must split width (%zu) into multiples of 8", name, c.heads,
-                    c.width);
-    }
-    if (c.length == 0 || c.length % 8 != 0 || c.length > kMaxLength) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: length (%zu) must be a multiple of 8 from 8 to %zu", name, c.length,
-                    kMaxLength);
-    }
-    if (c.block_size < c.length || c.block_size > kMaxLength) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: block_size (%zu) must be from length (%zu) to %zu", name, c.block_size,
-                    c.length, kMaxLength);
-    }
-    if (c.padded_vocab == 0 || c.padded_vocab % 8 != 0 || c.padded_vocab > kMaxPaddedVocab) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: padded_vocab (%zu) must be a multiple of 8 from 8 to %zu", name,
-                    c.padded_vocab, kMaxPaddedVocab);
-    }
-    if (c.vocab == 0 || c.vocab > c.padded_vocab) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: vocab (%zu) must be from 1 to padded_vocab (%zu)", name, c.vocab,
-                    c.padded_vocab);
-    }
-    if (c.sequences == 0 || c.sequences > kMaxHeadBatches / c.heads) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: sequences (%zu) x heads (%zu) must be from 1 to %zu", name, c.sequences,
-                    c.heads, kMaxHeadBatches);
-    }
-    if (c.sequences > kMaxRows / c.length) {
-        return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                    "%s: sequences (%zu) x length (%zu) can be up to %zu rows", name, c.sequences,
-                    c.length, kMaxRows);
-    }
+    ck.require(c.layers != 0 && c.layers <= kMaxLayers, "layers (%zu) must be from 1 to %zu",
+               c.layers, kMaxLayers)
+        .require(c.width != 0 && c.width % 8 == 0 && c.width <= kMaxWidth,
+                 "width (%zu) must be a multiple of 8 from 8 to %zu", c.width, kMaxWidth)
+        .require(c.heads != 0 && c.width % c.heads == 0 && (c.width / c.heads) % 8 == 0,
+                 "heads (%zu) must split width (%zu) into multiples of 8", c.heads, c.width)
+        .require(c.length != 0 && c.length % 8 == 0 && c.length <= kMaxLength,
+                 "length (%zu) must be a multiple of 8 from 8 to %zu", c.length, kMaxLength)
+        .require(c.block_size >= c.length && c.block_size <= kMaxLength,
+                 "block_size (%zu) must be from length (%zu) to %zu", c.block_size, c.length,
+                 kMaxLength)
+        .require(c.padded_vocab != 0 && c.padded_vocab % 8 == 0 && c.padded_vocab <= kMaxPaddedVocab,
+                 "padded_vocab (%zu) must be a multiple of 8 from 8 to %zu", c.padded_vocab,
+                 kMaxPaddedVocab)
+        .require(c.vocab != 0 && c.vocab <= c.padded_vocab,
+                 "vocab (%zu) must be from 1 to padded_vocab (%zu)", c.vocab, c.padded_vocab)
+        .require(c.sequences != 0 && c.heads != 0 && c.sequences <= kMaxHeadBatches / c.heads,
+                 "sequences (%zu) x heads (%zu) must be from 1 to %zu", c.sequences, c.heads,
+                 kMaxHeadBatches)
+        .require(c.length != 0 && c.sequences <= kMaxRows / c.length,
+                 "sequences (%zu) x length (%zu) can be up to %zu rows", c.sequences, c.length,
+                 kMaxRows);
     if (c.backward != 0) {
-        if (c.sequences > kMaxBackwardRows / c.length) {
-            return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                        "%s: sequences (%zu) x length (%zu) can be up to %zu rows with backward",
-                        name, c.sequences, c.length, kMaxBackwardRows);
-        }
-        if (c.length > kMaxBackwardPositionValues / c.width) {
-            return fail(FLINT_ERROR_INVALID_ARGUMENT,
-                        "%s: length (%zu) x width (%zu) can be up to %zu with backward", name,
-                        c.length, c.width, kMaxBackwardPositionValues);
-        }
+        ck.require(c.length != 0 && c.sequences <= kMaxBackwardRows / c.length,
+                   "sequences (%zu) x length (%zu) can be up to %zu rows with backward",
+                   c.sequences, c.length, kMaxBackwardRows)
+            .require(c.width != 0 && c.length <= kMaxBackwardPositionValues / c.width,
+                     "length (%zu) x width (%zu) can be up to %zu with backward", c.length,
+                     c.width, kMaxBackwardPositionValues);
     }
-    return FLINT_OK;
+    return ck.status();
 }
 
 Param* param(flint_gpt2& m, std::string name, size_t rows, size_t cols) {
@@ -220,11 +202,15 @@ flint_status size_workspaces(flint_gpt2& m) {
         FLINT_TRY(flint_bias_gradient_workspace(m.rows, cols, &b));
         need = std::max(need, b);
     }
-    FLINT_TRY(flint_layernorm_backward_workspace(m.rows, w, &b));
-    need = std::max(need, b);
-    m.ln_work_bytes = b;
+    size_t ln = 0, bias_w = 0;
+    FLINT_TRY(flint_layernorm_backward_workspace(m.rows, w, &ln));
+    need = std::max(need, ln);
     FLINT_TRY(flint_embedding_backward_workspace(c.sequences, c.length, c.padded_vocab, w, &b));
     m.work_bytes = std::max(need, b);
+    // The linear layer after a LayerNorm backward (attention projection, MLP
+    // down) has width-wide bias partials.
+    FLINT_TRY(flint_bias_gradient_workspace(m.rows, w, &bias_w));
+    m.ln_offset = round_up(bias_w) + ln <= m.work_bytes ? round_up(bias_w) : 0;
     const size_t shapes[][2] = {{c.padded_vocab, w}, {3 * w, w}, {w, w}, {4 * w, w}, {w, 4 * w}};
     need = 0;
     for (const auto& s : shapes) {
@@ -236,16 +222,9 @@ flint_status size_workspaces(flint_gpt2& m) {
 }
 
 // Declares every parameter (named_parameters order), gradient, compute copy,
-// activation and scratch buffer as a request; allocation comes after.
-// Whether the model runs the fused causal attention: head width 64 (the
-// kernels' width), unless FLINT_FLASH=0 asks for the stored scores and
-// probabilities (the reference's sequence; the bit-exactness tests of the
-// causal products use it).
-bool use_flash(size_t head_width) {
-    const char* e = std::getenv("FLINT_FLASH");
-    return head_width == 64 && !(e != nullptr && e[0] == '0' && e[1] == '\0');
-}
-
+// activation and scratch buffer as a request; allocation comes after. With
+// m.flash set (by the caller) the attention keeps the qkv projection and the
+// log-sum-exp instead of q, k, v and the probabilities.
 flint_status plan(flint_gpt2& m) {
     const flint_gpt2_config& c = m.cfg;
     const bool bwd = c.backward != 0;
@@ -253,7 +232,6 @@ flint_status plan(flint_gpt2& m) {
     m.rows = c.sequences * c.length;
     m.head_width = w / c.heads;
     m.head_batches = c.sequences * c.heads;
-    m.flash = use_flash(m.head_width);
 
     m.wte = param(m, "wte.weight", c.padded_vocab, w);
     m.wpe = param(m, "wpe.weight", c.block_size, w);
@@ -335,7 +313,6 @@ flint_status plan(flint_gpt2& m) {
         req(&m.dpre, rows * 4 * w * 2);
         req(&m.work, m.work_bytes);
         req(&m.tn_work, m.tn_work_bytes);
-        req(&m.ln_work, m.ln_work_bytes);
     } else {
         Saved& s = m.layers[0].s;
         req(&s.x_in, resid);
@@ -420,12 +397,9 @@ float score_scale(size_t head_width) { return 1.0f / std::sqrt(float(head_width)
 // causal softmax passes read the visible chunks alone), and P and dS are zero
 // above it, so the pipeline skips those tiles and k-ranges. The skipped
 // products are exact zeros, so no value that is read changes.
-// FLINT_ATTN_CAUSAL=0 computes everything and writes every zero (the tests
-// compare the two bit for bit).
-bool attn_causal() {
-    const char* e = std::getenv("FLINT_ATTN_CAUSAL");
-    return e == nullptr || !(e[0] == '0' && e[1] == '\0');
-}
+// The "attn_causal" override "0" computes everything and writes every zero
+// (the tests compare the two bit for bit).
+bool attn_causal() { return !flint::tuning_off(flint::Tune::kAttnCausal); }
 
 flint_status attn_nt(void* y, const void* x, const void* w, size_t batches, size_t m, size_t n,
                      size_t k, float scale, flint_stream st) {
@@ -575,17 +549,21 @@ flint_status bias_grad(const flint_gpt2& m, const Param& p, const void* dy, int 
 // partials, the bias's chunk partials, then one launch that sums the first
 // and merges the second, in place of flint_gemm_tn's and
 // flint_bias_gradient's two launches each (the same kernels' arithmetic, the
-// same bits). FLINT_FUSED_GRADS=0 calls the two entry points instead (the
-// tests compare the two).
+// same bits). The "fused_grads" override "0" calls the two entry points
+// instead (the tests compare the two).
 flint_status linear_grads(const flint_gpt2& m, const Param& w, const Param& b, const void* dy,
                           const void* x, int acc, flint_stream st) {
     const hipStream_t hs = flint::to_hip(st);
-    const char* e = std::getenv("FLINT_FUSED_GRADS");
-    if (e != nullptr && e[0] == '0' && e[1] == '\0') {
+    if (flint::tuning_off(flint::Tune::kFusedGrads)) {
         FLINT_TRY(flush_merge(m, st));
         FLINT_TRY(weight_grad(m, w, dy, x, acc, st));
         return bias_grad(m, b, dy, acc, st);
     }
+    // A deferred LayerNorm merge whose partials these bias partials would
+    // overwrite runs first.
+    size_t bias_bytes = 0;
+    FLINT_TRY(flint_bias_gradient_workspace(m.rows, b.cols, &bias_bytes));
+    if (bias_bytes > m.ln_offset) FLINT_TRY(flush_merge(m, st));
     int splits = 1;
     FLINT_HIP_CHECK(flint::launch_gemm_tn_split(w.grad, dy, x, w.rows, w.cols, m.rows, acc != 0,
                                                 m.tn_work, &splits, hs));
@@ -599,13 +577,10 @@ flint_status linear_grads(const flint_gpt2& m, const Param& w, const Param& b, c
 }
 
 // LayerNorm backward: dx, with its FP16 copy written by the dx kernel, then
-// dbeta and dgamma from one pass over dy and x. FLINT_FUSED_SUMS=0 calls
-// flint_layernorm_backward instead and converts dx to FP16 after it (the
-// tests compare the two).
-bool fused_sums() {
-    const char* e = std::getenv("FLINT_FUSED_SUMS");
-    return e == nullptr || !(e[0] == '0' && e[1] == '\0');
-}
+// dbeta and dgamma from one pass over dy and x. The "fused_sums" override
+// "0" calls flint_layernorm_backward instead and converts dx to FP16 after it
+// (the tests compare the two).
+bool fused_sums() { return !flint::tuning_off(flint::Tune::kFusedSums); }
 
 // On return dres holds the residual stream's gradient and dres_half its FP16
 // copy (written by the dx kernel, or converted after the ABI path).
@@ -618,13 +593,14 @@ flint_status norm_backward(const flint_gpt2& m, const Norm& n, const void* x, co
         return flint_fp32_to_fp16(m.dres_half, m.dres, m.rows * m.cfg.width, st);
     }
     // Its dbeta / dgamma merge is left to the next linear layer's finish
-    // (FLINT_LN_DEFER=0: merged here).
+    // where its partials fit beside that layer's bias partials ("ln_defer" =
+    // "0": merged here).
     FLINT_TRY(flush_merge(m, st));
-    const char* d = std::getenv("FLINT_LN_DEFER");
-    const bool defer = !(d != nullptr && d[0] == '0' && d[1] == '\0');
+    const bool defer = m.ln_offset > 0 && !flint::tuning_off(flint::Tune::kLnDefer);
+    void* const ws = static_cast<char*>(m.work) + (defer ? m.ln_offset : 0);
     FLINT_HIP_CHECK(flint::launch_layernorm_backward(m.dres, n.w->grad, n.b->grad, m.dh, x, mean,
                                                      rstd, n.w->data, m.rows, m.cfg.width,
-                                                     acc_dx != 0, acc != 0, m.ln_work,
+                                                     acc_dx != 0, acc != 0, ws,
                                                      flint::to_hip(st), m.dres_half,
                                                      defer ? &m.pending : nullptr));
     return FLINT_OK;
@@ -693,17 +669,23 @@ flint_status param_info(const char* name, const flint_gpt2* m, size_t index,
     return FLINT_OK;
 }
 
-}  // namespace
+// The fused attention's kernels take head width 64 only.
+flint_status check_fused(const char* name, const flint_gpt2_config& c) {
+    return flint::Checker(name)
+        .require(c.width / c.heads == 64, "the fused attention needs head width 64, not %zu",
+                 c.width / c.heads)
+        .status();
+}
 
-extern "C" {
-
-FLINT_API flint_status flint_gpt2_bytes(const flint_gpt2_config* config, size_t* bytes) {
-    constexpr const char* name = "flint_gpt2_bytes";
+flint_status model_bytes(const char* name, const flint_gpt2_config* config, bool fused,
+                         size_t* bytes) {
     FLINT_TRY(check_config(name, config));
+    if (fused) FLINT_TRY(check_fused(name, *config));
     if (bytes == nullptr) return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: bytes is null", name);
     try {
         flint_gpt2 m;
         m.cfg = *config;
+        m.flash = fused;
         FLINT_TRY(plan(m));
         *bytes = total_bytes(m);
     } catch (const std::bad_alloc&) {
@@ -712,14 +694,16 @@ FLINT_API flint_status flint_gpt2_bytes(const flint_gpt2_config* config, size_t*
     return FLINT_OK;
 }
 
-FLINT_API flint_status flint_gpt2_create(const flint_gpt2_config* config, flint_gpt2** model) {
-    constexpr const char* name = "flint_gpt2_create";
+flint_status create_model(const char* name, const flint_gpt2_config* config, bool fused,
+                          flint_gpt2** model) {
     if (model == nullptr) return fail(FLINT_ERROR_INVALID_ARGUMENT, "%s: model is null", name);
     *model = nullptr;
     FLINT_TRY(check_config(name, config));
+    if (fused) FLINT_TRY(check_fused(name, *config));
     try {
         auto m = std::make_unique<flint_gpt2>();
         m->cfg = *config;
+        m->flash = fused;
         FLINT_TRY(plan(*m));
         m->host_loss.resize(m->rows);
         FLINT_TRY(allocate(*m));
@@ -729,6 +713,27 @@ FLINT_API flint_status flint_gpt2_create(const flint_gpt2_config* config, flint_
         return fail(FLINT_ERROR_CUDA, "%s: out of host memory", name);
     }
     return FLINT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+FLINT_API flint_status flint_gpt2_bytes(const flint_gpt2_config* config, size_t* bytes) {
+    return model_bytes("flint_gpt2_bytes", config, false, bytes);
+}
+
+FLINT_API flint_status flint_gpt2_bytes_fused(const flint_gpt2_config* config, size_t* bytes) {
+    return model_bytes("flint_gpt2_bytes_fused", config, true, bytes);
+}
+
+FLINT_API flint_status flint_gpt2_create(const flint_gpt2_config* config, flint_gpt2** model) {
+    return create_model("flint_gpt2_create", config, false, model);
+}
+
+FLINT_API flint_status flint_gpt2_create_fused(const flint_gpt2_config* config,
+                                               flint_gpt2** model) {
+    return create_model("flint_gpt2_create_fused", config, true, model);
 }
 
 FLINT_API void flint_gpt2_destroy(flint_gpt2* model) { delete model; }

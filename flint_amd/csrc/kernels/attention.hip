@@ -39,6 +39,7 @@
 #include <type_traits>
 
 #include "common/common.h"
+#include "common/tuning.h"
 #include "kernels/gemm_common.h"
 #include "kernels/kernels.h"
 
@@ -618,11 +619,10 @@ attn_backward_dkdv(_Float16* __restrict__ dk, _Float16* __restrict__ dv, const _
 
 // Heads divide the batches, every stride holds a 64-half row, and buffer
 // offsets (32-bit bytes) reach every row.
-// work_rank's run: the CU count; FLINT_ATTN_ORDER=0 keeps plain
+// work_rank's run: the CU count; the "attn_order" override "0" keeps plain
 // longest-first order (A/B runs).
 int order_round() {
-    const char* e = std::getenv("FLINT_ATTN_ORDER");
-    if (e != nullptr && e[0] == '0' && e[1] == '\0') return 0;
+    if (tuning_off(Tune::kAttnOrder)) return 0;
     int cus = 0;
     if (device_cus(&cus) != hipSuccess || cus <= 0) return 0;
     return cus;

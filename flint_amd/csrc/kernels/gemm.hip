@@ -38,6 +38,7 @@
 #include <cstdlib>
 
 #include "common/common.h"
+#include "common/tuning.h"
 #include "kernels/kernels.h"
 #include "kernels/gemm_common.h"
 #include "kernels/split_sum.h"
@@ -649,11 +650,11 @@ int occupancy(const Config& c) {
     return 1;
 }
 
-// FLINT_GEMM_CONFIG="bm,bn,bk,stages,waves_m[,waves]" forces one of the instantiated
-// configurations (for tuning sweeps; read on every call so a sweep can change
-// it in-process); unset or unknown, the cost model below picks.
+// The "gemm_config" override, "bm,bn,bk,stages,waves_m[,waves]", forces one of
+// the instantiated configurations (tuning sweeps); unset or unknown, the cost
+// model below picks.
 bool forced_config(Config* out) {
-    const char* e = std::getenv("FLINT_GEMM_CONFIG");
+    const char* e = tuning(Tune::kGemmConfig);
     if (e == nullptr) return false;
     Config c{};
     c.waves = 4;
@@ -757,14 +758,14 @@ hipError_t run(Operands op, size_t slices, int split_len, hipStream_t stream) {
     ta.tiles_per_slice = ta.tiles_m * ta.tiles_n;
     ta.slices = int(slices);
     ta.group_m = 8;
-    if (const char* e = std::getenv("FLINT_GEMM_GROUP_M")) ta.group_m = std::max(1, std::atoi(e));
+    if (const char* e = tuning(Tune::kGemmGroupM)) ta.group_m = std::max(1, std::atoi(e));
     ta.split_len = split_len;
     // Persistent workgroups: as many as fit on the GPU at once (a multiple of
     // 8, so a workgroup keeps its XCD's share of the tiles), each walking ids
     // blockIdx.x, + gridDim.x, ...
     const size_t total = size_t(ta.tiles_per_slice) * slices;
     size_t slots = size_t(cus) * size_t(occupancy(c));
-    if (const char* e = std::getenv("FLINT_GEMM_SLOTS")) slots = std::max(1, std::atoi(e));
+    if (const char* e = tuning(Tune::kGemmSlots)) slots = std::max(1, std::atoi(e));
     size_t gx = std::min(total, slots);
     if (gx >= 8) gx -= gx % 8;
     const dim3 grid(static_cast<unsigned>(gx), 1, 1);
@@ -834,8 +835,6 @@ hipError_t gemm_tn_workspace(size_t m, size_t n, size_t k, size_t* bytes) {
 
 hipError_t launch_gemm_nt(void* y, const void* x, const void* w, const void* bias, void* aux,
                           Epilogue e, size_t m, size_t n, size_t k, hipStream_t stream) {
-    if (gemm_pp_eligible(e, m, n, k))
-        return launch_gemm_pp(e, y, x, w, bias, aux, m, n, k, stream);
     if (gemm_pipe_eligible(GemmLayout::kNT, e, m, n, k))
         return launch_gemm_pipe(GemmLayout::kNT, e, y, x, w, bias, aux, 1.0f, 1, m, n, k, false,
                                 nullptr, 0, stream);

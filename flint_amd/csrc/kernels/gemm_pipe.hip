@@ -56,6 +56,7 @@
 #include <type_traits>
 
 #include "common/common.h"
+#include "common/tuning.h"
 #include "kernels/gemm_common.h"
 #include "kernels/kernels.h"
 
@@ -375,21 +376,42 @@ gemm_pipe(Operands op, TileArgs ta) {
     // The issue side walks one stream of k-steps over all of the workgroup's
     // tiles, S steps ahead of the MFMAs; past the last one it reloads the last
     // step (into a stage nobody reads), so every wait counts the same loads.
+    // A raw buffer's range check covers the vector offset, not the scalar one.
+    // Row-major operands put the k-step in the scalar offset: it stays inside
+    // the row, and the check on the row's vector offset masks rows past the
+    // tile's last valid one. k-major operands instead get a resource based at
+    // the step's first k row and ending at the operand's end, so that at the
+    // last rows a chunk past the last column reads 0 rather than the memory
+    // after the operand.
     struct Issue {
         int tile, k0, k_end, st;
+        const _Float16 *a, *b;
+        unsigned a_bytes, b_bytes;
         __amdgpu_buffer_rsrc_t ra, rb;
+    };
+    auto make_rsrcs = [&](Issue& is) {
+        const unsigned ka = kXM ? unsigned(is.k0) * unsigned(a_ld) : 0u;
+        const unsigned kb = kWM ? unsigned(is.k0) * unsigned(b_ld) : 0u;
+        is.ra = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(is.a + ka), 0, is.a_bytes - 2u * ka,
+                                                  0x00020000);
+        is.rb = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(is.b + kb), 0, is.b_bytes - 2u * kb,
+                                                  0x00020000);
     };
     auto rsrc_of = [&](Issue& is) {
         const Tile t = tile(is.tile);
         is.k0 = t.k_begin;
         is.k_end = t.k_end;
-        is.ra = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(t.a), 0, t.a_bytes, 0x00020000);
-        is.rb = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(t.b), 0, t.b_bytes, 0x00020000);
+        is.a = t.a;
+        is.b = t.b;
+        is.a_bytes = t.a_bytes;
+        is.b_bytes = t.b_bytes;
+        make_rsrcs(is);
     };
     auto advance = [&](Issue& is) {
         is.st = is.st + 1 == S ? 0 : is.st + 1;
         if (is.k0 + BK < is.k_end) {
             is.k0 += BK;
+            if constexpr (kXM || kWM) make_rsrcs(is);
         } else if (is.tile + 1 < n_tiles) {
             ++is.tile;
             rsrc_of(is);
@@ -399,8 +421,9 @@ gemm_pipe(Operands op, TileArgs ta) {
         const bool xq = q < IA;
         const int u = (xq ? q : q - IA) * 4 + wave;
         lds_half* dst = (lds_half*)(stage(is.st) + (xq ? 0 : BM * BK) + u * 512);
-        // Row-major: k0 halves into every row. k-major: k0 rows down.
-        const unsigned soff = unsigned(is.k0) * 2u * unsigned(xq ? (kXM ? a_ld : 1) : (kWM ? b_ld : 1));
+        // Row-major: k0 halves into every row. k-major: in the resource's base.
+        const bool kmajor = xq ? kXM : kWM;
+        const unsigned soff = kmajor ? 0u : unsigned(is.k0) * 2u;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xq ? is.ra : is.rb,
                                                  (__attribute__((address_space(3))) void*)dst, 16,
                                                  voff[q], soff, 0, 0);
@@ -519,13 +542,16 @@ gemm_pipe(Operands op, TileArgs ta) {
                                 wave * 256;
         if constexpr (kBiasLds) {
             // One load puts columns col0 .. col0 + 255 of the bias in this
-            // wave's 1 KB block (those past n read 0); the epilogue reads them
-            // back once the k-loop's waits have retired it.
+            // wave's 1 KB block; the epilogue reads them back once the
+            // k-loop's waits have retired it. The column goes in the lane's
+            // vector offset, not the scalar one: a raw buffer's range check
+            // covers the vector offset only, and it is what makes the lanes
+            // past n read 0 instead of the memory after the bias.
             const auto rbias = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float*>(op.bias), 0, unsigned(n) * 4u, 0x00020000);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rbias, (__attribute__((address_space(3))) void*)(lds_half*)bias_lds, 16,
-                unsigned(lane) * 16u, unsigned(t.n0 + wn * WTN) * 4u, 0, 0);
+                unsigned(t.n0 + wn * WTN) * 4u + unsigned(lane) * 16u, 0, 0, 0);
         } else if constexpr (kBias) {
             const auto rbias = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float*>(op.bias), 0, unsigned(n) * 4u, 0x00020000);
@@ -849,12 +875,12 @@ constexpr PipeConfig kPipeConfigs[] = {
     {256, 256, 3, 32}, {256, 192, 4, 32}, {128, 192, 4, 32}, {256, 64, 4, 32},
     {128, 192, 3, 64}, {256, 128, 3, 64}, {256, 256, 2, 64}, {256, 192, 2, 64}};
 
-// FLINT_GEMM_PIPE: "0" routes every call to gemm.hip's kernels;
-// "bm,bn,stages[,bk]" forces one of kPipeConfigs (tuning sweeps and tests;
-// read per call; bk defaults to 32).
+// The "gemm_pipe" override: "0" routes every call to gemm.hip's kernels;
+// "bm,bn,stages[,bk]" forces one of kPipeConfigs (tests and tuning sweeps;
+// bk defaults to 32).
 bool pipe_forced(PipeConfig* out, bool* disabled) {
     *disabled = false;
-    const char* e = std::getenv("FLINT_GEMM_PIPE");
+    const char* e = tuning(Tune::kGemmPipe);
     if (e == nullptr) return false;
     if (e[0] == '0' && e[1] == '\0') {
         *disabled = true;

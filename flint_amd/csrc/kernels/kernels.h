@@ -45,12 +45,6 @@ hipError_t launch_gemm_pipe(GemmLayout l, Epilogue e, void* y, const void* x, co
                             const void* bias, void* aux, float scale, size_t slices, size_t m,
                             size_t n, size_t k, bool accumulate, void* partials, int split_len,
                             hipStream_t stream, bool causal = false);
-// The eight-wave ping-pong NT GEMM (gemm_pp.hip), for k % 64 == 0 and
-// n % 8 == 0; taken only when FLINT_GEMM_PP="bm,bn" forces a tile (it is
-// slower than the pipeline at the GPT-2 shapes).
-bool gemm_pp_eligible(Epilogue e, size_t m, size_t n, size_t k);
-hipError_t launch_gemm_pp(Epilogue e, void* y, const void* x, const void* w, const void* bias,
-                          void* aux, size_t m, size_t n, size_t k, hipStream_t stream);
 hipError_t launch_gemm_nn(void* y, const void* x, const void* w, const void* aux, Epilogue e,
                           size_t m, size_t n, size_t k, hipStream_t stream);
 // Number of k splits TN uses for m x n x k on this device (1 = none).

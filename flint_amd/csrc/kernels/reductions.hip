@@ -24,6 +24,7 @@
 #include <mutex>
 
 #include "common/common.h"
+#include "common/tuning.h"
 #include "kernels/kernels.h"
 #include "kernels/reduce_common.h"
 #include "kernels/split_sum.h"
@@ -404,9 +405,10 @@ column_partials2(float* part0, float* part1, const _Float16* __restrict__ dy,
 hipError_t launch_partials(float* partial, const void* dy, size_t rows, size_t cols,
                            hipStream_t stream) {
     const size_t chunks = (rows + kChunkRows - 1) / kChunkRows;
-    // FLINT_PARTIALS_CPL=1|2|4 forces the columns per lane (tuning sweeps).
+    // The "partials_cpl" override, 1 | 2 | 4, forces the columns per lane
+    // (tuning sweeps).
     int cpl = 1;
-    if (const char* e = std::getenv("FLINT_PARTIALS_CPL")) {
+    if (const char* e = tuning(Tune::kPartialsCpl)) {
         const int v = std::atoi(e);
         cpl = v == 2 || v == 4 ? v : 1;
     }
@@ -1020,10 +1022,9 @@ hipError_t launch_layernorm_backward(void* dx, void* dgamma, void* dbeta, const 
     const int acc = accumulate_dx ? 1 : 0;
     auto* dxh = static_cast<_Float16*>(dx_half);
     const size_t pieces = cols / 8;
-    // One launch for the partials and dx, then the merge (FLINT_LN_FUSED=0:
+    // One launch for the partials and dx, then the merge ("ln_fused" = "0":
     // the partials, then dx with the merge; the same bits).
-    const char* fe = std::getenv("FLINT_LN_FUSED");
-    const bool fused = pieces <= 256 && !(fe != nullptr && fe[0] == '0' && fe[1] == '\0');
+    const bool fused = pieces <= 256 && !tuning_off(Tune::kLnFused);
     if (fused) {
         const size_t units = std::min<size_t>(items, 1u << 20);
         const size_t row_blocks = std::min<size_t>((rows + 15) / 16, kMaxBlocks);
@@ -1099,12 +1100,13 @@ hipError_t launch_softmax_cross_entropy(void* dlogits, void* row_loss, const voi
     auto* l = static_cast<float*>(row_loss);
     const auto* lg = static_cast<const h8*>(logits);
     const auto* tg = static_cast<const uint16_t*>(targets);
-    // FLINT_CE_THREADS=256|512|1024 forces the workgroup size (tuning sweeps);
+    // The "ce_threads" override, 256 | 512 | 1024, forces the workgroup size
+    // (tuning sweeps);
     // the chunks per thread follow from it.
     // 256 threads while a row fits 25 chunks a thread (GPT-2's 50,257: 305.9
     // to 307.8 us against 309.8 to 309.9 at 512, two runs, the same bits).
     int threads = vc <= 256 * 25 ? 256 : 512;
-    if (const char* e = std::getenv("FLINT_CE_THREADS")) {
+    if (const char* e = tuning(Tune::kCeThreads)) {
         const int t = std::atoi(e);
         if (t == 256 || t == 512 || t == 1024) threads = t;
     }

@@ -9,6 +9,7 @@
 #include <cstdlib>
 
 #include "common/common.h"
+#include "common/tuning.h"
 #include "kernels/kernels.h"
 #include "kernels/reduce_common.h"
 
@@ -655,11 +656,10 @@ hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, con
     // into the sorted buffers; in one workgroup's LDS when the rows fit.
     const size_t cols = length * width;   // dwpe: column sums of dx as sequences x cols
     // With one chunk of sequences the position gradient rides in the sort's
-    // launch (FLINT_EMB_TOGETHER=0: its own launch after the token rows).
-    const char* te = std::getenv("FLINT_EMB_TOGETHER");
+    // launch ("emb_together" = "0": its own launch after the token rows).
     const bool together = rows <= size_t(kBlockSortRows) && sequences <= 256 &&
                           (cols / 4 + 1023) / 1024 < (size_t{1} << 30) &&
-                          !(te != nullptr && te[0] == '0' && te[1] == '\0');
+                          !tuning_off(Tune::kEmbTogether);
     if (together) {
         hipLaunchKernelGGL(sort_tokens_and_positions, dim3(unsigned(1 + (cols / 4 + 1023) / 1024)),
                            dim3(1024), 0, stream, sorted_tokens, sorted_rows, tok, int(rows),

@@ -21,6 +21,7 @@ HEADER = ROOT / "include" / "flint" / "flint.h"
 TRAIN_HEADER = ROOT / "include" / "flint" / "flint_train.h"
 NOALLOC_HEADER = ROOT / "include" / "flint" / "flint_noalloc.h"
 ATTENTION_HEADER = ROOT / "include" / "flint" / "flint_attention.h"
+TUNING_HEADER = ROOT / "include" / "flint" / "flint_tuning.h"
 LIBRARY = ROOT / "build" / "release" / "bin" / "libflint.so"
 
 OK = 0
@@ -95,6 +96,10 @@ SIGNATURES = {
     "flint_attention_forward": (I, [P, P, P, P, P, Z, Z, Z, F, P]),
     "flint_attention_backward_workspace": (I, [Z, Z, Z, ctypes.POINTER(Z)]),
     "flint_attention_backward": (I, [P, P, P, P, P, P, P, P, P, Z, Z, Z, F, P, Z, P]),
+    "flint_gpt2_bytes_fused": (I, [ctypes.POINTER(Gpt2Config), ctypes.POINTER(Z)]),
+    "flint_gpt2_create_fused": (I, [ctypes.POINTER(Gpt2Config), ctypes.POINTER(P)]),
+    # flint_tuning.h (no counterpart in the reference)
+    "flint_set_tuning": (I, [ctypes.c_char_p, ctypes.c_char_p]),
     "flint_gemm_nt_batched": (I, [P, P, P, Z, Z, Z, Z, F, P]),
     "flint_gemm_nn_batched": (I, [P, P, P, Z, Z, Z, Z, P]),
     "flint_gemm_tn_batched": (I, [P, P, P, Z, Z, Z, Z, P]),
@@ -186,6 +191,28 @@ class Flint:
             raise FlintError(status, f"{message}: {detail}" if detail else message)
 
     # -- GEMMs ----------------------------------------------------------------
+    def set_tuning(self, name, value):
+        """Forces (value a string) or clears (None) one plan override."""
+        self.check(self.lib.flint_set_tuning(
+            name.encode(), None if value is None else str(value).encode()))
+
+    def tuned(self, **overrides):
+        """A context in which the given plan overrides hold; each is cleared on
+        exit (the library starts with none set)."""
+        import contextlib
+
+        @contextlib.contextmanager
+        def scope():
+            try:
+                for name, value in overrides.items():
+                    self.set_tuning(name, value)
+                yield self
+            finally:
+                for name in overrides:
+                    self.set_tuning(name, None)
+
+        return scope()
+
     def copy(self, dst, src, nbytes, stream=None):
         self.check(self.lib.flint_copy(pointer(dst), pointer(src), nbytes, stream_handle(stream)))
 
@@ -417,17 +444,19 @@ class Flint:
 class Gpt2:
     """A flint_gpt2 model through the C ABI (ref tests/flint_lib.py's Gpt2 helper):
     parameters and gradients are (name, device address, rows, cols) and move in
-    and out of torch tensors with flint_copy."""
+    and out of torch tensors with flint_copy. fused=True creates the model with
+    the fused attention (flint_gpt2_create_fused, flint_attention.h)."""
 
     def __init__(self, flint, layers, heads, width, block_size, vocab, padded_vocab, sequences,
-                 length, separate_buffers=False, backward=True):
+                 length, separate_buffers=False, backward=True, fused=False):
         self.flint = flint
+        self.fused = bool(fused)
         self.config = Gpt2Config(layers, heads, width, block_size, vocab, padded_vocab,
                                  sequences, length, int(bool(separate_buffers)),
                                  int(bool(backward)))
         self.handle = P()
-        flint.check(flint.lib.flint_gpt2_create(ctypes.byref(self.config),
-                                                ctypes.byref(self.handle)))
+        create = flint.lib.flint_gpt2_create_fused if self.fused else flint.lib.flint_gpt2_create
+        flint.check(create(ctypes.byref(self.config), ctypes.byref(self.handle)))
 
     def close(self):
         if self.handle:
@@ -442,8 +471,8 @@ class Gpt2:
 
     def bytes(self):
         out = Z(0)
-        self.flint.check(self.flint.lib.flint_gpt2_bytes(ctypes.byref(self.config),
-                                                         ctypes.byref(out)))
+        fn = self.flint.lib.flint_gpt2_bytes_fused if self.fused else self.flint.lib.flint_gpt2_bytes
+        self.flint.check(fn(ctypes.byref(self.config), ctypes.byref(out)))
         return out.value
 
     def _infos(self, fn):
@@ -505,6 +534,6 @@ def declared_functions(header=None):
     import re
 
     headers = ([header] if header is not None
-               else [HEADER, TRAIN_HEADER, NOALLOC_HEADER, ATTENTION_HEADER])
+               else [HEADER, TRAIN_HEADER, NOALLOC_HEADER, ATTENTION_HEADER, TUNING_HEADER])
     text = "".join(Path(h).read_text() for h in headers)
     return re.findall(r"FLINT_API\s+[^;(]*?\b(flint_\w+)\s*\(", text)

@@ -51,10 +51,11 @@ FLINT_API const char* flint_status_string(flint_status status);
  * A successful call does not clear it (ref flint.h:42). */
 FLINT_API const char* flint_last_error(void);
 
-/* A HIP stream handle (hipStream_t is struct ihipStream_t*). The reference names
- * the CUDA stream type here (ref flint.h:46); both are one opaque pointer, so the
- * ABI is the same. */
-typedef struct ihipStream_t* flint_stream;
+/* The stream type keeps the reference's declaration (ref flint.h:46) so that
+ * code compiled against either header agrees on it. On this library the value
+ * is a hipStream_t (struct ihipStream_t*): one opaque pointer either way, passed
+ * as it is; HIP callers cast their stream to flint_stream. */
+typedef struct CUstream_st* flint_stream;
 
 /* Device-to-device byte copy; ranges must not overlap (ref flint.h:51). */
 FLINT_API flint_status flint_copy(void* dst, const void* src, size_t bytes, flint_stream stream);

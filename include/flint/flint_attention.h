@@ -43,6 +43,21 @@ FLINT_API flint_status flint_attention_backward(void* dq, void* dk, void* dv, co
                                                 void* workspace, size_t workspace_bytes,
                                                 flint_stream stream);
 
+/* The GPT-2 model with the fused attention in each block's place of the
+ * reference's stored scores and probabilities (flint_heads_split, the batched
+ * products, flint_causal_softmax_* and flint_heads_merge): the kernels above
+ * read each head's q, k and v rows inside the qkv projection and write their
+ * output rows into the attention projection's input, so a block keeps the
+ * projection and the log-sum-exp instead of q, k, v and the probabilities.
+ * Everything else is flint_gpt2_bytes / flint_gpt2_create's model, and every
+ * other flint_gpt2_* function takes it. The results pass the same accuracy
+ * bounds but differ in the last bits from the stored-probability model, which
+ * is the one equal to the public kernels called one by one. The head width
+ * (width / heads) must be 64. */
+FLINT_API flint_status flint_gpt2_bytes_fused(const flint_gpt2_config* config, size_t* bytes);
+FLINT_API flint_status flint_gpt2_create_fused(const flint_gpt2_config* config,
+                                               flint_gpt2** model);
+
 #ifdef __cplusplus
 }
 #endif

@@ -28,3 +28,19 @@ def cuda():
 
     assert torch.cuda.is_available(), "GPU test run without a HIP device"
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def tune(flint):
+    """tune(name, value) sets one plan override (flint_set_tuning) for this
+    test; value None clears it. Every override the test set is cleared after
+    it, so later tests run the default plans."""
+    names = set()
+
+    def set_(name, value):
+        flint.set_tuning(name, value)
+        names.add(name)
+
+    yield set_
+    for name in names:
+        flint.set_tuning(name, None)

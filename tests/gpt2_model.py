@@ -79,7 +79,7 @@ def forward(params, idx, targets, cfg, fp16=False):
     seqs, length = idx.shape
     hd = width // heads
     x = params["wte.weight"][idx] + params["wpe.weight"][:length]
-    mask = torch.triu(torch.ones(length, length, dtype=torch.bool), 1)
+    mask = torch.triu(torch.ones(length, length, dtype=torch.bool, device=x.device), 1)
     for i in range(layers):
         p = f"blocks.{i}."
         h = _layer_norm(x, params[p + "ln_1.weight"], params[p + "ln_1.bias"], fp16)
@@ -87,7 +87,7 @@ def forward(params, idx, targets, cfg, fp16=False):
                          fp16), fp16)
         q, k, v = qkv.split(width, dim=-1)
         q, k, v = (t.reshape(seqs, length, heads, hd).transpose(1, 2) for t in (q, k, v))
-        s = _h((q @ k.transpose(-1, -2)) / math.sqrt(hd), fp16)
+        s = _h((q @ k.transpose(-1, -2).contiguous()) / math.sqrt(hd), fp16)
         a = _h(torch.softmax(s.masked_fill(mask, float("-inf")), dim=-1), fp16)
         o = _h(a @ v, fp16).transpose(1, 2).reshape(seqs, length, width)
         x = x + _linear(o, params[p + "attn.c_proj.weight"], params[p + "attn.c_proj.bias"],

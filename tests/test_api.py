@@ -18,8 +18,13 @@ def test_header_matches_signatures():
     assert len(flint_lib.declared_functions(flint_lib.TRAIN_HEADER)) == 4
     # flint_noalloc.h: one entry point for callers that cannot allocate.
     assert flint_lib.declared_functions(flint_lib.NOALLOC_HEADER) == ["flint_bias_gradient_noalloc"]
-    # flint_attention.h: the fused causal attention, additive.
-    assert len(flint_lib.declared_functions(flint_lib.ATTENTION_HEADER)) == 3
+    # flint_attention.h: the fused causal attention and the model built on it,
+    # additive.
+    assert flint_lib.declared_functions(flint_lib.ATTENTION_HEADER) == [
+        "flint_attention_forward", "flint_attention_backward_workspace",
+        "flint_attention_backward", "flint_gpt2_bytes_fused", "flint_gpt2_create_fused"]
+    # flint_tuning.h: the plan overrides for tests and sweeps.
+    assert flint_lib.declared_functions(flint_lib.TUNING_HEADER) == ["flint_set_tuning"]
     declared = flint_lib.declared_functions()
     assert sorted(declared) == sorted(flint_lib.SIGNATURES)
 
@@ -31,6 +36,21 @@ def test_library_exports_exactly_the_header(flint):
                          text=True, check=True).stdout
     exported = [line.split()[-1] for line in out.splitlines() if line.strip()]
     assert sorted(exported) == sorted(flint_lib.declared_functions())
+
+
+def test_tuning_names_are_checked_and_read_no_environment(flint):
+    # Unknown names fail with a message; known ones set and clear. The
+    # library's source reads no environment variable.
+    from pathlib import Path
+
+    assert flint.lib.flint_set_tuning(b"no_such_plan", b"1") == flint_lib.ERROR_INVALID_ARGUMENT
+    assert "no_such_plan" in flint.last_error()
+    assert flint.lib.flint_set_tuning(None, None) == flint_lib.ERROR_INVALID_ARGUMENT
+    with flint.tuned(gemm_pipe="0", ln_defer="0"):
+        pass
+    src = Path(flint_lib.ROOT) / "flint_amd" / "csrc"
+    for f in list(src.rglob("*.cpp")) + list(src.rglob("*.hip")) + list(src.rglob("*.h")):
+        assert "getenv" not in f.read_text(), f
 
 
 def test_links_only_the_hip_runtime(flint):

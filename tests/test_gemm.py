@@ -274,8 +274,8 @@ PIPE_SHAPES = [(300, 200, 64), (4315, 4600, 96), (1100, 968, 448)]
 @pytest.mark.parametrize("cfg", PIPE_CONFIGS)
 @pytest.mark.parametrize("m,n,k", PIPE_SHAPES)
 @pytest.mark.parametrize("epi", ["none", "bias", "gelu", "residual"])
-def test_nt_pipe_forced(flint, cuda, monkeypatch, cfg, m, n, k, epi):
-    monkeypatch.setenv("FLINT_GEMM_PIPE", cfg)
+def test_nt_pipe_forced(flint, cuda, tune, cfg, m, n, k, epi):
+    tune("gemm_pipe", cfg)
     x = uniform((m, k), 40)
     w = normal((n, k), 41, 0.05, torch.float16)
     b = normal((n,), 42, 0.02)
@@ -308,8 +308,8 @@ def test_nt_pipe_forced(flint, cuda, monkeypatch, cfg, m, n, k, epi):
 
 
 @pytest.mark.parametrize("cfg", PIPE_CONFIGS)
-def test_nt_batched_pipe_forced(flint, cuda, monkeypatch, cfg):
-    monkeypatch.setenv("FLINT_GEMM_PIPE", cfg)
+def test_nt_batched_pipe_forced(flint, cuda, tune, cfg):
+    tune("gemm_pipe", cfg)
     batches, m, n, k = 5, 264, 200, 64
     x = uniform((batches, m, k), 44)
     w = uniform((batches, n, k), 45)
@@ -325,8 +325,8 @@ def test_nt_batched_pipe_forced(flint, cuda, monkeypatch, cfg):
 # shorter than the stages, splits of TN (whose workspace plan is the ABI's).
 @pytest.mark.parametrize("cfg", PIPE_CONFIGS)
 @pytest.mark.parametrize("m,n,k", [(300, 200, 64), (1100, 1096, 320)])
-def test_nn_pipe_forced(flint, cuda, monkeypatch, cfg, m, n, k):
-    monkeypatch.setenv("FLINT_GEMM_PIPE", cfg)
+def test_nn_pipe_forced(flint, cuda, tune, cfg, m, n, k):
+    tune("gemm_pipe", cfg)
     x = uniform((m, k), 46)
     w = normal((k, n), 47, 0.05, torch.float16)
     y = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
@@ -345,8 +345,8 @@ def test_nn_pipe_forced(flint, cuda, monkeypatch, cfg, m, n, k):
 @pytest.mark.parametrize("cfg", PIPE_CONFIGS)
 @pytest.mark.parametrize("m,n,k", [(296, 200, 2048), (1032, 264, 4096), (768, 768, 8192)])
 @pytest.mark.parametrize("accumulate", [False, True])
-def test_tn_pipe_forced(flint, cuda, monkeypatch, cfg, m, n, k, accumulate):
-    monkeypatch.setenv("FLINT_GEMM_PIPE", cfg)
+def test_tn_pipe_forced(flint, cuda, tune, cfg, m, n, k, accumulate):
+    tune("gemm_pipe", cfg)
     x = normal((k, m), 49, 1e-2, torch.float16)
     w = uniform((k, n), 50)
     y0 = normal((m, n), 51)
@@ -363,8 +363,8 @@ def test_tn_pipe_forced(flint, cuda, monkeypatch, cfg, m, n, k, accumulate):
 
 
 @pytest.mark.parametrize("cfg", PIPE_CONFIGS)
-def test_batched_nn_tn_pipe_forced(flint, cuda, monkeypatch, cfg):
-    monkeypatch.setenv("FLINT_GEMM_PIPE", cfg)
+def test_batched_nn_tn_pipe_forced(flint, cuda, tune, cfg):
+    tune("gemm_pipe", cfg)
     batches, m, n, k = 5, 264, 72, 96
     x = uniform((batches, m, k), 52)
     w = uniform((batches, k, n), 53)
@@ -454,9 +454,9 @@ GUARD_CASES = ["nt", "nt_bias", "nt_bias_gelu", "nt_bias_residual", "nn", "nn_dg
 @pytest.mark.parametrize("force", [None, "128,192,3,64", "256,128,3,64", "256,256,3", "256,64,4"])
 @pytest.mark.parametrize("offset", [16, 32, 48])
 @pytest.mark.parametrize("case", GUARD_CASES)
-def test_outputs_stay_inside_their_buffers(flint, cuda, monkeypatch, case, offset, force):
+def test_outputs_stay_inside_their_buffers(flint, cuda, tune, case, offset, force):
     if force is not None:
-        monkeypatch.setenv("FLINT_GEMM_PIPE", force)
+        tune("gemm_pipe", force)
     m, n, k = (264, 200, 96) if not case.startswith("tn") else (264, 200, 1000)
     x = uniform((m, k) if not case.startswith("tn") else (k, m), 50).to(cuda)
     w_shape = (n, k) if case.startswith("nt") else (k, n)
@@ -528,49 +528,6 @@ def test_gemm_is_ordered_on_the_given_stream(flint, cuda, case, side):
             flint.gemm_tn(y, x, w, m, n, k, stream=stream)
     stream.synchronize()
     assert bool((y.float() == k).all())
-
-
-# The eight-wave ping-pong NT kernel (gemm_pp.hip), each tile forced: edge
-# tiles on both sides, more tiles than CUs (so persistent workgroups run two
-# or three tiles and the k-step stream crosses tile boundaries), and a GPT-2
-# depth. Outputs start as NaN so a missed store shows.
-PP_SHAPES = [(264, 200, 128), (8408, 2040, 128), (1000, 3072, 768)]
-
-
-@pytest.mark.parametrize("m,n,k", PP_SHAPES)
-@pytest.mark.parametrize("epilogue", ["none", "bias", "bias_gelu", "bias_residual"])
-@pytest.mark.parametrize("force", ["256,256", "256,192", "256,128"])
-def test_nt_pingpong_forced(flint, cuda, monkeypatch, force, epilogue, m, n, k):
-    if force == "256,256" and epilogue != "none":
-        pytest.skip("256 x 256 serves the plain product only")
-    monkeypatch.setenv("FLINT_GEMM_PP", force)
-    x = uniform((m, k), 70)
-    w = normal((n, k), 71, 0.05, torch.float16)
-    b = normal((n,), 72, 0.02)
-    ref = ref_nt(x, w)
-    xd, wd, bd = x.to(cuda), w.to(cuda), b.to(cuda)
-    if epilogue == "bias_residual":
-        r = normal((m, n), 73)
-        y = torch.full((m, n), float("nan"), device=cuda)
-        flint.gemm_nt_bias_residual(y, xd, wd, bd, r.to(cuda), m, n, k)
-        ref = r + (ref + b)
-    else:
-        y = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
-        if epilogue == "none":
-            flint.gemm_nt(y, xd, wd, m, n, k)
-        elif epilogue == "bias":
-            flint.gemm_nt_bias(y, xd, wd, bd, m, n, k)
-            ref = ref + b
-        else:
-            pre = torch.full((m, n), float("nan"), dtype=torch.float16, device=cuda)
-            flint.gemm_nt_bias_gelu(y, pre, xd, wd, bd, m, n, k)
-            torch.cuda.synchronize()
-            assert rel_err(pre.cpu(), ref + b) <= TOL
-            ref = torch.nn.functional.gelu((ref + b).double(), approximate="tanh")
-    torch.cuda.synchronize()
-    got = y.cpu()
-    assert bool(torch.isfinite(got).all())
-    assert rel_err(got, ref) <= TOL
 
 
 # ---- exact-rounding contracts of the GELU and dGELU epilogues
@@ -688,3 +645,58 @@ def test_dgelu_epilogue_over_every_finite_fp16_pre(flint, cuda):
     assert safe.mean() > 0.95
     wrong = safe & (_ordered(y) != _ordered(exact))
     assert not wrong.any(), int(wrong.sum())
+
+
+# ---- Reads stay inside the operands ------------------------------------------
+# Each operand below ends at the last byte of a device allocation of its own
+# (a fresh segment of whole 2 MiB pieces: torch's caching allocator hands
+# such a request its own hipMalloc when nothing cached fits), so a load past
+# its end would leave the allocation. Buffer range checks cover the vector
+# offset only; these cases are the ones whose tiles run past an operand's
+# end: the bias of an edge column tile (read 256 columns a wave into LDS),
+# and a k-major operand's last k rows at an edge tile (NN's w, TN's x and w).
+
+
+def _at_allocation_end(t):
+    """A device copy of t whose last byte ends its allocation."""
+    nbytes = t.numel() * t.element_size()
+    piece = 2 << 20
+    total = (nbytes + piece - 1) // piece * piece + piece
+    torch.cuda.empty_cache()
+    buf = torch.empty(total, dtype=torch.uint8, device="cuda")
+    out = buf[total - nbytes:].view(t.dtype).view(t.shape)
+    out.copy_(t.to("cuda"))
+    return out
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 3072, 768), (300, 2312, 128), (256, 200, 64)])
+def test_bias_ending_at_its_allocation(flint, cuda, m, n, k):
+    x = uniform((m, k), 90)
+    w = normal((n, k), 91, 0.02, torch.float16)
+    b = normal((n,), 92, 0.02)
+    bd = _at_allocation_end(b)
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    pre = torch.empty_like(y)
+    flint.gemm_nt_bias_gelu(y, pre, x.to(cuda), w.to(cuda), bd, m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(pre.cpu(), ref_nt(x, w) + b) <= TOL
+    flint.gemm_nt_bias(y, x.to(cuda), w.to(cuda), bd, m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu(), ref_nt(x, w) + b) <= TOL
+
+
+@pytest.mark.parametrize("m,n,k", [(200, 136, 512), (520, 200, 256)])
+def test_k_major_operands_ending_at_their_allocation(flint, cuda, m, n, k):
+    # NN: w is k x n (k-major); TN: x is k x m and w is k x n.
+    x_nn = uniform((m, k), 93)
+    w_nn = uniform((k, n), 94)
+    y = torch.empty((m, n), dtype=torch.float16, device=cuda)
+    flint.gemm_nn(y, x_nn.to(cuda), _at_allocation_end(w_nn), m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu(), ref_nn(x_nn, w_nn)) <= TOL
+    x_tn = uniform((k, m), 95)
+    w_tn = uniform((k, n), 96)
+    yt = torch.empty((m, n), dtype=torch.float32, device=cuda)
+    flint.gemm_tn(yt, _at_allocation_end(x_tn), _at_allocation_end(w_tn), m, n, k)
+    torch.cuda.synchronize()
+    assert rel_err(yt.cpu(), ref_tn(x_tn, w_tn)) <= 1e-4

@@ -45,9 +45,9 @@ def _gate(name, got, ref, peer, factor, floor):
         assert e_got <= bound, f"{name}: {measure.__name__} {e_got:.3e} > {bound:.3e}"
 
 
-def _make(flint, cfg, sequences, length, separate=False, backward=True):
+def _make(flint, cfg, sequences, length, separate=False, backward=True, fused=False):
     return Gpt2(flint, cfg["layers"], cfg["heads"], cfg["width"], cfg["block_size"],
-                cfg["vocab"], cfg["padded_vocab"], sequences, length, separate, backward)
+                cfg["vocab"], cfg["padded_vocab"], sequences, length, separate, backward, fused)
 
 
 def _load(model, params):
@@ -69,9 +69,9 @@ def _dev16(t):
     return t.to(torch.int32).to(torch.int16).reshape(-1).cuda()
 
 
-def _run(flint, cfg, sequences, length, params, idx, tgt, scale, separate=False):
+def _run(flint, cfg, sequences, length, params, idx, tgt, scale, separate=False, fused=False):
     """(logits, row_loss, dlogits, grads, mean_loss) from the library, on the CPU."""
-    with _make(flint, cfg, sequences, length, separate) as model:
+    with _make(flint, cfg, sequences, length, separate, fused=fused) as model:
         _load(model, params)
         tok, trg = _dev16(idx), _dev16(tgt)
         model.forward(tok, trg, scale)
@@ -89,9 +89,21 @@ def _run(flint, cfg, sequences, length, params, idx, tgt, scale, separate=False)
     return logits, row_loss, dlogits, grads, mean
 
 
-def _gate_case(flint, cfg, sequences, length, trained, idx=None, tgt=None):
+def _reference(params, idx, tgt, cfg, scale, fp16, device):
+    """G.gradients on `device` (FP32 arithmetic either way), returned on the CPU."""
+    if device == "cpu":
+        return G.gradients(params, idx, tgt, cfg, scale, fp16=fp16)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = {n: t.to(device) for n, t in params.items()}
+    out = G.gradients(dev, idx.to(device), tgt.to(device), cfg, scale, fp16=fp16)
+    return (out[0].cpu(), out[1].cpu(), out[2].cpu(), {n: g.cpu() for n, g in out[3].items()})
+
+
+def _gate_case(flint, cfg, sequences, length, trained, idx=None, tgt=None, fused=False,
+               ref_device="cpu"):
     """The whole-model gate (forward outputs and every gradient) for one
-    configuration and batch."""
+    configuration and batch. ref_device "cuda" computes the FP32 reference and
+    the FP16 peer with torch on the GPU (the sizes of configs[4]'s batch)."""
     shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
                                 cfg["padded_vocab"])
     params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=5, trained=trained)
@@ -101,10 +113,10 @@ def _gate_case(flint, cfg, sequences, length, trained, idx=None, tgt=None):
         idx, tgt = _tokens(cfg, sequences, length, 6)
     rows = sequences * length
     scale = 1024.0 / rows
-    ref = G.gradients(params, idx, tgt, cfg, scale)
-    peer = G.gradients(params, idx, tgt, cfg, scale, fp16=True)
+    ref = _reference(params, idx, tgt, cfg, scale, False, ref_device)
+    peer = _reference(params, idx, tgt, cfg, scale, True, ref_device)
     logits, row_loss, dlogits, grads, mean = _run(flint, cfg, sequences, length, params, idx,
-                                                  tgt, scale)
+                                                  tgt, scale, fused=fused)
     v = cfg["vocab"]
     _gate("logits", logits[:, :v], ref[0], peer[0], 2.0, 1e-3)
     _gate("row_loss", row_loss, ref[1], peer[1], 2.0, 1e-4)
@@ -128,21 +140,20 @@ def test_forward_and_backward_pass_the_gate(flint, cuda, cfg, sequences, length,
     _gate_case(flint, cfg, sequences, length, trained)
 
 
-# Head width 64: the model runs the fused causal attention (flint_attention_*);
-# FLINT_FLASH=0 runs the stored scores and probabilities instead. Both pass the
-# gate; the fused path keeps scores and probabilities in FP32 longer, so its
-# forward error is no larger.
+# Head width 64: flint_gpt2_create (the reference's stored scores and
+# probabilities) and flint_gpt2_create_fused (the fused causal attention of
+# flint_attention.h) both pass the gate; the fused path keeps scores and
+# probabilities in FP32 longer, so its forward error is no larger.
 HEAD64 = dict(layers=2, heads=2, width=128, block_size=128, vocab=1000, padded_vocab=1024)
 
 
-@pytest.mark.parametrize("flash", ["1", "0"], ids=["fused", "stored"])
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "stored"])
 @pytest.mark.parametrize("trained", [False, True], ids=["init", "trained"])
-def test_head64_passes_the_gate_fused_and_stored(flint, cuda, monkeypatch, flash, trained):
-    monkeypatch.setenv("FLINT_FLASH", flash)
-    _gate_case(flint, HEAD64, 2, 128, trained)
+def test_head64_passes_the_gate_fused_and_stored(flint, cuda, fused, trained):
+    _gate_case(flint, HEAD64, 2, 128, trained, fused=fused)
 
 
-def test_fused_attention_forward_error_is_no_larger(flint, cuda, monkeypatch):
+def test_fused_attention_forward_error_is_no_larger(flint, cuda):
     cfg, sequences, length = HEAD64, 3, 96
     shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
                                 cfg["padded_vocab"])
@@ -151,12 +162,11 @@ def test_fused_attention_forward_error_is_no_larger(flint, cuda, monkeypatch):
     idx, tgt = _tokens(cfg, sequences, length, 22)
     ref = G.gradients(params, idx, tgt, cfg, 1.0)
     errs = {}
-    for flash in ("1", "0"):
-        monkeypatch.setenv("FLINT_FLASH", flash)
-        out = _run(flint, cfg, sequences, length, params, idx, tgt, 1.0)
-        errs[flash] = _rel_l2(out[0][:, :cfg["vocab"]], ref[0])
-    print(f"logits rel L2: fused {errs['1']:.3e} stored {errs['0']:.3e}")
-    assert errs["1"] <= errs["0"] * 1.05
+    for fused in (True, False):
+        out = _run(flint, cfg, sequences, length, params, idx, tgt, 1.0, fused=fused)
+        errs[fused] = _rel_l2(out[0][:, :cfg["vocab"]], ref[0])
+    print(f"logits rel L2: fused {errs[True]:.3e} stored {errs[False]:.3e}")
+    assert errs[True] <= errs[False] * 1.05
 
 
 # GPT-2 124M itself (configs[4]'s model), at the reference's gate shapes (ref
@@ -171,10 +181,18 @@ def test_gpt2_124m_passes_the_gate(flint, cuda, sequences, length, trained):
     _gate_case(flint, GPT2, sequences, length, trained)
 
 
-def test_gpt2_124m_full_batch_properties(flint, cuda):
-    """configs[4]'s own batch, 8 x 1024: every output and gradient finite, two
-    runs equal bit for bit, and the mean loss within 1e-3 of the FP32 CPU
-    model's on the same tokens."""
+@pytest.mark.parametrize("sequences", [8, 16], ids=["8x1024", "16x1024"])
+def test_gpt2_124m_passes_the_gate_at_full_batch(flint, cuda, sequences):
+    """configs[4]'s own batch (8 x 1024) and the reference's micro-batch
+    (16 x 1024, ref tests/test_gpt2.py:744-755): every output and gradient
+    through the gate, with the FP32 reference and the FP16 peer computed by
+    torch on the GPU (FP32 matmuls, no TF32)."""
+    _gate_case(flint, GPT2, sequences, 1024, trained=sequences == 16, ref_device="cuda")
+
+
+def test_gpt2_124m_full_batch_is_deterministic(flint, cuda):
+    """configs[4]'s batch run twice: every output, gradient and the mean loss
+    equal bit for bit, every gradient finite and somewhere nonzero."""
     cfg, sequences, length = GPT2, 8, 1024
     shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
                                 cfg["padded_vocab"])
@@ -195,11 +213,6 @@ def test_gpt2_124m_full_batch_properties(flint, cuda):
     for n in a[3]:
         assert torch.equal(a[3][n].view(torch.int32), b[3][n].view(torch.int32)), n
     assert a[4] == b[4]
-    with torch.no_grad():
-        _, ref_loss = G.forward(params, idx, tgt, cfg)
-    ref_mean = float(ref_loss.double().mean())
-    print(f"mean loss: flint {a[4]:.6f} FP32 CPU {ref_mean:.6f}")
-    assert abs(a[4] - ref_mean) <= 1e-3 * ref_mean
 
 
 def test_a_token_file_batch_runs_through_the_model(flint, cuda, tmp_path):
@@ -253,7 +266,7 @@ def test_run_twice_and_separate_buffers_give_the_same_bits(flint, cuda):
 
 @pytest.mark.parametrize("length", [1024, 320])
 @pytest.mark.parametrize("force", [None, "128,192,3,64", "256,128,3,64", "256,256,3"])
-def test_causal_attention_products_change_no_bits(flint, cuda, monkeypatch, length, force):
+def test_causal_attention_products_change_no_bits(flint, cuda, tune, length, force):
     """The attention GEMMs skip the tiles and k-ranges above the diagonal
     (FLINT_ATTN_CAUSAL unset); computing everything (=0) must give the same
     bits in every output and gradient, whichever tiles the pipeline uses."""
@@ -265,13 +278,11 @@ def test_causal_attention_products_change_no_bits(flint, cuda, monkeypatch, leng
     params = {n: t.half().float() for n, t in params.items()}
     idx, tgt = _tokens(cfg, sequences, length, 12)
     if force is not None:
-        monkeypatch.setenv("FLINT_GEMM_PIPE", force)
-    # The stored scores and probabilities (head width 64 would take the fused
-    # attention, which has no causal-skip variant to compare).
-    monkeypatch.setenv("FLINT_FLASH", "0")
-    monkeypatch.setenv("FLINT_ATTN_CAUSAL", "0")
+        tune("gemm_pipe", force)
+    # The stored scores and probabilities (flint_gpt2_create's model).
+    tune("attn_causal", "0")
     full = _run(flint, cfg, sequences, length, params, idx, tgt, 0.25)
-    monkeypatch.delenv("FLINT_ATTN_CAUSAL")
+    tune("attn_causal", None)
     causal = _run(flint, cfg, sequences, length, params, idx, tgt, 0.25)
     for x, y in zip(full[:3], causal[:3]):
         assert torch.equal(x.view(torch.int32) if x.dtype == torch.float32 else x,
@@ -287,7 +298,7 @@ WIDE = dict(layers=1, heads=4, width=256, block_size=1024, vocab=1000, padded_vo
 
 @pytest.mark.parametrize("cfg,sequences,length", [(TINY, 8, 64), (ODD, 2, 48), (WIDE, 2, 520)],
                          ids=["tiny-8x64", "odd-2x48", "wide-2x520"])
-def test_fused_column_sums_change_no_bits(flint, cuda, monkeypatch, cfg, sequences, length):
+def test_fused_column_sums_change_no_bits(flint, cuda, tune, cfg, sequences, length):
     """The model's LayerNorm backward runs its chunk partials and dx rows in
     one launch and leaves the dbeta / dgamma merge to the next linear layer's
     finish (FLINT_FUSED_SUMS and FLINT_LN_DEFER unset); the merge in a launch
@@ -297,12 +308,12 @@ def test_fused_column_sums_change_no_bits(flint, cuda, monkeypatch, cfg, sequenc
                                 cfg["padded_vocab"])
     params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=13, trained=True)
     idx, tgt = _tokens(cfg, sequences, length, 14)
-    monkeypatch.setenv("FLINT_FUSED_SUMS", "0")
+    tune("fused_sums", "0")
     plain = _run(flint, cfg, sequences, length, params, idx, tgt, 0.5)
-    monkeypatch.delenv("FLINT_FUSED_SUMS")
-    monkeypatch.setenv("FLINT_LN_DEFER", "0")
+    tune("fused_sums", None)
+    tune("ln_defer", "0")
     in_place = _run(flint, cfg, sequences, length, params, idx, tgt, 0.5)
-    monkeypatch.delenv("FLINT_LN_DEFER")
+    tune("ln_defer", None)
     fused = _run(flint, cfg, sequences, length, params, idx, tgt, 0.5)
     for other in (in_place, fused):
         for n in plain[3]:
@@ -312,7 +323,7 @@ def test_fused_column_sums_change_no_bits(flint, cuda, monkeypatch, cfg, sequenc
 
 @pytest.mark.parametrize("cfg,sequences,length", [(TINY, 8, 64), (ODD, 2, 48), (WIDE, 2, 520)],
                          ids=["tiny-8x64", "odd-2x48", "wide-2x520"])
-def test_fused_linear_grads_change_no_bits(flint, cuda, monkeypatch, cfg, sequences, length):
+def test_fused_linear_grads_change_no_bits(flint, cuda, tune, cfg, sequences, length):
     """The model finishes each linear layer's weight and bias gradients in one
     launch (FLINT_FUSED_GRADS unset); flint_gemm_tn and flint_bias_gradient
     called one after the other (=0) must give the same bits, after a fresh
@@ -336,9 +347,9 @@ def test_fused_linear_grads_change_no_bits(flint, cuda, monkeypatch, cfg, sequen
             torch.cuda.synchronize()
         return fresh, twice
 
-    monkeypatch.setenv("FLINT_FUSED_GRADS", "0")
+    tune("fused_grads", "0")
     plain = grads_twice()
-    monkeypatch.delenv("FLINT_FUSED_GRADS")
+    tune("fused_grads", None)
     fused = grads_twice()
     for a, b in zip(plain, fused):
         assert a.keys() == b.keys()
@@ -399,3 +410,84 @@ def test_mean_loss_of_equal_logits_is_log_vocab(flint, cuda):
     _, row_loss, _, _, mean = _run(flint, cfg, sequences, length, params, idx, tgt, 1.0)
     assert np.allclose(row_loss.numpy(), np.log(cfg["vocab"]), rtol=1e-6)
     assert mean == pytest.approx(np.log(cfg["vocab"]), rel=1e-6)
+
+
+# ---- The assembly equals the public kernels called one by one --------------
+# (ref tests/test_gpt2.py:1114-1123, ref tests/test_gpt2_backward.py:896-950)
+
+# The reference's TINY model (ref scripts/gpt2_torch.py:34): heads of width 64.
+REF_TINY = dict(layers=2, heads=2, width=128, block_size=64, vocab=50257, padded_vocab=50304)
+
+
+def _model_passes(flint, cfg, sequences, length, params, tok, trg, scale, fused, old=None):
+    """flint_gpt2_forward + flint_gpt2_backward; (logits, dlogits, row_loss,
+    grads) on the device."""
+    rows, pv = sequences * length, cfg["padded_vocab"]
+    with _make(flint, cfg, sequences, length, fused=fused) as model:
+        for name, address, _, _ in model.parameters():
+            model.write(address, params[name].contiguous())
+        model.sync_weights()
+        if old is not None:
+            for name, address, _, _ in model.gradients():
+                model.write(address, old[name].contiguous())
+        model.forward(tok, trg, scale)
+        model.backward(tok, accumulate=old is not None)
+        lg, dl, rl = model.outputs()
+        out = (model.read(lg, (rows, pv), torch.float16), model.read(dl, (rows, pv), torch.float16),
+               model.read(rl, (rows,), torch.float32),
+               {n: model.read(a, (r, c), torch.float32) for n, a, r, c in model.gradients()})
+        torch.cuda.synchronize()
+    return out
+
+
+def _same_bits(a, b, what):
+    ia = a.view(torch.int16 if a.dtype == torch.float16 else torch.int32)
+    ib = b.view(torch.int16 if b.dtype == torch.float16 else torch.int32)
+    differ = int((ia != ib).sum())
+    assert differ == 0, f"{what}: {differ} of {a.numel()} values differ"
+
+
+def _compare_with_hand(flint, cfg, sequences, length, fused, accumulate, seed):
+    import compose
+
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    # FP32 masters off FP16's grid, so the FP16 copies round.
+    params = {n: t.cuda() for n, t in
+              G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=seed, trained=True).items()}
+    idx, tgt = _tokens(cfg, sequences, length, seed + 1)
+    tok, trg = _dev16(idx), _dev16(tgt)
+    scale = 1024.0 / (sequences * length)
+    old = None
+    if accumulate:
+        g = torch.Generator().manual_seed(seed + 2)
+        old = {n: (0.01 * torch.randn(r, c, generator=g)).cuda() for n, r, c in shapes}
+    by_model = _model_passes(flint, cfg, sequences, length, params, tok, trg, scale, fused, old)
+    by_hand = compose.passes(flint, cfg, sequences, length, params, tok, trg, scale,
+                             fused=fused, old=old)
+    for what, a, b in zip(("logits", "dlogits", "row_loss"), by_model[:3], by_hand[:3]):
+        _same_bits(a, b, what)
+    assert by_model[3].keys() == by_hand[3].keys()
+    for n in by_model[3]:
+        _same_bits(by_model[3][n], by_hand[3][n], n)
+
+
+@pytest.mark.parametrize("sequences,length", [(1, 8), (3, 64), (2, 32)], ids=str)
+@pytest.mark.parametrize("fused", [False, True], ids=["stored", "fused"])
+def test_the_assembly_equals_the_kernels_called_by_hand(flint, cuda, fused, sequences, length):
+    _compare_with_hand(flint, REF_TINY, sequences, length, fused, False, 31)
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["stored", "fused"])
+def test_the_accumulating_assembly_equals_the_kernels_called_by_hand(flint, cuda, fused):
+    _compare_with_hand(flint, REF_TINY, 2, 32, fused, True, 41)
+
+
+@pytest.mark.parametrize("cfg,sequences,length", [(TINY, 2, 64), (ODD, 2, 48)],
+                         ids=["heads-of-32", "heads-of-32-odd-vocab"])
+def test_other_head_widths_equal_the_kernels_called_by_hand(flint, cuda, cfg, sequences, length):
+    _compare_with_hand(flint, cfg, sequences, length, False, False, 51)
+
+
+def test_gpt2_124m_equals_the_kernels_called_by_hand(flint, cuda):
+    _compare_with_hand(flint, GPT2, 1, 256, False, False, 61)

@@ -93,8 +93,8 @@ def test_bias_gradient_past_65535_chunks(flint, cuda):
                                        (9, 1032), (100, 4096)])
 @pytest.mark.parametrize("acc", [False, True])
 @pytest.mark.parametrize("fused", ["1", "0"])
-def test_layernorm_backward(flint, cuda, monkeypatch, rows, cols, acc, fused):
-    monkeypatch.setenv("FLINT_LN_FUSED", fused)
+def test_layernorm_backward(flint, cuda, tune, rows, cols, acc, fused):
+    tune("ln_fused", fused)
     x = normal((rows, cols), 8)
     gamma = 1 + normal((cols,), 9, 0.1)
     beta = normal((cols,), 10, 0.1)

@@ -52,10 +52,10 @@ def test_embedding_forward_matches_pytorch_bitwise(flint, cuda, sequences, lengt
     (300, 8, 100, 8, "uniform"), (3, 4000, 65536, 8, "uniform"), (5, 1700, 3000, 8, "zipf")])
 @pytest.mark.parametrize("accumulate", [False, True])
 @pytest.mark.parametrize("together", ["1", "0"])   # position sums in the sort's launch, or after
-def test_embedding_backward_matches_the_oracle_bitwise(flint, cuda, monkeypatch, together,
+def test_embedding_backward_matches_the_oracle_bitwise(flint, cuda, tune, together,
                                                        sequences, length, vocab,
                                                        width, kind, accumulate):
-    monkeypatch.setenv("FLINT_EMB_TOGETHER", together)
+    tune("emb_together", together)
     rows = sequences * length
     g = torch.Generator().manual_seed(4)
     if kind == "uniform":
