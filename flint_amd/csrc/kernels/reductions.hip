@@ -682,9 +682,12 @@ causal_softmax_forward(h8* __restrict__ p, const h8* __restrict__ s, size_t rows
         const int c = lane + i * 64;
         if (c < written) {
             if (c < visible_chunks) {
+                // Masked columns of the diagonal chunk are selected as +0, not
+                // formed as 0 / sum: a row whose sum is NaN keeps them +0.
+                const int vis = min(t + 1 - c * 8, 8);
                 float o[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = mul_rn(v[i][j], inv);
+                for (int j = 0; j < 8; ++j) o[j] = j < vis ? mul_rn(v[i][j], inv) : 0.0f;
                 pr[c] = pack8(o);
             } else {
                 pr[c] = h8{};

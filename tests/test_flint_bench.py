@@ -177,209 +177,228 @@ def test_the_generated_tables_cover_each_rule():
 
 
 # ------------------------------------------------------------------ GPU: quick runs
+#
+# Each run below is one quick invocation and the labels its cases must carry.
+# The log's invariants are checked by small functions, each stating one
+# property of the "flint-bench/1" format (its field names are the harness's
+# interface): the header, the timing rounds, the monitor windows, and what a
+# GEMM case must record. The shapes are chosen to mix GPT-2 sizes with edge
+# tiles and short k.
 
-def quick(exe, tmp_path, *args):
-    out = tmp_path / "bench.json"
-    result = run(exe, *args, "--out", str(out), timeout=600)
-    assert result.returncode == 0, f"stdout:\n{result.stdout}\nstderr:\n{result.stderr}"
-    text = out.read_text()
-    assert str(tmp_path) not in text and str(flint_lib.ROOT) not in text
-    data = json.loads(text)
-    assert data["schema"] == "flint-bench/1"
-    assert data["args"] == list(args)
-    assert data["quick"] is True and data["standard_protocol"] is False
-    start = data["gpu_at_start"]
-    assert isinstance(start["process_detection"], bool)
-    if start["utilization_percent"] is not None:
-        assert 0 <= start["utilization_percent"] <= 100
-    return result, data
+BASELINES = {"none": "rocBLAS", "bias": "hipBLASLt, FP32 bias",
+             "bias-gelu": "hipBLASLt, FP32 bias", "bias-residual": "hipBLASLt, residual in C",
+             "dgelu": "hipBLASLt DGELU"}
+# (layout, epilogue, shapes)
+GEMM_RUNS = {
+    "nt": ("nt", "none", "2048x2304x768,96x136x56"),
+    "nt-bias": ("nt", "bias", "512x768x3072,72x264x32"),
+    "nt-bias-gelu": ("nt", "bias-gelu", "2048x3072x768,40x520x64"),
+    "nt-bias-residual": ("nt", "bias-residual", "1024x768x768,8x130x16"),
+    "nn": ("nn", "none", "2048x768x3072,200x264x24"),
+    "nn-dgelu": ("nn", "dgelu", "2048x3072x768,64x136x40"),
+    "tn": ("tn", "none", "3072x768x2048,264x200x1000,16x8x8"),
+}
 
 
-def assert_rounds(case, options, two_sided=True):
+def run_quick(exe, tmp_path, argv):
+    """Runs one quick invocation with --out; its log, after the header checks."""
+    out = tmp_path / "log.json"
+    res = run(exe, *argv, "--out", str(out), timeout=600)
+    assert res.returncode == 0, f"{res.stdout}\n{res.stderr}"
+    raw = out.read_text()
+    for private in (str(tmp_path), str(flint_lib.ROOT)):
+        assert private not in raw, "the log names a local path"
+    log = json.loads(raw)
+    check_header(log, argv)
+    return res, log
+
+
+def check_header(log, argv):
+    assert (log["schema"], log["args"]) == ("flint-bench/1", list(argv))
+    assert (log["quick"], log["standard_protocol"]) == (True, False)
+    util = log["gpu_at_start"]["utilization_percent"]
+    assert util is None or 0 <= util <= 100
+    assert type(log["gpu_at_start"]["process_detection"]) is bool
+
+
+def median_of(values):
+    return statistics.median(values)
+
+
+def check_side_timing(case, side, opts, valid):
+    """A side's time is the median of its valid rounds' times, every sample
+    ran at least (nearly) the sample window."""
+    per_round = [r[side]["ms_per_launch"] for r in valid]
+    assert case[side]["ms_per_launch"] == pytest.approx(median_of(per_round))
+    assert min(r[side]["sample_ms"] for r in valid) >= 0.9 * opts["sample_ms"]
+    assert case[side]["min_sample_ms"] >= 0.9 * opts["sample_ms"]
+
+
+def check_rounds(case, opts, sides):
     valid = [r for r in case["rounds"] if r["valid"]]
-    assert case["valid_rounds"] == len(valid) >= options["rounds"]
-    assert case["warmup_seconds"] >= options["warmup_seconds"]
-    if two_sided:
-        for r in valid:
-            assert r["ratio"] == pytest.approx(r["baseline"]["ms_per_launch"] / r["flint"]["ms_per_launch"])
-        ratios = [r["ratio"] for r in valid]
-        assert case["ratio"]["median"] == pytest.approx(statistics.median(ratios))
-        assert case["ratio"]["min"] == pytest.approx(min(ratios))
-        assert case["ratio"]["max"] == pytest.approx(max(ratios))
-        assert [r["flint_first"] for r in valid] == [i % 2 == 0 for i in range(len(valid))]
-    for name in ("flint", "baseline") if two_sided else ("flint",):
-        side = case[name]
-        assert side["min_sample_ms"] >= 0.9 * options["sample_ms"]
-        assert side["ms_per_launch"] == pytest.approx(statistics.median(
-            [r[name]["ms_per_launch"] for r in valid]))
-        for r in valid:
-            assert r[name]["sample_ms"] >= 0.9 * options["sample_ms"]
-        if side["stats"] is not None:
-            assert_stats_follow_from_rounds(side["stats"], [r[name]["stats"] for r in valid])
-            if case["flops"] > 0 and side["stats"]["samples"] > 0:
-                # The firmware's clock readings lag short bursts of launches,
-                # so only the sign is pinned here.
-                assert side["clock_adjusted_compute_fraction"] > 0
+    assert len(valid) == case["valid_rounds"] and len(valid) >= opts["rounds"]
+    assert case["warmup_seconds"] >= opts["warmup_seconds"]
+    for side in sides:
+        check_side_timing(case, side, opts, valid)
+        if case[side]["stats"] is not None:
+            check_monitor(case[side]["stats"], [r[side]["stats"] for r in valid])
+    if sides == ("flint", "baseline"):
+        # Interleaved rounds: the two sides alternate in going first, and each
+        # round's ratio is baseline time over Flint time.
+        assert [r["flint_first"] for r in valid] == [k % 2 == 0 for k in range(len(valid))]
+        ratios = [r["baseline"]["ms_per_launch"] / r["flint"]["ms_per_launch"] for r in valid]
+        assert [r["ratio"] for r in valid] == pytest.approx(ratios)
+        summary = case["ratio"]
+        assert (summary["min"], summary["median"], summary["max"]) == pytest.approx(
+            (min(ratios), median_of(ratios), max(ratios)))
 
 
-def assert_stats_follow_from_rounds(stats, windows):
-    """A side's stats merge its valid rounds' windows: counts add up, means are
-    weighted by each window's seconds, maxima and the new-process flag carry."""
-    seconds = sum(w["seconds"] for w in windows)
-    assert stats["seconds"] == pytest.approx(seconds)
-    assert stats["samples"] == sum(w["samples"] for w in windows)
-    assert stats["failed_reads"] == sum(w["failed_reads"] for w in windows)
-    # Means weigh only the windows that hold a reading; without any they are null.
-    read = [w for w in windows if w["samples"] > 0]
-    read_seconds = sum(w["seconds"] for w in read)
-    for name in ("sm_mhz", "mem_mhz", "power_w", "gfx_activity_percent", "power_cap_share", "thermal_share"):
-        if not read:
-            assert stats[name] is None, name
-            continue
-        expect = sum(w[name] * w["seconds"] for w in read) / read_seconds
-        assert stats[name] == pytest.approx(expect), name
-    if read:
-        assert stats["temp_c_max"] == max(w["temp_c_max"] for w in read)
-    assert stats["new_process"] == any(w["new_process"] for w in windows)
-    # A window with no reading of its own holds the last one before it, so
-    # once the monitor has read the device every window has a clock.
-    for w in windows:
-        assert w["samples"] >= 0
-        if w["samples"] > 0:
-            assert w["sm_mhz"] > 0 and w["power_w"] > 0
+def check_monitor(merged, windows):
+    """The merged monitor statistics of a side are its windows' totals, their
+    means weighted by the seconds of the windows that hold readings, and
+    their extremes."""
+    for total in ("samples", "failed_reads"):
+        assert merged[total] == sum(w[total] for w in windows), total
+    assert merged["seconds"] == pytest.approx(sum(w["seconds"] for w in windows))
+    assert merged["new_process"] == any(w["new_process"] for w in windows)
+    with_reading = [w for w in windows if w["samples"] > 0]
+    weight = sum(w["seconds"] for w in with_reading)
+    for field in ("sm_mhz", "mem_mhz", "power_w", "gfx_activity_percent", "power_cap_share",
+                  "thermal_share"):
+        if with_reading:
+            mean = sum(w[field] * w["seconds"] for w in with_reading) / weight
+            assert merged[field] == pytest.approx(mean), field
+        else:
+            assert merged[field] is None, field
+    if with_reading:
+        assert merged["temp_c_max"] == max(w["temp_c_max"] for w in with_reading)
+        assert all(w["sm_mhz"] > 0 and w["power_w"] > 0 for w in with_reading)
+
+
+def gemm_bytes(layout, epilogue, m, n, k):
+    """Bytes one launch's buffers hold: the operands, the output (FP32 for TN
+    and the residual form), pre, the residual, the bias."""
+    operands = 2 * (m * k + n * k)
+    out = m * n * (4 if layout == "tn" or epilogue == "bias-residual" else 2)
+    extra = {"bias": 4 * n, "bias-gelu": 2 * m * n + 4 * n, "dgelu": 2 * m * n,
+             "bias-residual": 4 * m * n + 4 * n}.get(epilogue, 0)
+    return operands + out + extra
+
+
+def check_gemm_case(case, layout, epilogue, shape, l2_bytes):
+    m, n, k = shape
+    assert (case["layout"], case["epilogue"]) == (layout, epilogue)
+    assert case["baseline_name"] == BASELINES[epilogue]
+    assert case["ok"] and case["outputs_match"], case["output_check"]
+    assert case["flops"] == 2 * m * n * k
+    assert case["size_bytes"] == gemm_bytes(layout, epilogue, m, n, k)
+    assert case["rotation_sets"] * case["size_bytes"] > 4 * l2_bytes
+    for side in ("flint", "baseline"):
+        t = case[side]
+        assert t["tflops"] == pytest.approx(case["flops"] / t["ms_per_launch"] / 1e9)
+    checks = [case["output_check"]]
+    if epilogue == "bias-gelu":
+        checks.append(case["pre_check"])
+    else:
+        assert case["pre_check"] is None
+    for c in checks:
+        assert c["deterministic"] is True and c["nonfinite"] == 0
+        assert 0 <= c["rel_l2"] <= 2.0**-10 and c["max_abs_baseline"] > 0
+    algo = case["baseline_algorithm"]
+    if epilogue == "none":
+        assert algo is None
+    else:
+        timed = [c["ms_per_launch"] for c in algo["candidates"] if c["ms_per_launch"] is not None]
+        assert timed and len(algo["candidates"]) <= 8
+        assert algo["candidates"][algo["used"]]["ms_per_launch"] == min(timed)
 
 
 @pytest.mark.gpu
-def test_quick_copy(exe, tmp_path):
-    args = ["copy", "--quick", "--sizes", "1M,4097", "--allow-busy"]
-    _, data = quick(exe, tmp_path, *args)
-    device, options = data["device"], data["options"]
-    assert device["arch"].startswith("gfx950")
-    assert device["rated_bandwidth_gbs"] == 8000
-    cases = data["cases"]
-    assert [c["label"] for c in cases] == ["1 MiB", "4097 B"]
-    for case in cases:
-        assert case["layout"] is None and case["epilogue"] is None
+@pytest.mark.parametrize("name", list(GEMM_RUNS))
+def test_quick_gemm_run(exe, tmp_path, name):
+    layout, epilogue, shapes = GEMM_RUNS[name]
+    argv = ["gemm", "--quick", "--allow-busy", "--layout", layout, "--epilogue", epilogue,
+            "--shapes", shapes]
+    res, log = run_quick(exe, tmp_path, argv)
+    labels = shapes.split(",")
+    assert [c["label"] for c in log["cases"]] == labels
+    assert log["options"]["lt_algo"] == "fastest"
+    tag = layout if epilogue == "none" else f"{layout}+{epilogue}"
+    assert f"gemm {tag} {labels[0]}" in res.stdout
+    for case, label in zip(log["cases"], labels):
+        shape = tuple(int(v) for v in label.split("x"))
+        check_gemm_case(case, layout, epilogue, shape, log["device"]["l2_bytes"])
+        check_rounds(case, log["options"], ("flint", "baseline"))
+
+
+@pytest.mark.gpu
+def test_quick_copy_run(exe, tmp_path):
+    argv = ["copy", "--quick", "--allow-busy", "--sizes", "3M,12345"]
+    _, log = run_quick(exe, tmp_path, argv)
+    dev = log["device"]
+    assert dev["arch"].startswith("gfx950") and dev["rated_bandwidth_gbs"] == 8000
+    assert [c["label"] for c in log["cases"]] == ["3 MiB", "12345 B"]
+    for case in log["cases"]:
         assert case["ok"] and case["outputs_match"]
-        assert case["output_check"] is None and case["baseline_algorithm"] is None
-        assert_rounds(case, options)
-        for name in ("flint", "baseline"):
-            side = case[name]
-            assert 0 < side["gbs"] <= 1.1 * device["rated_bandwidth_gbs"]
-            assert side["gbs"] == pytest.approx(case["bytes_moved"] / (side["ms_per_launch"] * 1e-3) / 1e9)
-            # Against the bandwidth at the monitored memory clock: HBM3E moves
-            # four transfers per reported clock over the bus.
-            st = side["stats"]
+        assert (case["layout"], case["epilogue"], case["output_check"],
+                case["baseline_algorithm"]) == (None, None, None, None)
+        check_rounds(case, log["options"], ("flint", "baseline"))
+        for side in ("flint", "baseline"):
+            t = case[side]
+            assert t["gbs"] == pytest.approx(case["bytes_moved"] / t["ms_per_launch"] / 1e6)
+            assert 0 < t["gbs"] <= 1.1 * dev["rated_bandwidth_gbs"]
+            st = t["stats"]
             if st is not None and st["samples"] > 0 and st["mem_mhz"] > 0:
-                at_clock = 4 * st["mem_mhz"] * 1e6 * device["bus_width_bits"] / 8 / 1e9
-                assert side["clock_adjusted_fraction"] == pytest.approx(side["gbs"] / at_clock)
-            else:
-                assert side["clock_adjusted_fraction"] is None
-        stride = (case["size_bytes"] + 255) // 256 * 256
-        assert case["rotation_sets"] * 2 * stride > 4 * device["l2_bytes"]
+                # HBM3E: four transfers per reported memory clock.
+                peak = 4 * st["mem_mhz"] * 1e6 * dev["bus_width_bits"] / 8 / 1e9
+                assert t["clock_adjusted_fraction"] == pytest.approx(t["gbs"] / peak)
+        padded = -(-case["size_bytes"] // 256) * 256
+        assert case["rotation_sets"] * 2 * padded > 4 * dev["l2_bytes"]
 
 
 @pytest.mark.gpu
-def test_quick_mma(exe, tmp_path):
-    args = ["mma", "--quick", "--chains", "4,8,16", "--allow-busy"]
-    _, data = quick(exe, tmp_path, *args)
-    device, options = data["device"], data["options"]
-    cases = data["cases"]
-    assert [c["label"] for c in cases] == [f"mfma 32x32x16 f16->f32, {n} chains, 2 blocks/CU" for n in (4, 8, 16)]
-    for case in cases:
-        assert case["one_sided"] is True and case["baseline"] is None and case["ratio"] is None
+def test_quick_mma_run(exe, tmp_path):
+    argv = ["mma", "--quick", "--allow-busy", "--chains", "16,4"]
+    _, log = run_quick(exe, tmp_path, argv)
+    cus = log["device"]["cu_count"]
+    assert [c["label"] for c in log["cases"]] == [
+        f"mfma 32x32x16 f16->f32, {c} chains, 2 blocks/CU" for c in (16, 4)]
+    for case in log["cases"]:
+        assert case["one_sided"] and case["baseline"] is None and case["ratio"] is None
         assert case["ok"] and case["outputs_match"]
-        # 2 blocks/CU x CUs blocks of 4 waves, each wave 32768 MFMAs of 32768 FLOP.
-        assert case["flops"] == 2 * device["cu_count"] * 4 * 32768 * 32768
         assert case["peak_flop_per_cu_per_clock"] == 4096
-        assert_rounds(case, options, two_sided=False)
+        # Two 4-wave blocks per CU, each wave 32,768 MFMAs of 32 x 32 x 16 x 2 FLOP.
+        assert case["flops"] == (2 * cus) * 4 * 32768 * (32 * 32 * 16 * 2)
         assert 0 < case["flint"]["rated_compute_fraction"] <= 1.05
+        check_rounds(case, log["options"], ("flint",))
 
 
-GEMM_CASES = [
-    ("nt", "none", "1000x2304x768,129x257x40"),
-    ("nt", "bias", "1000x2304x768,129x257x40"),
-    ("nt", "bias-gelu", "1000x3072x768,129x264x40"),
-    ("nt", "bias-residual", "1000x768x3072,129x266x40"),
-    ("nn", "none", "1000x768x2304,129x264x40"),
-    ("nn", "dgelu", "1000x3072x768,129x264x40"),
-    ("tn", "none", "768x768x8192,136x120x3000,1032x8x4096,72x40x1001"),
+# Runs whose point is one option: the hipBLASLt candidate choice, and the
+# GPT-2 shapes an epilogue runs when --shapes is left out.
+OPTION_RUNS = [
+    (["--layout", "nt", "--epilogue", "bias-residual", "--lt-algo", "first", "--shapes",
+      "512x768x768"], ["512x768x768"], "first"),
+    (["--layout", "nn", "--epilogue", "dgelu", "--lt-algo", "first", "--shapes", "256x3072x768"],
+     ["256x3072x768"], "first"),
+    (["--epilogue", "bias-gelu"], ["8192x3072x768"], "fastest"),
+    (["--epilogue", "bias-residual"], ["8192x768x768", "8192x768x3072"], "fastest"),
+    (["--layout", "nn", "--epilogue", "dgelu"], ["8192x3072x768"], "fastest"),
 ]
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("layout, epilogue, shape_list", GEMM_CASES)
-def test_quick_gemm(exe, tmp_path, layout, epilogue, shape_list):
-    args = ["gemm", "--quick", "--shapes", shape_list, "--allow-busy"]
-    if layout != "nt":
-        args[1:1] = ["--layout", layout]
-    if epilogue != "none":
-        args[1:1] = ["--epilogue", epilogue]
-    result, data = quick(exe, tmp_path, *args)
-    first = shape_list.split(",")[0]
-    for name in ("none", "bias", "bias-gelu", "dgelu", "bias-residual"):
-        label = f"gemm {layout}" + ("" if name == "none" else f"+{name}") + f" {first}"
-        assert (label in result.stdout) == (epilogue == name), label
-    device, options = data["device"], data["options"]
-    assert options["lt_algo"] == "fastest"
-    shapes = [tuple(int(d) for d in item.split("x")) for item in shape_list.split(",")]
-    assert [c["label"] for c in data["cases"]] == shape_list.split(",")
-    for case, (m, n, k) in zip(data["cases"], shapes):
-        assert case["layout"] == layout and case["epilogue"] == epilogue
-        assert case["baseline_name"] == {
-            "none": "rocBLAS", "bias": "hipBLASLt, FP32 bias", "bias-gelu": "hipBLASLt, FP32 bias",
-            "dgelu": "hipBLASLt DGELU", "bias-residual": "hipBLASLt, residual in C"}[epilogue]
-        assert case["ok"] and case["outputs_match"], case["output_check"]
-        if epilogue == "none":
-            assert case["baseline_algorithm"] is None
-        else:
-            algorithm = case["baseline_algorithm"]
-            timed = [c for c in algorithm["candidates"] if c["ms_per_launch"] is not None]
-            assert 1 <= len(algorithm["candidates"]) <= 8 and timed
-            assert algorithm["candidates"][algorithm["used"]]["ms_per_launch"] == min(
-                c["ms_per_launch"] for c in timed)
-        checks = [case["output_check"]] + ([case["pre_check"]] if epilogue == "bias-gelu" else [])
-        if epilogue != "bias-gelu":
-            assert case["pre_check"] is None
-        for check in checks:
-            assert check["deterministic"] is True and check["nonfinite"] == 0
-            assert 0 <= check["rel_l2"] <= 2**-10
-            assert check["max_abs_baseline"] > 0
-        assert case["flops"] == 2 * m * n * k
-        assert_rounds(case, options)
-        for name in ("flint", "baseline"):
-            assert case[name]["tflops"] == pytest.approx(case["flops"] / (case[name]["ms_per_launch"] * 1e-3) / 1e12)
-        assert case["size_bytes"] == (
-            2 * (m * k + n * k)
-            + m * n * (4 if layout == "tn" or epilogue == "bias-residual" else 2)
-            + (2 * m * n if epilogue in ("bias-gelu", "dgelu") else 0)
-            + (4 * m * n if epilogue == "bias-residual" else 0)
-            + (4 * n if epilogue in ("bias", "bias-gelu", "bias-residual") else 0))
-        assert case["rotation_sets"] * case["size_bytes"] > 4 * device["l2_bytes"]
-
-
-@pytest.mark.gpu
-@pytest.mark.parametrize("layout, epilogue", [("nt", "bias"), ("nn", "dgelu")])
-def test_quick_gemm_lt_algo_first(exe, tmp_path, layout, epilogue):
-    args = ["gemm", "--quick", "--layout", layout, "--epilogue", epilogue, "--lt-algo", "first",
-            "--shapes", "1000x768x768", "--allow-busy"]
-    _, data = quick(exe, tmp_path, *args)
-    assert data["options"]["lt_algo"] == "first"
-    (case,) = data["cases"]
-    assert case["ok"]
-    assert case["baseline_algorithm"]["selection"] == "first" and case["baseline_algorithm"]["used"] == 0
-
-
-@pytest.mark.gpu
-@pytest.mark.parametrize("args, labels", [
-    (["--epilogue", "bias-gelu"], ["8192x3072x768"]),
-    (["--epilogue", "bias-residual"], ["8192x768x768", "8192x768x3072"]),
-    (["--layout", "nn", "--epilogue", "dgelu"], ["8192x3072x768"]),
-])
-def test_epilogue_defaults_are_the_gpt2_layers(exe, tmp_path, args, labels):
-    _, data = quick(exe, tmp_path, "gemm", *args, "--quick", "--allow-busy")
-    assert [c["label"] for c in data["cases"]] == labels
-    assert all(c["ok"] for c in data["cases"])
+@pytest.mark.parametrize("extra,labels,choice", OPTION_RUNS,
+                         ids=[" ".join(a) for a, _, _ in OPTION_RUNS])
+def test_quick_option_run(exe, tmp_path, extra, labels, choice):
+    _, log = run_quick(exe, tmp_path, ["gemm", "--quick", "--allow-busy", *extra])
+    assert [c["label"] for c in log["cases"]] == labels
+    assert log["options"]["lt_algo"] == choice
+    for case in log["cases"]:
+        assert case["ok"]
+        algo = case["baseline_algorithm"]
+        assert algo["selection"] == choice
+        if choice == "first":
+            assert algo["used"] == 0
 
 
 # ------------------------------------------------------------------ CPU: results_table
