@@ -36,14 +36,12 @@ M, C, V, VP, T, H = 8192, 768, 50257, 50304, 1024, 12
 B = 8 * H   # attention batch: 8 sequences x 12 heads
 
 
-def _time_gpu(torch, fn, sets, rounds=5, per_round=None):
-    """Median per-launch ms over rounds of back-to-back launches (HIP events)."""
-    for i in range(3):
-        fn(sets[i % len(sets)])
-    torch.cuda.synchronize()
-    n = per_round or max(len(sets), 4)
-    res = []
-    for _ in range(rounds):
+def _time_gpu(torch, fn, sets, rounds=5, per_round=None, warmup_s=1.5, sample_ms=100.0):
+    """Median per-launch ms over `rounds` samples of back-to-back launches
+    (HIP events), after `warmup_s` seconds of launches; each sample holds
+    enough launches (a multiple of the buffer sets, at least `per_round`) to
+    last `sample_ms` (ref bench/harness.cpp:158-288 for the protocol)."""
+    def window(n):
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record()
@@ -51,8 +49,20 @@ def _time_gpu(torch, fn, sets, rounds=5, per_round=None):
             fn(sets[i % len(sets)])
         b.record()
         torch.cuda.synchronize()
-        res.append(a.elapsed_time(b) / n)
-    return statistics.median(res)
+        return a.elapsed_time(b)
+
+    n = max(per_round or 1, len(sets))
+    start = time.perf_counter()
+    while True:                       # warm-up, sizing the sample as it goes
+        ms = window(n)
+        if time.perf_counter() - start >= warmup_s:
+            break
+        if ms < sample_ms:
+            n = min(n * 2, 1 << 20)
+    while ms < sample_ms and n < (1 << 20):
+        n = max(n + len(sets), int(n * sample_ms / max(ms, 1e-3) * 1.1))
+        ms = window(n)
+    return statistics.median(window(n) / n for _ in range(rounds))
 
 
 def _time_cpu(fn, reps=3):
@@ -400,9 +410,13 @@ def run(f, torch, dev, path, only=None):
         from flint_amd.flint_lib import Gpt2
 
         L_, S_, T_ = 12, 8, 1024
-        # The fused attention unless FLINT_FLASH=0 (read when the model is created).
-        flash = os.environ.get("FLINT_FLASH", "1") != "0"
-        model = Gpt2(f, L_, H, C, T_, V, VP, S_, T_, backward=True)
+        for flash in (False, True):
+            train_step(Gpt2, L_, S_, T_, flash)
+
+    def train_step(Gpt2, L_, S_, T_, flash):
+        # flint_gpt2_create's model (the reference's sequence: stored scores
+        # and probabilities), then flint_gpt2_create_fused's.
+        model = Gpt2(f, L_, H, C, T_, V, VP, S_, T_, backward=True, fused=flash)
         g = torch.Generator().manual_seed(5)
         for name, addr, rows, cols in model.parameters():
             if name.endswith(("ln_1.weight", "ln_2.weight")) or name == "ln_f.weight":

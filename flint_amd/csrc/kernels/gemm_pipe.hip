@@ -143,28 +143,30 @@ constexpr bool is_bias_store(Store st) {
 }
 // Two-stage tiles with 64-deep steps read fragments two sub-steps ahead (four
 // fragment buffers) where the accumulators and buffers fit in 320 registers;
-// their bias then waits in LDS (4 KB, 1 KB per wave) instead of registers.
-__host__ __device__ constexpr bool pipe_look2(int bm, int bn, int s, int bk) {
+// their bias then waits in LDS (1 KB per wave) instead of registers. nw is the
+// workgroup's wave count: 4 (one wave per SIMD) or 8 (two).
+__host__ __device__ constexpr bool pipe_look2(int bm, int bn, int s, int bk, int nw = 4) {
     const int wn = pipe_waves_n(bn);
-    const int fm = bm / (4 / wn) / 32, fn = bn / wn / 32;
+    const int fm = bm / (nw / wn) / 32, fn = bn / wn / 32;
     return s == 2 && bk == 64 && fm * fn * 16 + 16 * (fm + fn) <= 320;
 }
-__host__ __device__ constexpr size_t pipe_bias_lds(int bm, int bn, int s, int bk, Store st) {
-    return pipe_look2(bm, bn, s, bk) && is_bias_store(st) ? 4096 : 0;
+__host__ __device__ constexpr size_t pipe_bias_lds(int bm, int bn, int s, int bk, Store st,
+                                                   int nw = 4) {
+    return pipe_look2(bm, bn, s, bk, nw) && is_bias_store(st) ? 1024 * size_t(nw) : 0;
 }
 // Whether a configuration stages its epilogue compactly (see PipeEpi).
-template <int BM, int BN, int S, int BK, Store ST>
+template <int BM, int BN, int S, int BK, Store ST, int NW = 4>
 constexpr bool pipe_compact() {
     using E = PipeEpi<BN / pipe_waves_n(BN), ST>;
-    return size_t(S) * (BM + BN) * BK * 2 + 4 * size_t(E::kHalves) * 2 +
-               pipe_bias_lds(BM, BN, S, BK, ST) >
+    return size_t(S) * (BM + BN) * BK * 2 + NW * size_t(E::kHalves) * 2 +
+               pipe_bias_lds(BM, BN, S, BK, ST, NW) >
            kPipeMaxLds;
 }
-template <int BM, int BN, int S, int BK, Layout L, Store ST>
+template <int BM, int BN, int S, int BK, Layout L, Store ST, int NW = 4>
 constexpr size_t pipe_lds_bytes() {
-    using E = PipeEpi<BN / pipe_waves_n(BN), ST, pipe_compact<BM, BN, S, BK, ST>()>;
-    return size_t(S) * (BM + BN) * BK * 2 + 4 * size_t(E::kHalves) * 2 +
-           pipe_bias_lds(BM, BN, S, BK, ST);
+    using E = PipeEpi<BN / pipe_waves_n(BN), ST, pipe_compact<BM, BN, S, BK, ST, NW>()>;
+    return size_t(S) * (BM + BN) * BK * 2 + NW * size_t(E::kHalves) * 2 +
+           pipe_bias_lds(BM, BN, S, BK, ST, NW);
 }
 
 // Tiles of one slice at or below the diagonal of a causal NT output: row
@@ -193,8 +195,12 @@ __device__ inline void map_tile_causal(const TileArgs& t, unsigned id, int bm, i
     *tn = rest;
 }
 
-template <int BM, int BN, int S, int BK, Layout L, Store ST>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// NW waves per workgroup: 4 (one per SIMD, 256 threads) or 8 (two per SIMD,
+// 512 threads, each wave half the rows of the 4-wave tile's): the same tile
+// and LDS stages, with twice the waves issuing the direct-to-LDS loads and
+// two instruction streams per SIMD.
+template <int BM, int BN, int S, int BK, Layout L, Store ST, int NW>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 gemm_pipe(Operands op, TileArgs ta) {
     // The host pass only needs a kernel to emit a launch stub for; the buffer
     // resource builtins below exist on the device side only.
@@ -203,10 +209,14 @@ gemm_pipe(Operands op, TileArgs ta) {
     static_assert(kCausalZeroSpan % BM == 0 && kCausalZeroSpan % BK == 0,
                   "causal tiles must stay inside the softmax's zero span");
     constexpr int NS = BK / 16;                 // k16 sub-steps per k-step
+    static_assert(NW == 4 || NW == 8, "waves per workgroup");
     constexpr int WAVES_N = pipe_waves_n(BN);
-    constexpr int WTM = BM / (4 / WAVES_N), WTN = BN / WAVES_N;
+    constexpr int WTM = BM / (NW / WAVES_N), WTN = BN / WAVES_N;
     constexpr int FM = WTM / 32, FN = WTN / 32;
-    constexpr int IA = BM * BK / 2048, IB = BN * BK / 2048;   // 1 KB loads per thread per step
+    // 1 KB loads per wave per step (each operand's stage is BM (BN) rows of
+    // BK halves, 1 KB a load, spread over NW waves).
+    static_assert(BM * BK % (512 * NW) == 0 && BN * BK % (512 * NW) == 0, "whole loads per wave");
+    constexpr int IA = BM * BK / (512 * NW), IB = BN * BK / (512 * NW);
     constexpr int PER = IA + IB;
     // A step's loads: POST of them in the sub-step after the barrier, the rest
     // PRE at a time in the NS - 1 sub-steps before the next one. With two
@@ -236,14 +246,14 @@ gemm_pipe(Operands op, TileArgs ta) {
     using WFrag = std::conditional_t<kWM, TrFrag, f16x8>;
     constexpr bool kBias =
         ST == Store::kBias || ST == Store::kBiasGelu || ST == Store::kBiasResidual;
-    using E = PipeEpi<WTN, ST, pipe_compact<BM, BN, S, BK, ST>()>;
+    using E = PipeEpi<WTN, ST, pipe_compact<BM, BN, S, BK, ST, NW>()>;
     constexpr int kStageHalves = S * (BM + BN) * BK;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "whole 32 x 32 blocks per wave");
-    static_assert(pipe_lds_bytes<BM, BN, S, BK, L, ST>() <= kPipeMaxLds, "LDS");
+    static_assert(pipe_lds_bytes<BM, BN, S, BK, L, ST, NW>() <= kPipeMaxLds, "LDS");
     static_assert((S - 2) * PER + PER < 64, "vmcnt range");
     // Buffer stores per wave per tile, bias loads per wave per tile.
     constexpr int kStores = FM * E::kSubs * E::kPerLane * E::kPasses;
-    constexpr bool kLook2 = pipe_look2(BM, BN, S, BK);
+    constexpr bool kLook2 = pipe_look2(BM, BN, S, BK, NW);
     constexpr bool kBiasLds = kBias && kLook2;
     // Bias loads per wave per tile: FN * 4 into registers, or one 1 KB load
     // into the wave's LDS bias block.
@@ -251,7 +261,7 @@ gemm_pipe(Operands op, TileArgs ta) {
     // The residual is loaded into registers at tile start where it fits in
     // 128 VGPRs (128 x 192: 96), so that its latency hides under the k-loop.
     constexpr int kResAll = FM * E::kSubs * E::kPerLane;
-    constexpr bool kResEarly = ST == Store::kBiasResidual && kResAll <= 32;
+    constexpr bool kResEarly = ST == Store::kBiasResidual && kResAll <= (NW == 4 ? 32 : 8);
     // dGELU's pre: the first staged block's chunks load at tile start, and
     // each later block's while the block before it is stored, so that no
     // block waits out a load's full latency.
@@ -261,7 +271,7 @@ gemm_pipe(Operands op, TileArgs ta) {
     // One LDS object for everything: with a second one, the compiler's LDS-DMA
     // alias tracking put a vmcnt(0) in front of every fragment read.
     __shared__ __attribute__((aligned(16)))
-    _Float16 lds[kStageHalves + 4 * E::kHalves + pipe_bias_lds(BM, BN, S, BK, ST) / 2];
+    _Float16 lds[kStageHalves + NW * E::kHalves + pipe_bias_lds(BM, BN, S, BK, ST, NW) / 2];
     auto stage = [&](int st) { return lds + st * (BM + BN) * BK; };
 
     const int tid = threadIdx.x;
@@ -349,14 +359,14 @@ gemm_pipe(Operands op, TileArgs ta) {
         return t;
     };
 
-    // Instruction u = q * 4 + wave of an operand fills LDS bytes
+    // Instruction u = q * NW + wave of an operand fills LDS bytes
     // [u KB, u KB + 1 KB) of its region; lane l writes bytes l * 16 .. + 16.
     // voff: the lane's byte offset in the global operand for k = 0 (the
     // k-step goes in the scalar offset).
     const int a_ld = kXM ? m : K;
     const int b_ld = kWM ? n : K;
     auto lane_voff = [&](int q, int rows, bool kmajor, int ld) {
-        const int u = q * 4 + wave;
+        const int u = q * NW + wave;
         if (kmajor) {
             const int p = u * 1024 + lane * 16;       // byte in the [32][rows] tile
             const int r = p / (rows * 2);             // k within the step
@@ -419,7 +429,7 @@ gemm_pipe(Operands op, TileArgs ta) {
     };
     auto issue_q = [&](const Issue& is, int q) {
         const bool xq = q < IA;
-        const int u = (xq ? q : q - IA) * 4 + wave;
+        const int u = (xq ? q : q - IA) * NW + wave;
         lds_half* dst = (lds_half*)(stage(is.st) + (xq ? 0 : BM * BK) + u * 512);
         // Row-major: k0 halves into every row. k-major: in the resource's base.
         const bool kmajor = xq ? kXM : kWM;
@@ -538,7 +548,7 @@ gemm_pipe(Operands op, TileArgs ta) {
         // Bias of this lane's columns, for the epilogue: buffer loads with the
         // resource ending at n (columns past it read 0), FN * 4 of them per wave.
         f32x4 bias[kBias ? FN : 1][4];
-        float* const bias_lds = reinterpret_cast<float*>(lds + kStageHalves + 4 * E::kHalves) +
+        float* const bias_lds = reinterpret_cast<float*>(lds + kStageHalves + NW * E::kHalves) +
                                 wave * 256;
         if constexpr (kBiasLds) {
             // One load puts columns col0 .. col0 + 255 of the bias in this
@@ -869,15 +879,21 @@ gemm_pipe(Operands op, TileArgs ta) {
 
 struct PipeConfig {
     int bm, bn, stages, bk;
+    int waves = 4;   // per workgroup: 4, or 8 (two per SIMD; NT layouts only)
+
+    bool same(const PipeConfig& o) const {
+        return bm == o.bm && bn == o.bn && stages == o.stages && bk == o.bk && waves == o.waves;
+    }
 };
 
 constexpr PipeConfig kPipeConfigs[] = {
     {256, 256, 3, 32}, {256, 192, 4, 32}, {128, 192, 4, 32}, {256, 64, 4, 32},
-    {128, 192, 3, 64}, {256, 128, 3, 64}, {256, 256, 2, 64}, {256, 192, 2, 64}};
+    {128, 192, 3, 64}, {256, 128, 3, 64}, {256, 256, 2, 64}, {256, 192, 2, 64},
+    {256, 192, 2, 64, 8}};
 
 // The "gemm_pipe" override: "0" routes every call to gemm.hip's kernels;
-// "bm,bn,stages[,bk]" forces one of kPipeConfigs (tests and tuning sweeps;
-// bk defaults to 32).
+// "bm,bn,stages[,bk[,waves]]" forces one of kPipeConfigs (tests and tuning
+// sweeps; bk defaults to 32, waves to 4).
 bool pipe_forced(PipeConfig* out, bool* disabled) {
     *disabled = false;
     const char* e = tuning(Tune::kGemmPipe);
@@ -888,10 +904,11 @@ bool pipe_forced(PipeConfig* out, bool* disabled) {
     }
     PipeConfig c{};
     c.bk = 32;
-    const int got = std::sscanf(e, "%d,%d,%d,%d", &c.bm, &c.bn, &c.stages, &c.bk);
-    if (got != 3 && got != 4) return false;
+    c.waves = 4;
+    const int got = std::sscanf(e, "%d,%d,%d,%d,%d", &c.bm, &c.bn, &c.stages, &c.bk, &c.waves);
+    if (got < 3) return false;
     for (const PipeConfig& k : kPipeConfigs) {
-        if (k.bm == c.bm && k.bn == c.bn && k.stages == c.stages && k.bk == c.bk) {
+        if (k.same(c)) {
             *out = c;
             return true;
         }
@@ -906,15 +923,16 @@ size_t lds_bytes(const PipeConfig& c, Store st) {
     const int wtn = c.bn / pipe_waves_n(c.bn), per = f32 && st != Store::kDGelu ? 4 : 8,
               rows = f32 ? 16 : 32;
     const size_t stages = size_t(c.stages) * (c.bm + c.bn) * c.bk * 2 +
-                          pipe_bias_lds(c.bm, c.bn, c.stages, c.bk, st);
-    const size_t staging = 4 * size_t(rows) * (wtn + per) * (f32 ? 4 : 2);
+                          pipe_bias_lds(c.bm, c.bn, c.stages, c.bk, st, c.waves);
+    const size_t staging = size_t(c.waves) * rows * (wtn + per) * (f32 ? 4 : 2);
     return stages + staging <= kPipeMaxLds ? stages + staging : stages + staging / 2;
 }
 
 // Whether a configuration can run an epilogue over k: it fits in LDS and k is
-// whole k-steps.
-bool usable(const PipeConfig& c, Store st, size_t k) {
-    return lds_bytes(c, st) <= kPipeMaxLds && k % size_t(c.bk) == 0;
+// whole k-steps; the 8-wave configuration serves the NT layout only.
+bool usable(const PipeConfig& c, Store st, size_t k, Layout l) {
+    return lds_bytes(c, st) <= kPipeMaxLds && k % size_t(c.bk) == 0 &&
+           (c.waves == 4 || l == Layout::kNT);
 }
 
 // Relative throughput per unit of tile area, measured on the GPT-2 shapes at
@@ -925,6 +943,12 @@ bool usable(const PipeConfig& c, Store st, size_t k) {
 // operands are k-major, whole lines at either depth; there the 64-deep steps
 // gain from half the barriers, most in 128 x 192 tiles.
 double pipe_eff(const PipeConfig& c, Store st) {
+    // The 8-wave tile: same bits as the 4-wave 256 x 192 x 2 x 64; faster only
+    // for plain NT products of many tile rounds (logits 8192 x 50304 x 768:
+    // 632.6 -> 608.0 us, same process, five rounds); slower at two rounds with
+    // an epilogue (MLP up + GELU 53.9 -> 58.1 us). pick_pipe admits it only
+    // for plain NT products of at least kPipe8MinRounds rounds.
+    if (c.waves == 8) return 1.04;
     if (c.bn == 64) return 0.55;
     // Two stages: worth it for 256 x 192 outside TN (MLP up 59 -> 56 us,
     // dGELU 77 -> 74 us); 256 x 256 measured no better than at 32-deep steps.
@@ -941,14 +965,17 @@ double pipe_eff(const PipeConfig& c, Store st) {
 // The macro-tile: whole waves of tiles over the CUs weigh most (a K = 768
 // tile is short, so a partial last wave costs nearly a full one); among equal
 // wave counts the larger tile needs fewer bytes per FLOP.
-PipeConfig pick_pipe(size_t m, size_t n, size_t k, size_t slices, int cus, Store st) {
+constexpr double kPipe8MinRounds = 8.0;
+
+PipeConfig pick_pipe(size_t m, size_t n, size_t k, size_t slices, int cus, Store st, Layout l) {
     PipeConfig best = kPipeConfigs[0];
     double best_cost = 1e300;
     for (const PipeConfig& c : kPipeConfigs) {
-        if (!usable(c, st, k)) continue;
+        if (!usable(c, st, k, l)) continue;
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn) *
                              double(slices);
         const double rounds = std::ceil(tiles / cus);
+        if (c.waves == 8 && (st != Store::kNone || rounds < kPipe8MinRounds)) continue;
         const double cost = rounds * double(c.bm) * double(c.bn) / pipe_eff(c, st);
         if (cost < best_cost * 0.999) {
             best_cost = cost;
@@ -968,13 +995,11 @@ void plan_tn(size_t m, size_t n, size_t k, int max_splits, int cus, bool accumul
              const PipeConfig* only, PipeConfig* best_c, int* best_s) {
     const Store st = Store::kTn;
     double best = 1e300;
-    *best_c = only != nullptr ? *only : pick_pipe(m, n, k, 1, cus, st);
+    *best_c = only != nullptr ? *only : pick_pipe(m, n, k, 1, cus, st, Layout::kTN);
     *best_s = 1;
     for (const PipeConfig& c : kPipeConfigs) {
-        if (!usable(c, st, k)) continue;
-        if (only != nullptr && (c.bm != only->bm || c.bn != only->bn ||
-                                c.stages != only->stages || c.bk != only->bk))
-            continue;
+        if (!usable(c, st, k, Layout::kTN)) continue;
+        if (only != nullptr && !c.same(*only)) continue;
         const double eff = pipe_eff(c, st);
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn);
         for (int sp = 1; sp <= max_splits; ++sp) {
@@ -1020,22 +1045,25 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     size_t gx = std::min(total, size_t(cus));
     if (gx >= 8) gx -= gx % 8;
     const dim3 grid(unsigned(gx), 1, 1);
-#define FLINT_PIPE_CASE(BM_, BN_, S_, BK_)                                                     \
-    if constexpr (pipe_lds_bytes<BM_, BN_, S_, BK_, L, ST>() <= kPipeMaxLds) {                 \
-        if (c.bm == BM_ && c.bn == BN_ && c.stages == S_ && c.bk == BK_) {                     \
-            hipLaunchKernelGGL((gemm_pipe<BM_, BN_, S_, BK_, L, ST>), grid, dim3(256), 0,      \
-                               stream, op, ta);                                                \
+#define FLINT_PIPE_CASE(BM_, BN_, S_, BK_, NW_)                                                \
+    if constexpr (pipe_lds_bytes<BM_, BN_, S_, BK_, L, ST, NW_>() <= kPipeMaxLds) {            \
+        if (c.same(PipeConfig{BM_, BN_, S_, BK_, NW_})) {                                      \
+            hipLaunchKernelGGL((gemm_pipe<BM_, BN_, S_, BK_, L, ST, NW_>), grid,               \
+                               dim3(NW_ * 64), 0, stream, op, ta);                             \
             return hipGetLastError();                                                          \
         }                                                                                      \
     }
-    FLINT_PIPE_CASE(256, 256, 3, 32)
-    FLINT_PIPE_CASE(256, 192, 4, 32)
-    FLINT_PIPE_CASE(128, 192, 4, 32)
-    FLINT_PIPE_CASE(256, 64, 4, 32)
-    FLINT_PIPE_CASE(128, 192, 3, 64)
-    FLINT_PIPE_CASE(256, 128, 3, 64)
-    FLINT_PIPE_CASE(256, 256, 2, 64)
-    FLINT_PIPE_CASE(256, 192, 2, 64)
+    FLINT_PIPE_CASE(256, 256, 3, 32, 4)
+    FLINT_PIPE_CASE(256, 192, 4, 32, 4)
+    FLINT_PIPE_CASE(128, 192, 4, 32, 4)
+    FLINT_PIPE_CASE(256, 64, 4, 32, 4)
+    FLINT_PIPE_CASE(128, 192, 3, 64, 4)
+    FLINT_PIPE_CASE(256, 128, 3, 64, 4)
+    FLINT_PIPE_CASE(256, 256, 2, 64, 4)
+    FLINT_PIPE_CASE(256, 192, 2, 64, 4)
+    if constexpr (L == Layout::kNT) {
+        FLINT_PIPE_CASE(256, 192, 2, 64, 8)
+    }
 #undef FLINT_PIPE_CASE
     return hipErrorInvalidValue;
 }
@@ -1101,7 +1129,7 @@ hipError_t launch_gemm_pipe_tn(void* y, const void* x, const void* w, size_t m, 
     int sp = 1;
     bool disabled = false;
     PipeConfig forced;
-    const bool force = pipe_forced(&forced, &disabled) && usable(forced, Store::kTn, k);
+    const bool force = pipe_forced(&forced, &disabled) && usable(forced, Store::kTn, k, Layout::kTN);
     plan_tn(m, n, k, workspace != nullptr ? max_splits : 1, cus, accumulate,
             force ? &forced : nullptr, &c, &sp);
     const size_t len = ((k + sp - 1) / sp + c.bk - 1) / c.bk * c.bk;
@@ -1169,7 +1197,7 @@ hipError_t launch_gemm_pipe(GemmLayout gl, Epilogue e, void* y, const void* x, c
     const Store st = store_of(e, l);
     PipeConfig c;
     bool disabled = false;
-    if (!pipe_forced(&c, &disabled) || !usable(c, st, k)) c = pick_pipe(m, n, k, slices, cus, st);
+    if (!pipe_forced(&c, &disabled) || !usable(c, st, k, l)) c = pick_pipe(m, n, k, slices, cus, st, l);
     switch (l) {
     case Layout::kNT: return dispatch_pipe<Layout::kNT>(c, st, op, slices, split_len, cus, stream);
     case Layout::kNN: return dispatch_pipe<Layout::kNN>(c, st, op, slices, split_len, cus, stream);

@@ -155,4 +155,10 @@ __device__ __forceinline__ h8 pack8(const float (&v)[8]) {
     return h;
 }
 
+// Streaming access for the row passes, which read each input byte and write
+// each output byte once per launch: the nt bit marks the lines as the first
+// to leave the caches.
+__device__ __forceinline__ h8 load_stream(const h8* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void store_stream(h8* p, const h8& v) { __builtin_nontemporal_store(v, p); }
+
 }  // namespace flint

@@ -637,7 +637,7 @@ causal_softmax_forward(h8* __restrict__ p, const h8* __restrict__ s, size_t rows
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int c = lane + i * 64;
-            if (c < visible_chunks) raw[r][i] = s[row * chunks + c];
+            if (c < visible_chunks) raw[r][i] = load_stream(s + row * chunks + c);
         }
     }
 #pragma unroll
@@ -717,8 +717,8 @@ causal_softmax_backward(h8* ds, const h8* __restrict__ p, const h8* dp, size_t r
     for (int i = 0; i < 2; ++i) {
         const int c = lane + i * 64;
         if (c < visible_chunks) {
-            unpack8(p[row * chunks + c], pv[i]);
-            unpack8(dp[row * chunks + c], dv[i]);
+            unpack8(load_stream(p + row * chunks + c), pv[i]);
+            unpack8(load_stream(dp + row * chunks + c), dv[i]);
             const int vis = min(t + 1 - c * 8, 8);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
@@ -740,9 +740,9 @@ causal_softmax_backward(h8* ds, const h8* __restrict__ p, const h8* dp, size_t r
                     const float diff = sub_rn(sub_rn(dv[i][j], d.sum), d.error);
                     o[j] = j < vis ? mul_rn(mul_rn(pv[i][j], diff), scale) : 0.0f;
                 }
-                ds[row * chunks + c] = pack8(o);
+                store_stream(ds + row * chunks + c, pack8(o));
             } else {
-                ds[row * chunks + c] = h8{};
+                store_stream(ds + row * chunks + c, h8{});
             }
         }
     }
@@ -804,7 +804,7 @@ softmax_cross_entropy(h8* __restrict__ dlogits, float* __restrict__ row_loss,
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
         const int c = tid + i * THREADS;
-        raw[i] = c < vocab_chunks ? lr[c] : h8(neg_inf);
+        raw[i] = c < vocab_chunks ? load_stream(lr + c) : h8(neg_inf);
     }
     if (last_count < 8 && last >= tid && (last - tid) % THREADS == 0) {
         const int i = (last - tid) / THREADS;
@@ -898,9 +898,9 @@ softmax_cross_entropy(h8* __restrict__ dlogits, float* __restrict__ row_loss,
                 o[j] = c * 8 + j < vocab ? mul_rn(p, scale) : 0.0f;
             }
         }
-        dr[c] = pack8(o);
+        store_stream(dr + c, pack8(o));
     }
-    for (int c = vocab_chunks + tid; c < chunks; c += THREADS) dr[c] = h8{};
+    for (int c = vocab_chunks + tid; c < chunks; c += THREADS) store_stream(dr + c, h8{});
 }
 
 }  // namespace

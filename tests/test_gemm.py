@@ -269,9 +269,11 @@ def test_deterministic(flint, cuda):
 PIPE_CONFIGS = ["256,256,3", "256,192,4", "128,192,4", "256,64,4", "128,192,3,64", "256,128,3,64",
                 "256,256,2,64", "256,192,2,64"]
 PIPE_SHAPES = [(300, 200, 64), (4315, 4600, 96), (1100, 968, 448)]
+# The NT layout also has an 8-wave configuration (two waves per SIMD).
+NT_PIPE_CONFIGS = PIPE_CONFIGS + ["256,192,2,64,8"]
 
 
-@pytest.mark.parametrize("cfg", PIPE_CONFIGS)
+@pytest.mark.parametrize("cfg", NT_PIPE_CONFIGS)
 @pytest.mark.parametrize("m,n,k", PIPE_SHAPES)
 @pytest.mark.parametrize("epi", ["none", "bias", "gelu", "residual"])
 def test_nt_pipe_forced(flint, cuda, tune, cfg, m, n, k, epi):
@@ -307,7 +309,7 @@ def test_nt_pipe_forced(flint, cuda, tune, cfg, m, n, k, epi):
         assert rel_err(y.cpu(), r + (s + b)) <= TOL
 
 
-@pytest.mark.parametrize("cfg", PIPE_CONFIGS)
+@pytest.mark.parametrize("cfg", NT_PIPE_CONFIGS)
 def test_nt_batched_pipe_forced(flint, cuda, tune, cfg):
     tune("gemm_pipe", cfg)
     batches, m, n, k = 5, 264, 200, 64
@@ -451,7 +453,8 @@ def _assert_guards(name, buf, off, count):
 GUARD_CASES = ["nt", "nt_bias", "nt_bias_gelu", "nt_bias_residual", "nn", "nn_dgelu", "tn", "tn_acc"]
 
 
-@pytest.mark.parametrize("force", [None, "128,192,3,64", "256,128,3,64", "256,256,3", "256,64,4"])
+@pytest.mark.parametrize("force", [None, "128,192,3,64", "256,128,3,64", "256,256,3", "256,64,4",
+                                   "256,192,2,64,8"])
 @pytest.mark.parametrize("offset", [16, 32, 48])
 @pytest.mark.parametrize("case", GUARD_CASES)
 def test_outputs_stay_inside_their_buffers(flint, cuda, tune, case, offset, force):
