@@ -195,12 +195,14 @@ __device__ inline void map_tile_causal(const TileArgs& t, unsigned id, int bm, i
     *tn = rest;
 }
 
-// NW waves per workgroup: 4 (one per SIMD, 256 threads) or 8 (two per SIMD,
-// 512 threads, each wave half the rows of the 4-wave tile's): the same tile
-// and LDS stages, with twice the waves issuing the direct-to-LDS loads and
-// two instruction streams per SIMD.
-template <int BM, int BN, int S, int BK, Layout L, Store ST, int NW>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
+// NW MFMA waves per workgroup: 4 (one per SIMD) or 8 (two per SIMD, each
+// wave half the rows of the 4-wave tile's): the same tile and LDS stages.
+// LD adds four loader waves (one more per SIMD) that issue every operand load
+// and join the k-step barriers, so that twice the waves issue the direct-to-
+// LDS loads while the LDS fragment reads stay those of four MFMA waves.
+template <int BM, int BN, int S, int BK, Layout L, Store ST, int NW, bool LD = false>
+__global__ void __launch_bounds__((NW + (LD ? 4 : 0)) * 64)
+__attribute__((amdgpu_waves_per_eu((NW + (LD ? 4 : 0)) / 4, (NW + (LD ? 4 : 0)) / 4)))
 gemm_pipe(Operands op, TileArgs ta) {
     // The host pass only needs a kernel to emit a launch stub for; the buffer
     // resource builtins below exist on the device side only.
@@ -210,13 +212,16 @@ gemm_pipe(Operands op, TileArgs ta) {
                   "causal tiles must stay inside the softmax's zero span");
     constexpr int NS = BK / 16;                 // k16 sub-steps per k-step
     static_assert(NW == 4 || NW == 8, "waves per workgroup");
+    static_assert(!LD || NW == 4, "loader waves serve four MFMA waves");
     constexpr int WAVES_N = pipe_waves_n(BN);
     constexpr int WTM = BM / (NW / WAVES_N), WTN = BN / WAVES_N;
     constexpr int FM = WTM / 32, FN = WTN / 32;
-    // 1 KB loads per wave per step (each operand's stage is BM (BN) rows of
-    // BK halves, 1 KB a load, spread over NW waves).
-    static_assert(BM * BK % (512 * NW) == 0 && BN * BK % (512 * NW) == 0, "whole loads per wave");
-    constexpr int IA = BM * BK / (512 * NW), IB = BN * BK / (512 * NW);
+    // The waves that issue the operand loads: the MFMA waves, or the loaders.
+    constexpr int NLW = LD ? 4 : NW;
+    // 1 KB loads per loading wave per step (each operand's stage is BM (BN)
+    // rows of BK halves, 1 KB a load, spread over NLW waves).
+    static_assert(BM * BK % (512 * NLW) == 0 && BN * BK % (512 * NLW) == 0, "whole loads per wave");
+    constexpr int IA = BM * BK / (512 * NLW), IB = BN * BK / (512 * NLW);
     constexpr int PER = IA + IB;
     // A step's loads: POST of them in the sub-step after the barrier, the rest
     // PRE at a time in the NS - 1 sub-steps before the next one. With two
@@ -261,7 +266,8 @@ gemm_pipe(Operands op, TileArgs ta) {
     // The residual is loaded into registers at tile start where it fits in
     // 128 VGPRs (128 x 192: 96), so that its latency hides under the k-loop.
     constexpr int kResAll = FM * E::kSubs * E::kPerLane;
-    constexpr bool kResEarly = ST == Store::kBiasResidual && kResAll <= (NW == 4 ? 32 : 8);
+    constexpr bool kResEarly =
+        ST == Store::kBiasResidual && kResAll <= (NW == 4 && !LD ? 32 : 8);
     // dGELU's pre: the first staged block's chunks load at tile start, and
     // each later block's while the block before it is stored, so that no
     // block waits out a load's full latency.
@@ -277,6 +283,9 @@ gemm_pipe(Operands op, TileArgs ta) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool loader = LD && wave >= NW;
+    // The wave's index among the waves that load (its loads' positions).
+    const int lw = LD ? wave - NW : wave;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int m = op.m, n = op.n, K = op.k;
     const bool split = ST == Store::kTn && op.partials != nullptr;
@@ -359,14 +368,14 @@ gemm_pipe(Operands op, TileArgs ta) {
         return t;
     };
 
-    // Instruction u = q * NW + wave of an operand fills LDS bytes
+    // Instruction u = q * NLW + lw of an operand fills LDS bytes
     // [u KB, u KB + 1 KB) of its region; lane l writes bytes l * 16 .. + 16.
     // voff: the lane's byte offset in the global operand for k = 0 (the
     // k-step goes in the scalar offset).
     const int a_ld = kXM ? m : K;
     const int b_ld = kWM ? n : K;
     auto lane_voff = [&](int q, int rows, bool kmajor, int ld) {
-        const int u = q * NW + wave;
+        const int u = q * NLW + lw;
         if (kmajor) {
             const int p = u * 1024 + lane * 16;       // byte in the [32][rows] tile
             const int r = p / (rows * 2);             // k within the step
@@ -428,8 +437,9 @@ gemm_pipe(Operands op, TileArgs ta) {
         }
     };
     auto issue_q = [&](const Issue& is, int q) {
+        if (LD && !loader) return;   // with loader waves, only they load operands
         const bool xq = q < IA;
-        const int u = (xq ? q : q - IA) * NW + wave;
+        const int u = (xq ? q : q - IA) * NLW + lw;
         lds_half* dst = (lds_half*)(stage(is.st) + (xq ? 0 : BM * BK) + u * 512);
         // Row-major: k0 halves into every row. k-major: in the resource's base.
         const bool kmajor = xq ? kXM : kWM;
@@ -509,7 +519,43 @@ gemm_pipe(Operands op, TileArgs ta) {
         }
     };
 
+    // Loader waves: the operand loads of every k-step, S steps ahead of the
+    // MFMAs, and one barrier per k-step in step with the MFMA waves'. Before
+    // the barrier of step g (which frees step g's stage) step g + 1 has
+    // landed; right after it step g + S goes into that stage. Past the last
+    // step the stream reloads the last step into stages nobody reads.
+    if constexpr (LD) {
+        if (loader) {
+            Issue ld;
+            ld.tile = 0;
+            ld.st = 0;
+            rsrc_of(ld);
+#pragma unroll
+            for (int j = 0; j < S; ++j) {
+#pragma unroll
+                for (int q = 0; q < PER; ++q) issue_q(ld, q);
+                advance(ld);
+            }
+            wait_vmcnt<(S - 1) * PER>();
+            block_sync();
+            for (int i = 0; i < n_tiles; ++i) {
+                const Tile t = tile(i);
+                const int steps = (t.k_end - t.k_begin) / BK;
+                for (int s = 0; s < steps; ++s) {
+                    wait_vmcnt<(S - 2) * PER>();
+                    block_sync();
+#pragma unroll
+                    for (int q = 0; q < PER; ++q) issue_q(ld, q);
+                    advance(ld);
+                }
+            }
+            wait_vmcnt<0>();
+            return;
+        }
+    }
+
     // Prologue: stream steps 0 .. S-2 and the post-barrier share of step S-1.
+    // (MFMA waves of a loader kernel issue none of these loads.)
     Issue cur;
     cur.tile = 0;
     cur.st = 0;
@@ -641,11 +687,13 @@ gemm_pipe(Operands op, TileArgs ta) {
             // has landed; at a tile's first step the previous tile's stores
             // and this tile's bias (and residual) loads, issued after it, may
             // stay in flight. After the barrier stage st is free.
-            if (s == 0) {
-                if (i == 0) wait_vm_lgkm0<cap63(kEarlyLoads)>();
-                else wait_vm_lgkm0<cap63(kEarlyLoads + kStores)>();
-            } else {
-                wait_vm_lgkm0<0>();
+            if constexpr (!LD) {
+                if (s == 0) {
+                    if (i == 0) wait_vm_lgkm0<cap63(kEarlyLoads)>();
+                    else wait_vm_lgkm0<cap63(kEarlyLoads + kStores)>();
+                } else {
+                    wait_vm_lgkm0<0>();
+                }
             }
             block_sync();
             const int st_next = st + 1 == S ? 0 : st + 1;
@@ -688,11 +736,13 @@ gemm_pipe(Operands op, TileArgs ta) {
             // retires in issue order), so they may stay in flight too: the
             // stores drain while the MFMAs run. After the barrier nobody reads
             // stage st any more.
-            if (s <= S - (kAllPost ? 2 : 3)) {
-                if (i == 0) wait_vm_lgkm0<cap63((S - 2) * PER + kEarlyLoads)>();
-                else wait_vm_lgkm0<cap63((S - 2) * PER + kEarlyLoads + kStores)>();
-            } else {
-                wait_vm_lgkm0<(S - 2) * PER>();
+            if constexpr (!LD) {
+                if (s <= S - (kAllPost ? 2 : 3)) {
+                    if (i == 0) wait_vm_lgkm0<cap63((S - 2) * PER + kEarlyLoads)>();
+                    else wait_vm_lgkm0<cap63((S - 2) * PER + kEarlyLoads + kStores)>();
+                } else {
+                    wait_vm_lgkm0<(S - 2) * PER>();
+                }
             }
             block_sync();
             const int st_next = st + 1 == S ? 0 : st + 1;
@@ -719,7 +769,8 @@ gemm_pipe(Operands op, TileArgs ta) {
         // are added, so that they take no registers across the epilogue (the
         // next tile's first fragments are live there).
         if constexpr (kBiasLds) {
-            if (steps == 1) wait_vmcnt<0>();
+            // With loader waves nothing else of this wave's retires it first.
+            if (LD || steps == 1) wait_vmcnt<0>();
         }
         auto bias_of = [&](int ii, int g4) {
             if constexpr (kBiasLds)
@@ -879,21 +930,23 @@ gemm_pipe(Operands op, TileArgs ta) {
 
 struct PipeConfig {
     int bm, bn, stages, bk;
-    int waves = 4;   // per workgroup: 4, or 8 (two per SIMD; NT layouts only)
+    int waves = 4;         // MFMA waves: 4, or 8 (two per SIMD; NT layouts only)
+    int loaders = 0;       // 1: four more waves issue the operand loads
 
     bool same(const PipeConfig& o) const {
-        return bm == o.bm && bn == o.bn && stages == o.stages && bk == o.bk && waves == o.waves;
+        return bm == o.bm && bn == o.bn && stages == o.stages && bk == o.bk &&
+               waves == o.waves && loaders == o.loaders;
     }
 };
 
 constexpr PipeConfig kPipeConfigs[] = {
     {256, 256, 3, 32}, {256, 192, 4, 32}, {128, 192, 4, 32}, {256, 64, 4, 32},
     {128, 192, 3, 64}, {256, 128, 3, 64}, {256, 256, 2, 64}, {256, 192, 2, 64},
-    {256, 192, 2, 64, 8}};
+    {256, 192, 2, 64, 8}, {128, 192, 3, 64, 4, 1}, {256, 128, 3, 64, 4, 1}};
 
 // The "gemm_pipe" override: "0" routes every call to gemm.hip's kernels;
-// "bm,bn,stages[,bk[,waves]]" forces one of kPipeConfigs (tests and tuning
-// sweeps; bk defaults to 32, waves to 4).
+// "bm,bn,stages[,bk[,waves[,loaders]]]" forces one of kPipeConfigs (tests and
+// tuning sweeps; bk defaults to 32, waves to 4, loaders to 0).
 bool pipe_forced(PipeConfig* out, bool* disabled) {
     *disabled = false;
     const char* e = tuning(Tune::kGemmPipe);
@@ -905,7 +958,9 @@ bool pipe_forced(PipeConfig* out, bool* disabled) {
     PipeConfig c{};
     c.bk = 32;
     c.waves = 4;
-    const int got = std::sscanf(e, "%d,%d,%d,%d,%d", &c.bm, &c.bn, &c.stages, &c.bk, &c.waves);
+    c.loaders = 0;
+    const int got = std::sscanf(e, "%d,%d,%d,%d,%d,%d", &c.bm, &c.bn, &c.stages, &c.bk, &c.waves,
+                                &c.loaders);
     if (got < 3) return false;
     for (const PipeConfig& k : kPipeConfigs) {
         if (k.same(c)) {
@@ -943,6 +998,14 @@ bool usable(const PipeConfig& c, Store st, size_t k, Layout l) {
 // operands are k-major, whole lines at either depth; there the 64-deep steps
 // gain from half the barriers, most in 128 x 192 tiles.
 double pipe_eff(const PipeConfig& c, Store st) {
+    // Loader waves pay where the MFMA waves' own stream is the bottleneck:
+    // TN, whose fragments come from transposing LDS reads with a full LDS
+    // wait per sub-step (3072 x 768 x 8192: 64.2 -> 55.2 us, 768 x 3072: 60.2
+    // -> 55.1, 2304 x 768: 46.0 -> 43.6, same process; the logits dW 50304 x
+    // 768 x 8192: 744 -> 671 us at 256 x 128). NT and NN ran slower with them
+    // (MLP down 46.4 -> 54.8 us), so there they are taken only when forced.
+    if (c.loaders)
+        return st == Store::kTn || st == Store::kTnHalf ? 1.0 : 0.01;
     // The 8-wave tile: same bits as the 4-wave 256 x 192 x 2 x 64; faster only
     // for plain NT products of many tile rounds (logits 8192 x 50304 x 768:
     // 632.6 -> 608.0 us, same process, five rounds); slower at two rounds with
@@ -1000,6 +1063,8 @@ void plan_tn(size_t m, size_t n, size_t k, int max_splits, int cus, bool accumul
     for (const PipeConfig& c : kPipeConfigs) {
         if (!usable(c, st, k, Layout::kTN)) continue;
         if (only != nullptr && !c.same(*only)) continue;
+        // The 256 x 128 loader tile won only on the logits' size of output.
+        if (only == nullptr && c.loaders && c.bm == 256 && double(m) * double(n) < 8e6) continue;
         const double eff = pipe_eff(c, st);
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn);
         for (int sp = 1; sp <= max_splits; ++sp) {
@@ -1045,24 +1110,26 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     size_t gx = std::min(total, size_t(cus));
     if (gx >= 8) gx -= gx % 8;
     const dim3 grid(unsigned(gx), 1, 1);
-#define FLINT_PIPE_CASE(BM_, BN_, S_, BK_, NW_)                                                \
+#define FLINT_PIPE_CASE(BM_, BN_, S_, BK_, NW_, LD_)                                           \
     if constexpr (pipe_lds_bytes<BM_, BN_, S_, BK_, L, ST, NW_>() <= kPipeMaxLds) {            \
-        if (c.same(PipeConfig{BM_, BN_, S_, BK_, NW_})) {                                      \
-            hipLaunchKernelGGL((gemm_pipe<BM_, BN_, S_, BK_, L, ST, NW_>), grid,               \
-                               dim3(NW_ * 64), 0, stream, op, ta);                             \
+        if (c.same(PipeConfig{BM_, BN_, S_, BK_, NW_, LD_})) {                                 \
+            hipLaunchKernelGGL((gemm_pipe<BM_, BN_, S_, BK_, L, ST, NW_, LD_ != 0>), grid,     \
+                               dim3((NW_ + 4 * LD_) * 64), 0, stream, op, ta);                 \
             return hipGetLastError();                                                          \
         }                                                                                      \
     }
-    FLINT_PIPE_CASE(256, 256, 3, 32, 4)
-    FLINT_PIPE_CASE(256, 192, 4, 32, 4)
-    FLINT_PIPE_CASE(128, 192, 4, 32, 4)
-    FLINT_PIPE_CASE(256, 64, 4, 32, 4)
-    FLINT_PIPE_CASE(128, 192, 3, 64, 4)
-    FLINT_PIPE_CASE(256, 128, 3, 64, 4)
-    FLINT_PIPE_CASE(256, 256, 2, 64, 4)
-    FLINT_PIPE_CASE(256, 192, 2, 64, 4)
+    FLINT_PIPE_CASE(256, 256, 3, 32, 4, 0)
+    FLINT_PIPE_CASE(256, 192, 4, 32, 4, 0)
+    FLINT_PIPE_CASE(128, 192, 4, 32, 4, 0)
+    FLINT_PIPE_CASE(256, 64, 4, 32, 4, 0)
+    FLINT_PIPE_CASE(128, 192, 3, 64, 4, 0)
+    FLINT_PIPE_CASE(256, 128, 3, 64, 4, 0)
+    FLINT_PIPE_CASE(256, 256, 2, 64, 4, 0)
+    FLINT_PIPE_CASE(256, 192, 2, 64, 4, 0)
+    FLINT_PIPE_CASE(128, 192, 3, 64, 4, 1)
+    FLINT_PIPE_CASE(256, 128, 3, 64, 4, 1)
     if constexpr (L == Layout::kNT) {
-        FLINT_PIPE_CASE(256, 192, 2, 64, 8)
+        FLINT_PIPE_CASE(256, 192, 2, 64, 8, 0)
     }
 #undef FLINT_PIPE_CASE
     return hipErrorInvalidValue;
