@@ -411,7 +411,8 @@ def run(f, torch, dev, path, only=None):
 
         L_, S_, T_ = 12, 8, 1024
         for flash in (False, True):
-            train_step(Gpt2, L_, S_, T_, flash)
+            if want("gpt2_124m_train_step " + ("fused" if flash else "stored")):
+                train_step(Gpt2, L_, S_, T_, flash)
 
     def train_step(Gpt2, L_, S_, T_, flash):
         # flint_gpt2_create's model (the reference's sequence: stored scores
@@ -508,7 +509,7 @@ def run(f, torch, dev, path, only=None):
         section_ce()
     if want("flint_attention_forward") or want("flint_attention_backward"):
         section_attention()
-    if want("gpt2_124m_train_step"):
+    if want("gpt2_124m_train_step stored") or want("gpt2_124m_train_step fused"):
         section_gpt2()
     if any(want(x) for x in ("flint_copy", "flint_fp32_to_fp16", "flint_heads_split",
                              "flint_heads_merge", "flint_embedding")):
