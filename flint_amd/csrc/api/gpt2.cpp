@@ -453,6 +453,18 @@ int attn_zero_span(size_t length, size_t head_width) {
     return taken ? flint::kCausalZeroSpan : 0;
 }
 
+// Scores and softmax (forward), dP and the softmax backward: one fused launch
+// each where attention_stored.hip takes the shape and the batched product
+// would run on the pipeline (whose MFMA chain and rounding the fused kernels
+// reproduce); the "attn_scores" override "0" runs the two launches instead.
+// The same bits either way.
+bool attn_scores_fused(size_t length, size_t head_width) {
+    return !flint::tuning_off(flint::Tune::kAttnScores) &&
+           flint::attn_scores_fusable(length, head_width) &&
+           flint::gemm_pipe_eligible(flint::GemmLayout::kNT, flint::Epilogue::kScale, length,
+                                     length, head_width);
+}
+
 flint_status attn_softmax_forward(void* p, const void* s, size_t batches, size_t length,
                                   size_t head_width, flint_stream st) {
     FLINT_HIP_CHECK(flint::launch_causal_softmax_forward(p, s, batches * length, length,
@@ -507,9 +519,15 @@ flint_status forward_layer(const flint_gpt2& m, const Layer& L, flint_stream st)
                                      st));
         void* const qkv_parts[] = {s.q, s.k, s.v};
         FLINT_TRY(attn_heads3(m.qkv, qkv_parts, c.sequences, c.length, c.heads, hw, false, st));
-        FLINT_TRY(attn_nt(m.scores, s.q, s.k, m.head_batches, c.length, c.length, hw,
-                          score_scale(hw), st));
-        FLINT_TRY(attn_softmax_forward(s.p, m.scores, m.head_batches, c.length, hw, st));
+        if (attn_scores_fused(c.length, hw)) {
+            FLINT_HIP_CHECK(flint::launch_attn_scores_softmax(
+                s.p, s.q, s.k, m.head_batches, c.length, hw, score_scale(hw), flint::to_hip(st),
+                attn_zero_span(c.length, hw)));
+        } else {
+            FLINT_TRY(attn_nt(m.scores, s.q, s.k, m.head_batches, c.length, c.length, hw,
+                              score_scale(hw), st));
+            FLINT_TRY(attn_softmax_forward(s.p, m.scores, m.head_batches, c.length, hw, st));
+        }
         FLINT_TRY(attn_nn(m.heads_out, s.p, s.v, m.head_batches, c.length, hw, c.length, st));
         FLINT_TRY(flint_heads_merge(s.attn_out, m.heads_out, c.sequences, c.length, c.heads, hw,
                                     w, 0, st));
@@ -636,8 +654,14 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
     } else {
         FLINT_TRY(flint_heads_split(m.heads_out, m.dh, c.sequences, len, c.heads, hw, w, 0, st));
         FLINT_TRY(attn_tn(m.dv, s.p, m.heads_out, nb, len, hw, len, st));
-        FLINT_TRY(attn_nt(m.scores, m.heads_out, s.v, nb, len, len, hw, 1.0f, st));
-        FLINT_TRY(attn_softmax_backward(m.scores, s.p, m.scores, nb, len, hw, st));
+        if (attn_scores_fused(len, hw)) {
+            FLINT_HIP_CHECK(flint::launch_attn_scores_softmax_backward(
+                m.scores, s.p, m.heads_out, s.v, nb, len, hw, score_scale(hw), flint::to_hip(st),
+                attn_zero_span(len, hw)));
+        } else {
+            FLINT_TRY(attn_nt(m.scores, m.heads_out, s.v, nb, len, len, hw, 1.0f, st));
+            FLINT_TRY(attn_softmax_backward(m.scores, s.p, m.scores, nb, len, hw, st));
+        }
         FLINT_TRY(attn_nn(m.dq, m.scores, s.k, nb, len, hw, len, st));
         FLINT_TRY(attn_tn(m.dk, m.scores, s.q, nb, len, hw, len, st));
         void* const parts[] = {m.dq, m.dk, m.dv};

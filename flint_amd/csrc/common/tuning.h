@@ -22,6 +22,8 @@ enum class Tune : int {
     kEmbTogether,   // "0": the position gradient in its own launch
     kAttnOrder,     // "0": the fused attention's plain longest-first order
     kPartialsCpl,   // 1 | 2 | 4: bias-gradient partials' columns per lane
+    kAttnScores,    // "0": the model's scores and dP through the batched product
+                    // and the softmax passes (no fused scores + softmax)
     kCount
 };
 

@@ -189,6 +189,21 @@ hipError_t launch_causal_softmax_forward(void* p, const void* s, size_t rows, si
 hipError_t launch_causal_softmax_backward(void* ds, const void* p, const void* dp, size_t rows,
                                           size_t length, float scale, hipStream_t stream,
                                           int zero_span = 0);
+// The model's stored-probability attention with the scores (dP) kept out of
+// memory (attention_stored.hip): P = causal_softmax_forward(RN16(scale q kᵀ))
+// and dS = causal_softmax_backward(p, RN16(dout vᵀ)), the same bits as the
+// batched NT product followed by the softmax pass. Head width 64, lengths a
+// multiple of 32 up to 1,024 (attn_scores_fusable); q, k, v, dout are
+// [batches][length][64], p and ds [batches][length][length] (ds not aliasing
+// p); zero_span as for the softmax passes.
+bool attn_scores_fusable(size_t length, size_t head_width);
+hipError_t launch_attn_scores_softmax(void* p, const void* q, const void* k, size_t batches,
+                                      size_t length, size_t head_width, float scale,
+                                      hipStream_t stream, int zero_span);
+hipError_t launch_attn_scores_softmax_backward(void* ds, const void* p, const void* dout,
+                                               const void* v, size_t batches, size_t length,
+                                               size_t head_width, float scale,
+                                               hipStream_t stream, int zero_span);
 hipError_t launch_softmax_cross_entropy(void* dlogits, void* row_loss, const void* logits,
                                         const void* targets, float scale, size_t rows,
                                         size_t vocab, size_t cols, hipStream_t stream);

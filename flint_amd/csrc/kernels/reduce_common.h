@@ -148,10 +148,20 @@ __device__ __forceinline__ void unpack8(const h8& h, float (&v)[8]) {
     for (int i = 0; i < 8; ++i) v[i] = float(h[i]);
 }
 
+// RN16 of a value already rounded to FP32, as the reference's
+// __float2half_rn of a float. The empty asm hides how x was formed, so that
+// the compiler cannot fold the multiply or fma that produced it into a
+// v_fma_mix with one rounding straight to FP16 (different in the last bit now
+// and then, and chosen per value by the instruction selector).
+__device__ __forceinline__ _Float16 to_half(float x) {
+    asm("" : "+v"(x));
+    return _Float16(x);
+}
+
 __device__ __forceinline__ h8 pack8(const float (&v)[8]) {
     h8 h;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = _Float16(v[i]);
+    for (int i = 0; i < 8; ++i) h[i] = to_half(v[i]);
     return h;
 }
 

@@ -27,6 +27,7 @@
 #include "common/tuning.h"
 #include "kernels/kernels.h"
 #include "kernels/reduce_common.h"
+#include "kernels/softmax_rows.h"
 #include "kernels/split_sum.h"
 
 #pragma clang fp contract(off)
@@ -109,8 +110,8 @@ layernorm_forward_regs(_Float16* __restrict__ y, float* __restrict__ mean,
                 h4 o;
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    o[j] = _Float16(__builtin_fmaf(mul_rn(sub_rn(v[i][j], mu), rs), ga[i][j],
-                                                   be[i][j]));
+                    o[j] = to_half(__builtin_fmaf(mul_rn(sub_rn(v[i][j], mu), rs), ga[i][j],
+                                                  be[i][j]));
                 yr[g] = o;
             }
         }
@@ -145,7 +146,7 @@ layernorm_forward_any(_Float16* __restrict__ y, float* __restrict__ mean,
     const float rs = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(var, eps)));
     _Float16* yr = y + row * cols;
     for (int c = lane; c < cols; c += 64)
-        yr[c] = _Float16(__builtin_fmaf(mul_rn(sub_rn(xr[c], mu), rs), gamma[c], beta[c]));
+        yr[c] = to_half(__builtin_fmaf(mul_rn(sub_rn(xr[c], mu), rs), gamma[c], beta[c]));
     if (lane == 0) {
         mean[row] = mu;
         rstd[row] = rs;
@@ -509,7 +510,7 @@ __device__ __forceinline__ void dx_rows(float* __restrict__ dx, const _Float16* 
             if (dx_half != nullptr) {
                 h8 hv;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) hv[j] = _Float16(o[j]);
+                for (int j = 0; j < 8; ++j) hv[j] = to_half(o[j]);
                 *reinterpret_cast<h8*>(dx_half + row * cols + p * 8) = hv;
             }
         }
@@ -592,7 +593,7 @@ layernorm_backward_dx_any(float* __restrict__ dx, const _Float16* __restrict__ d
             float v = mul_rn(rs, sub_rn(sub_rn(gv, g_mean), mul_rn(xh, gx_mean)));
             if (accumulate) v = add_rn(o[c], v);
             o[c] = v;
-            if (dx_half != nullptr) dx_half[row * cols + c] = _Float16(v);
+            if (dx_half != nullptr) dx_half[row * cols + c] = to_half(v);
         }
     }
     }
@@ -603,20 +604,12 @@ layernorm_backward_dx_any(float* __restrict__ dx, const _Float16* __restrict__ d
 constexpr int kSmRowsPerBlock = 4;   // waves per workgroup, one row group each
 constexpr int kSmRowsPerWave = 1;   // 96 x 1024: 58.6 us, against 60.3 at 2 rows and 75.1 at 4
 
-// Chunks of row t written by the causal passes: all of them, or with a zero
-// span Z, those below the end of the Z-column block holding the diagonal (the
-// model's causal GEMMs read no further; the chunks past it keep old values).
-__device__ __forceinline__ int written_chunks(int t, int chunks, int zero_span) {
-    if (zero_span == 0) return chunks;
-    const int end = (t / zero_span + 1) * (zero_span >> 3);
-    return end < chunks ? end : chunks;
-}
-
-// One wave per row of length L <= 1024: lane l holds chunks l and l + 64.
-// Row t sees columns 0..t; masked chunks are written as zeros and never read.
-// The zeros go out with the row's values, after its reductions: stored first,
-// under the loads, they made the pass slower (60.5 -> 64.7 us at 96 x 1024,
-// and 74.2 -> 76.5 for the backward pass).
+// One wave per row of length L <= 1024: lane l holds chunks l and l + 64
+// (the row arithmetic is softmax_rows.h's, shared with the fused attention
+// passes). Row t sees columns 0..t; masked chunks are written as zeros and
+// never read. The zeros go out with the row's values, after its reductions:
+// stored first, under the loads, they made the pass slower (60.5 -> 64.7 us
+// at 96 x 1024, and 74.2 -> 76.5 for the backward pass).
 // A wave takes R consecutive rows and loads all of them before the first
 // reduction, so R times the bytes are in flight; each row's arithmetic is
 // the one-row order.
@@ -642,66 +635,18 @@ causal_softmax_forward(h8* __restrict__ p, const h8* __restrict__ s, size_t rows
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-    const size_t row = row0 + r;
-    if (row >= rows) break;
-    const int t = int(row % size_t(length));
-    const int visible_chunks = (t >> 3) + 1;
-    h8* pr = p + row * chunks;
-    float v[2][8];
-    float mx = -__builtin_huge_valf();
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = lane + i * 64;
-        if (c < visible_chunks) {
-            unpack8(raw[r][i], v[i]);
-            const int vis = min(t + 1 - c * 8, 8);
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (j < vis) mx = fmaxf(mx, v[i][j]);
-        }
-    }
-    mx = max_reduce<64>(mx);
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = lane + i * 64;
-        if (c < visible_chunks) {
-            const int vis = min(t + 1 - c * 8, 8);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                v[i][j] = j < vis ? exp_accurate(v[i][j] - mx) : 0.0f;
-                sum = add_rn(sum, v[i][j]);
-            }
-        }
-    }
-    sum = sum_reduce<64>(sum);
-    const float inv = __fdiv_rn(1.0f, sum);
-    const int written = written_chunks(t, chunks, zero_span);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = lane + i * 64;
-        if (c < written) {
-            if (c < visible_chunks) {
-                // Masked columns of the diagonal chunk are selected as +0, not
-                // formed as 0 / sum: a row whose sum is NaN keeps them +0.
-                const int vis = min(t + 1 - c * 8, 8);
-                float o[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = j < vis ? mul_rn(v[i][j], inv) : 0.0f;
-                pr[c] = pack8(o);
-            } else {
-                pr[c] = h8{};
-            }
-        }
-    }
+        const size_t row = row0 + r;
+        if (row >= rows) break;
+        const int t = int(row % size_t(length));
+        softmax_forward_row(p + row * chunks, raw[r], t, chunks, lane, zero_span);
     }
     }
 }
 
 // ds = scale * p * ((dp - D.sum) - D.error) over the visible columns, with D
-// the compensated sum of the exact products p * dp. Each lane reads all of
-// its dp before the butterfly and writes only its own chunks afterwards, so
-// ds may alias dp.
+// the compensated sum of the exact products p * dp (softmax_backward_row).
+// Each lane reads all of its dp before the butterfly and writes only its own
+// chunks afterwards, so ds may alias dp.
 __global__ void __launch_bounds__(256)
 causal_softmax_backward(h8* ds, const h8* __restrict__ p, const h8* dp, size_t rows, int length,
                         float scale, int zero_span) {
@@ -712,40 +657,15 @@ causal_softmax_backward(h8* ds, const h8* __restrict__ p, const h8* dp, size_t r
     const int t = int(row % size_t(length));
     const int visible_chunks = (t >> 3) + 1;
     float pv[2][8], dv[2][8];
-    Comp d;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int c = lane + i * 64;
         if (c < visible_chunks) {
             unpack8(load_stream(p + row * chunks + c), pv[i]);
             unpack8(load_stream(dp + row * chunks + c), dv[i]);
-            const int vis = min(t + 1 - c * 8, 8);
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (j < vis) comp_add(d, mul_rn(pv[i][j], dv[i][j]));
         }
     }
-    d = comp_reduce<64>(d);
-    if (!__builtin_isfinite(d.sum)) d.error = 0.0f;
-    const int written = written_chunks(t, chunks, zero_span);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = lane + i * 64;
-        if (c < written) {
-            if (c < visible_chunks) {
-                const int vis = min(t + 1 - c * 8, 8);
-                float o[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float diff = sub_rn(sub_rn(dv[i][j], d.sum), d.error);
-                    o[j] = j < vis ? mul_rn(mul_rn(pv[i][j], diff), scale) : 0.0f;
-                }
-                store_stream(ds + row * chunks + c, pack8(o));
-            } else {
-                store_stream(ds + row * chunks + c, h8{});
-            }
-        }
-    }
+    softmax_backward_row(ds + row * chunks, pv, dv, t, chunks, lane, scale, zero_span);
     }
 }
 

@@ -293,6 +293,36 @@ def test_causal_attention_products_change_no_bits(flint, cuda, tune, length, for
     assert bool(torch.isfinite(full[1]).all())
 
 
+@pytest.mark.parametrize("length", [1024, 320, 32])
+@pytest.mark.parametrize("causal", ["1", "0"], ids=["causal", "full"])
+def test_fused_scores_and_softmax_change_no_bits(flint, cuda, tune, length, causal):
+    """The stored-probability model computes P = softmax(scale q kᵀ) and
+    dS = softmax_backward(p, dO vᵀ) in one launch each, the scores kept in
+    LDS; the two-launch sequence (attn_scores=0: the batched product, then
+    the softmax pass) must give the same bits in every output and gradient,
+    with the causal products or the full ones."""
+    cfg = dict(layers=1, heads=4, width=256, block_size=1024, vocab=1000, padded_vocab=1024)
+    sequences = 2
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=13, trained=True)
+    params = {n: t.half().float() for n, t in params.items()}
+    idx, tgt = _tokens(cfg, sequences, length, 14)
+    if causal == "0":
+        tune("attn_causal", "0")
+    tune("attn_scores", "0")
+    two = _run(flint, cfg, sequences, length, params, idx, tgt, 0.25)
+    tune("attn_scores", None)
+    one = _run(flint, cfg, sequences, length, params, idx, tgt, 0.25)
+    for x, y in zip(two[:3], one[:3]):
+        assert torch.equal(x.view(torch.int32) if x.dtype == torch.float32 else x,
+                           y.view(torch.int32) if y.dtype == torch.float32 else y)
+    for n in two[3]:
+        assert torch.equal(two[3][n].view(torch.int32), one[3][n].view(torch.int32)), n
+    assert two[4] == one[4]
+    assert bool(torch.isfinite(one[1]).all())
+
+
 WIDE = dict(layers=1, heads=4, width=256, block_size=1024, vocab=1000, padded_vocab=1024)
 
 
