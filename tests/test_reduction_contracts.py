@@ -313,6 +313,25 @@ def test_softmax_backward_is_within_an_ulp_of_the_correct_rounding(flint, cuda, 
     assert bool((_bits(ds)[:, ~_mask(t)] == 0).all())
 
 
+def test_softmax_backward_signed_zeros_are_ieee(flint, cuda):
+    """A zero probability times a negative (dp - D) is -0, as the reference's
+    FP32 arithmetic then __float2half_rn gives; a positive one +0. (A
+    mixed-precision fma with a +0 addend would turn the -0 into +0.)"""
+    t = 16
+    p = torch.zeros((1, t, t), dtype=torch.float16, device=cuda)
+    dp = torch.zeros_like(p)
+    for r in range(t):
+        p[0, r, 0] = 1.0           # D = dp[r, 0] = 1 for every row
+        dp[0, r, 0] = 1.0
+        dp[0, r, 1:r + 1] = torch.where(torch.arange(1, r + 1, device=cuda) % 2 == 0, 3.0, -2.0)
+    ds = _backward(flint, p, dp, 0.5).cpu()
+    for r in range(t):
+        for c in range(1, r + 1):
+            want_negative = c % 2 == 1   # dp - D = -3 < 0 on odd columns
+            assert float(ds[0, r, c]) == 0.0
+            assert bool(torch.signbit(ds[0, r, c])) == want_negative, (r, c)
+
+
 @pytest.mark.parametrize("target", ["p", "dp"])
 @pytest.mark.parametrize("t", [72, 1016])
 def test_softmax_backward_non_finite_values_reach_only_their_rows(flint, cuda, target, t):
