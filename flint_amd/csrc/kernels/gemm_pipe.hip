@@ -675,6 +675,7 @@ gemm_pipe(Operands op, TileArgs ta) {
             advance(nxt);
           if constexpr (kLook2) {
             static_assert(NS == 4, "two-stage tiles take 64-deep steps");
+            static_assert(FM * FN >= FM + FN, "a slot for every fragment read");
             // Sub-steps 0 and 1: read sub-steps 2 and 3 of this step.
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
@@ -727,6 +728,11 @@ gemm_pipe(Operands op, TileArgs ta) {
                     if (q % kLoadEvery == kLoadEvery - 1 && q / kLoadEvery < PRE && li < PER)
                         issue_q(cur, li);
                 });
+                // Fragments without an MFMA slot (a wave tile of one 32-row
+                // block: fewer MFMAs than fragments per sub-step).
+#pragma unroll
+                for (int q = FM * FN; q < FM + FN; ++q)
+                    read_one(st, kk + 1, q, xf[(kk + 1) & 1], wf[(kk + 1) & 1]);
             }
             // The next step has landed once only the loads of the S - 2 steps
             // after it remain outstanding. For the first S - 2 steps of a tile
@@ -753,6 +759,8 @@ gemm_pipe(Operands op, TileArgs ta) {
                 if (q % kLoadEvery == kLoadEvery - 1 && q / kLoadEvery < POST)
                     issue_q(nxt, q / kLoadEvery);
             });
+#pragma unroll
+            for (int q = FM * FN; q < FM + FN; ++q) read_one(st_next, 0, q, xf[0], wf[0]);
             if constexpr (kAllPost) {
 #pragma unroll
                 for (int q = FM * FN / kLoadEvery; q < POST; ++q) issue_q(nxt, q);
@@ -942,7 +950,7 @@ struct PipeConfig {
 constexpr PipeConfig kPipeConfigs[] = {
     {256, 256, 3, 32}, {256, 192, 4, 32}, {128, 192, 4, 32}, {256, 64, 4, 32},
     {128, 192, 3, 64}, {256, 128, 3, 64}, {256, 256, 2, 64}, {256, 192, 2, 64},
-    {256, 192, 2, 64, 8}, {128, 192, 3, 64, 4, 1}, {256, 128, 3, 64, 4, 1}};
+    {256, 192, 2, 64, 8}, {128, 192, 3, 64, 4, 1}, {256, 128, 3, 64, 4, 1}, {128, 64, 4, 32}};
 
 // The "gemm_pipe" override: "0" routes every call to gemm.hip's kernels;
 // "bm,bn,stages[,bk[,waves[,loaders]]]" forces one of kPipeConfigs (tests and
@@ -1030,11 +1038,22 @@ double pipe_eff(const PipeConfig& c, Store st) {
 // wave counts the larger tile needs fewer bytes per FLOP.
 constexpr double kPipe8MinRounds = 8.0;
 
-PipeConfig pick_pipe(size_t m, size_t n, size_t k, size_t slices, int cus, Store st, Layout l) {
+PipeConfig pick_pipe(size_t m, size_t n, size_t k, size_t slices, int cus, Store st, Layout l,
+                     bool causal = false) {
     PipeConfig best = kPipeConfigs[0];
     double best_cost = 1e300;
     for (const PipeConfig& c : kPipeConfigs) {
         if (!usable(c, st, k, l)) continue;
+        // 64-wide tiles only for outputs that narrow: elsewhere a round of
+        // them costs as much as one of the wider tiles and loads far more.
+        if (c.bn == 64 && n > 64) continue;
+        // 128 x 64 only for the causal attention products, whose tiles' work
+        // grows with their row block: three rounds of the shorter tiles
+        // balance better than one and a half of 256 x 64 (the default GPT-2
+        // model's step 13.78 -> 13.60 ms, same process, the same bits). On
+        // full products 256 x 64 is faster (96 x 1024 x 64 x 1024 NN: 41.8
+        // against 44.8 us).
+        if (c.bm == 128 && c.bn == 64 && !causal) continue;
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn) *
                              double(slices);
         const double rounds = std::ceil(tiles / cus);
@@ -1063,6 +1082,7 @@ void plan_tn(size_t m, size_t n, size_t k, int max_splits, int cus, bool accumul
     for (const PipeConfig& c : kPipeConfigs) {
         if (!usable(c, st, k, Layout::kTN)) continue;
         if (only != nullptr && !c.same(*only)) continue;
+        if (only == nullptr && c.bn == 64 && (n > 64 || c.bm == 128)) continue;
         // The 256 x 128 loader tile won only on the logits' size of output.
         if (only == nullptr && c.loaders && c.bm == 256 && double(m) * double(n) < 8e6) continue;
         const double eff = pipe_eff(c, st);
@@ -1122,6 +1142,7 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     FLINT_PIPE_CASE(256, 192, 4, 32, 4, 0)
     FLINT_PIPE_CASE(128, 192, 4, 32, 4, 0)
     FLINT_PIPE_CASE(256, 64, 4, 32, 4, 0)
+    FLINT_PIPE_CASE(128, 64, 4, 32, 4, 0)
     FLINT_PIPE_CASE(128, 192, 3, 64, 4, 0)
     FLINT_PIPE_CASE(256, 128, 3, 64, 4, 0)
     FLINT_PIPE_CASE(256, 256, 2, 64, 4, 0)
@@ -1264,7 +1285,8 @@ hipError_t launch_gemm_pipe(GemmLayout gl, Epilogue e, void* y, const void* x, c
     const Store st = store_of(e, l);
     PipeConfig c;
     bool disabled = false;
-    if (!pipe_forced(&c, &disabled) || !usable(c, st, k, l)) c = pick_pipe(m, n, k, slices, cus, st, l);
+    if (!pipe_forced(&c, &disabled) || !usable(c, st, k, l))
+        c = pick_pipe(m, n, k, slices, cus, st, l, op.causal != 0);
     switch (l) {
     case Layout::kNT: return dispatch_pipe<Layout::kNT>(c, st, op, slices, split_len, cus, stream);
     case Layout::kNN: return dispatch_pipe<Layout::kNN>(c, st, op, slices, split_len, cus, stream);
