@@ -465,6 +465,36 @@ bool attn_scores_fused(size_t length, size_t head_width) {
                                      length, head_width);
 }
 
+// The stored path without head copies: q, k and v are read as heads views of
+// the qkv projection (written into the layer's q, k, v buffers, which then lie
+// back to back as one [rows][3 width] block), O, dQ, dK and dV are written as
+// heads views of their token rows, and dO is read as one. The split / merge
+// launches of the sequence (flint_heads_split / _merge) go away; the products
+// and their bits do not change. Taken where the fused scores take the shape,
+// the pipeline takes both batched products, and the buffers lie back to back
+// (one allocation whose 256-byte grid the head buffers' size is on).
+bool attn_views(const flint_gpt2& m, const Saved& s) {
+    using flint::GemmLayout;
+    const size_t len = m.cfg.length, hw = m.head_width;
+    const size_t heads_bytes = m.head_batches * len * hw * 2;
+    const char* q = static_cast<const char*>(s.q);
+    return s.k == q + heads_bytes && s.v == q + 2 * heads_bytes &&
+           attn_scores_fused(len, hw) &&
+           flint::gemm_batched_causal_taken(GemmLayout::kNN, len, hw, len) &&
+           flint::gemm_batched_causal_taken(GemmLayout::kTN, len, hw, len);
+}
+
+// Slices of [tokens][cols] rows as heads: slice b = sequence b / heads, head
+// b % heads, at column (b % heads) * head_width.
+flint::HeadView heads_view(const flint_gpt2& m, size_t cols) {
+    flint::HeadView v;
+    v.heads = int(m.cfg.heads);
+    v.ld = int(cols);
+    v.seq = (long long)(m.cfg.length * cols);
+    v.head = (long long)(m.head_width);
+    return v;
+}
+
 flint_status attn_softmax_forward(void* p, const void* s, size_t batches, size_t length,
                                   size_t head_width, flint_stream st) {
     FLINT_HIP_CHECK(flint::launch_causal_softmax_forward(p, s, batches * length, length,
@@ -514,6 +544,16 @@ flint_status forward_layer(const flint_gpt2& m, const Layer& L, flint_stream st)
         FLINT_HIP_CHECK(flint::launch_attention_forward(
             s.attn_out, s.lse, qkv, qkv + w, qkv + 2 * w, m.head_batches, c.length,
             score_scale(hw), flint::to_hip(st), attn_layout(m)));
+    } else if (attn_views(m, s)) {
+        auto* qkv = static_cast<_Float16*>(s.q);   // q, k, v back to back: [rows][3 width]
+        FLINT_TRY(flint_gemm_nt_bias(qkv, s.h1, L.attn.half, L.attn.b->data, rows, 3 * w, w, st));
+        const flint::HeadView qkv_v = heads_view(m, 3 * w), rows_v = heads_view(m, w);
+        FLINT_HIP_CHECK(flint::launch_attn_scores_softmax(
+            s.p, qkv, qkv + w, m.head_batches, c.length, hw, score_scale(hw), flint::to_hip(st),
+            attn_zero_span(c.length, hw), &qkv_v, &qkv_v));
+        FLINT_HIP_CHECK(flint::launch_gemm_nn_batched_views(
+            s.attn_out, s.p, qkv + 2 * w, m.head_batches, c.length, hw, c.length, qkv_v, rows_v,
+            flint::to_hip(st), attn_causal()));
     } else {
         FLINT_TRY(flint_gemm_nt_bias(m.qkv, s.h1, L.attn.half, L.attn.b->data, rows, 3 * w, w,
                                      st));
@@ -651,6 +691,22 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
         FLINT_HIP_CHECK(flint::launch_attention_backward(
             g, g + w, g + 2 * w, m.dh, qkv, qkv + w, qkv + 2 * w, s.attn_out, s.lse,
             m.attn_work, nb, len, score_scale(hw), flint::to_hip(st), attn_layout(m)));
+    } else if (attn_views(m, s)) {
+        // dO rows in dh, q, k, v in the layer's projection block; dQ, dK, dV
+        // straight into the qkv gradient's columns.
+        auto* g = static_cast<_Float16*>(m.qkv);
+        auto* qkv = static_cast<_Float16*>(s.q);
+        const flint::HeadView qkv_v = heads_view(m, 3 * w), rows_v = heads_view(m, w);
+        const hipStream_t hs = flint::to_hip(st);
+        FLINT_HIP_CHECK(flint::launch_gemm_tn_batched_views(g + 2 * w, s.p, m.dh, nb, len, hw, len,
+                                                            rows_v, qkv_v, hs, attn_causal()));
+        FLINT_HIP_CHECK(flint::launch_attn_scores_softmax_backward(
+            m.scores, s.p, m.dh, qkv + 2 * w, nb, len, hw, score_scale(hw), hs,
+            attn_zero_span(len, hw), &rows_v, &qkv_v));
+        FLINT_HIP_CHECK(flint::launch_gemm_nn_batched_views(g, m.scores, qkv + w, nb, len, hw, len,
+                                                            qkv_v, qkv_v, hs, attn_causal()));
+        FLINT_HIP_CHECK(flint::launch_gemm_tn_batched_views(g + w, m.scores, qkv, nb, len, hw, len,
+                                                            qkv_v, qkv_v, hs, attn_causal()));
     } else {
         FLINT_TRY(flint_heads_split(m.heads_out, m.dh, c.sequences, len, c.heads, hw, w, 0, st));
         FLINT_TRY(attn_tn(m.dv, s.p, m.heads_out, nb, len, hw, len, st));

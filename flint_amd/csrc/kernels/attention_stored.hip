@@ -24,8 +24,9 @@
 // 13.64 ms. Sixteen waves a workgroup gave 13.61 ms with a register spill in
 // the backward; four, 14.60 (slower than the two launches).
 // Head width 64, lengths a multiple of 32 up to 1,024 (the staged rows fit in
-// LDS); operands are [batches][length][64] FP16 rows, P and dS
-// [batches][length][length].
+// LDS); operands are [batches][length][64] FP16 rows, or heads views of token
+// rows (HeadView: the model reads q, k, v and dO where the projections left
+// them), P and dS [batches][length][length].
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -58,14 +59,14 @@ constexpr int kStagedHalves = kBlockRows * staged_stride(kMaxLength);
 // 16-wide k-step, k columns 8 (l / 32) .. + 8 of it (the pipeline's B
 // fragment) and likewise key rows (its A fragment); accumulator element r is
 // key 8 (r / 4) + 4 (l / 32) + r % 4 of the group for that query.
-__device__ __forceinline__ void stage_scores(_Float16* st, int stride, const _Float16* q,
-                                             const _Float16* k, int r0, float scale, int wave,
-                                             int lane) {
+__device__ __forceinline__ void stage_scores(_Float16* st, int stride, const _Float16* q, int q_ld,
+                                             const _Float16* k, int k_ld, int r0, float scale,
+                                             int wave, int lane) {
     const int fr = lane & 31, fc = lane >> 5;
     h8 qf[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-        qf[kk] = *reinterpret_cast<const h8*>(q + size_t(r0 + fr) * kHeadWidth + kk * 16 + fc * 8);
+        qf[kk] = *reinterpret_cast<const h8*>(q + size_t(r0 + fr) * q_ld + kk * 16 + fc * 8);
     const int groups = r0 / 32 + 1;
     // Every group's key fragments first, so that their loads overlap.
     h8 kf[kGroupsPerWave][4];
@@ -75,7 +76,7 @@ __device__ __forceinline__ void stage_scores(_Float16* st, int stride, const _Fl
         if (g < groups) {
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
-                kf[gi][kk] = *reinterpret_cast<const h8*>(k + size_t(g * 32 + fr) * kHeadWidth +
+                kf[gi][kk] = *reinterpret_cast<const h8*>(k + size_t(g * 32 + fr) * k_ld +
                                                           kk * 16 + fc * 8);
         }
     }
@@ -107,15 +108,15 @@ __device__ __forceinline__ void block_of(int batches, int blocks_per_head, int* 
 __global__ void __launch_bounds__(kWaves * 64)
 __attribute__((amdgpu_waves_per_eu(kWaves / 2, kWaves / 2)))
 scores_softmax(h8* __restrict__ p, const _Float16* __restrict__ q, const _Float16* __restrict__ k,
-               int batches, int length, float scale, int zero_span) {
+               HeadView qv, HeadView kv, int batches, int length, float scale, int zero_span) {
     __shared__ __attribute__((aligned(16))) _Float16 staged[kStagedHalves];
     const int wave = int(threadIdx.x >> 6), lane = int(threadIdx.x & 63);
     int b, r0;
     block_of(batches, length / kBlockRows, &b, &r0);
     const size_t head = size_t(b) * length;
     const int stride = staged_stride(length);
-    stage_scores(staged, stride, q + head * kHeadWidth, k + head * kHeadWidth, r0, scale, wave,
-                 lane);
+    stage_scores(staged, stride, q + head_view_offset(qv, b), qv.ld, k + head_view_offset(kv, b),
+                 kv.ld, r0, scale, wave, lane);
     __syncthreads();
     const int chunks = length >> 3;
     for (int i = wave; i < kBlockRows; i += kWaves) {
@@ -137,15 +138,16 @@ __global__ void __launch_bounds__(kWaves * 64)
 __attribute__((amdgpu_waves_per_eu(kWaves / 2, kWaves / 2)))
 scores_softmax_backward(h8* __restrict__ ds, const h8* __restrict__ p,
                         const _Float16* __restrict__ dout, const _Float16* __restrict__ v,
-                        int batches, int length, float scale, int zero_span) {
+                        HeadView dv_, HeadView vv, int batches, int length, float scale,
+                        int zero_span) {
     __shared__ __attribute__((aligned(16))) _Float16 staged[kStagedHalves];
     const int wave = int(threadIdx.x >> 6), lane = int(threadIdx.x & 63);
     int b, r0;
     block_of(batches, length / kBlockRows, &b, &r0);
     const size_t head = size_t(b) * length;
     const int stride = staged_stride(length);
-    stage_scores(staged, stride, dout + head * kHeadWidth, v + head * kHeadWidth, r0, 1.0f, wave,
-                 lane);
+    stage_scores(staged, stride, dout + head_view_offset(dv_, b), dv_.ld,
+                 v + head_view_offset(vv, b), vv.ld, r0, 1.0f, wave, lane);
     __syncthreads();
     const int chunks = length >> 3;
     for (int i = wave; i < kBlockRows; i += kWaves) {
@@ -172,17 +174,41 @@ bool attn_scores_fusable(size_t length, size_t head_width) {
            length % kBlockRows == 0 && length <= size_t(kMaxLength);
 }
 
+namespace {
+
+// The operand rows of each slice: a heads view, or [batches][length][64].
+HeadView rows_of(const HeadView* v, size_t length) {
+    if (v != nullptr) return *v;
+    HeadView c;
+    c.heads = 1;
+    c.ld = kHeadWidth;
+    c.seq = (long long)(length) * kHeadWidth;
+    c.head = 0;
+    return c;
+}
+
+bool launchable(size_t batches, size_t length, size_t head_width, int zero_span,
+                const HeadView& a, const HeadView& b) {
+    auto ok = [&](const HeadView& v) {
+        return v.heads > 0 && batches % size_t(v.heads) == 0 && v.ld >= kHeadWidth &&
+               v.seq >= 0 && v.head >= 0;
+    };
+    return attn_scores_fusable(length, head_width) && batches > 0 && batches <= 65535 &&
+           zero_span >= 0 && zero_span % 8 == 0 && ok(a) && ok(b);
+}
+
+}  // namespace
+
 hipError_t launch_attn_scores_softmax(void* p, const void* q, const void* k, size_t batches,
                                       size_t length, size_t head_width, float scale,
-                                      hipStream_t stream, int zero_span) {
-    if (!attn_scores_fusable(length, head_width) || batches == 0 || batches > 65535 ||
-        zero_span < 0 || zero_span % 8 != 0) {
-        return hipErrorInvalidValue;
-    }
+                                      hipStream_t stream, int zero_span, const HeadView* qv,
+                                      const HeadView* kv) {
+    const HeadView qr = rows_of(qv, length), kr = rows_of(kv, length);
+    if (!launchable(batches, length, head_width, zero_span, qr, kr)) return hipErrorInvalidValue;
     const unsigned blocks = unsigned(batches * (length / kBlockRows));
     hipLaunchKernelGGL(scores_softmax, dim3(blocks), dim3(kWaves * 64), 0, stream,
                        static_cast<h8*>(p), static_cast<const _Float16*>(q),
-                       static_cast<const _Float16*>(k), int(batches), int(length), scale,
+                       static_cast<const _Float16*>(k), qr, kr, int(batches), int(length), scale,
                        zero_span);
     return hipGetLastError();
 }
@@ -190,15 +216,15 @@ hipError_t launch_attn_scores_softmax(void* p, const void* q, const void* k, siz
 hipError_t launch_attn_scores_softmax_backward(void* ds, const void* p, const void* dout,
                                                const void* v, size_t batches, size_t length,
                                                size_t head_width, float scale,
-                                               hipStream_t stream, int zero_span) {
-    if (!attn_scores_fusable(length, head_width) || batches == 0 || batches > 65535 ||
-        zero_span < 0 || zero_span % 8 != 0) {
-        return hipErrorInvalidValue;
-    }
+                                               hipStream_t stream, int zero_span,
+                                               const HeadView* dov, const HeadView* vv) {
+    const HeadView dr = rows_of(dov, length), vr = rows_of(vv, length);
+    if (!launchable(batches, length, head_width, zero_span, dr, vr)) return hipErrorInvalidValue;
     const unsigned blocks = unsigned(batches * (length / kBlockRows));
-    hipLaunchKernelGGL(scores_softmax_backward, dim3(blocks), dim3(kWaves * 64), 0, stream, static_cast<h8*>(ds), static_cast<const h8*>(p),
-                       static_cast<const _Float16*>(dout), static_cast<const _Float16*>(v),
-                       int(batches), int(length), scale, zero_span);
+    hipLaunchKernelGGL(scores_softmax_backward, dim3(blocks), dim3(kWaves * 64), 0, stream,
+                       static_cast<h8*>(ds), static_cast<const h8*>(p),
+                       static_cast<const _Float16*>(dout), static_cast<const _Float16*>(v), dr,
+                       vr, int(batches), int(length), scale, zero_span);
     return hipGetLastError();
 }
 

@@ -930,6 +930,24 @@ hipError_t launch_gemm_nn_batched(void* y, const void* x, const void* w, size_t 
     return run<Layout::kNN, Store::kNone>(op, batches, 0, stream);
 }
 
+hipError_t launch_gemm_nn_batched_views(void* y, const void* x, const void* w, size_t batches,
+                                        size_t m, size_t n, size_t k, const HeadView& wv,
+                                        const HeadView& yv, hipStream_t stream, bool causal) {
+    if (!gemm_pipe_eligible(GemmLayout::kNN, Epilogue::kNone, m, n, k)) return hipErrorInvalidValue;
+    return launch_gemm_pipe(GemmLayout::kNN, Epilogue::kNone, y, x, w, nullptr, nullptr, 1.0f,
+                            batches, m, n, k, false, nullptr, 0, stream, causal && m == k, &wv,
+                            &yv);
+}
+
+hipError_t launch_gemm_tn_batched_views(void* y, const void* x, const void* w, size_t batches,
+                                        size_t m, size_t n, size_t k, const HeadView& wv,
+                                        const HeadView& yv, hipStream_t stream, bool causal) {
+    if (!gemm_pipe_eligible(GemmLayout::kTN, Epilogue::kNone, m, n, k)) return hipErrorInvalidValue;
+    return launch_gemm_pipe(GemmLayout::kTN, Epilogue::kNone, y, x, w, nullptr, nullptr, 1.0f,
+                            batches, m, n, k, false, nullptr, 0, stream, causal && m == k, &wv,
+                            &yv);
+}
+
 hipError_t launch_gemm_tn_batched(void* y, const void* x, const void* w, size_t batches,
                                   size_t m, size_t n, size_t k, hipStream_t stream, bool causal) {
     if (gemm_pipe_eligible(GemmLayout::kTN, Epilogue::kNone, m, n, k))

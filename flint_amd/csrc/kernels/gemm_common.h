@@ -8,6 +8,8 @@
 
 #include <cstdint>
 
+#include "kernels/kernels.h"
+
 namespace flint {
 namespace {
 
@@ -140,6 +142,8 @@ struct Operands {
     int causal;            // attention (pipeline only): the per-slice m x m
                            // operand (NT's y, NN's and TN's x) is zero, or
                            // not wanted, above its diagonal
+    HeadView wv, yv;       // batched NN / TN (pipeline only): w (k-major) and
+                           // y as heads views
 };
 
 }  // namespace

@@ -200,7 +200,11 @@ __device__ inline void map_tile_causal(const TileArgs& t, unsigned id, int bm, i
 // LD adds four loader waves (one more per SIMD) that issue every operand load
 // and join the k-step barriers, so that twice the waves issue the direct-to-
 // LDS loads while the LDS fragment reads stay those of four MFMA waves.
-template <int BM, int BN, int S, int BK, Layout L, Store ST, int NW, bool LD = false>
+// HV (batched NN / TN only): w and y are heads views (op.wv, op.yv), rows
+// op.wv.ld / op.yv.ld apart. A template flag, so that the other instances
+// keep their scalar registers: the runtime strides alone spilled SGPRs.
+template <int BM, int BN, int S, int BK, Layout L, Store ST, int NW, bool LD = false,
+          bool HV = false>
 __global__ void __launch_bounds__((NW + (LD ? 4 : 0)) * 64)
 __attribute__((amdgpu_waves_per_eu((NW + (LD ? 4 : 0)) / 4, (NW + (LD ? 4 : 0)) / 4)))
 gemm_pipe(Operands op, TileArgs ta) {
@@ -213,6 +217,8 @@ gemm_pipe(Operands op, TileArgs ta) {
     constexpr int NS = BK / 16;                 // k16 sub-steps per k-step
     static_assert(NW == 4 || NW == 8, "waves per workgroup");
     static_assert(!LD || NW == 4, "loader waves serve four MFMA waves");
+    static_assert(!HV || (L != Layout::kNT && (ST == Store::kNone || ST == Store::kTnHalf)),
+                  "heads views: batched NN / TN, FP16 outputs");
     constexpr int WAVES_N = pipe_waves_n(BN);
     constexpr int WTM = BM / (NW / WAVES_N), WTN = BN / WAVES_N;
     constexpr int FM = WTM / 32, FN = WTN / 32;
@@ -289,6 +295,11 @@ gemm_pipe(Operands op, TileArgs ta) {
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int m = op.m, n = op.n, K = op.k;
     const bool split = ST == Store::kTn && op.partials != nullptr;
+    // Row strides: k-major operands' rows are the output's columns (w's are
+    // op.wv.ld apart in a heads view); y's rows are n apart, or op.yv.ld.
+    const int a_ld = kXM ? m : K;
+    const int b_ld = kWM ? (HV ? op.wv.ld : n) : K;
+    const int y_ld = HV ? op.yv.ld : n;
     _Float16* const cst = lds + kStageHalves + wave * E::kHalves;
 
     // This workgroup's tiles: ids blockIdx.x, + gridDim.x, ... (gridDim.x is a
@@ -346,8 +357,8 @@ gemm_pipe(Operands op, TileArgs ta) {
             t.y_off = size_t(t.slice) * m * n;
         } else if (ta.slices > 1) {
             xs += size_t(t.slice) * m * K;
-            ws += size_t(t.slice) * n * K;
-            t.y_off = size_t(t.slice) * m * n;
+            ws += HV ? head_view_offset(op.wv, t.slice) : size_t(t.slice) * n * K;
+            t.y_off = HV ? head_view_offset(op.yv, t.slice) : size_t(t.slice) * m * n;
         }
         // Row-major operands: the resource ends at the tile's last valid row.
         // k-major ones: at the end of the slice's matrix.
@@ -359,8 +370,10 @@ gemm_pipe(Operands op, TileArgs ta) {
             t.a_bytes = unsigned(min(BM, m - t.m0)) * unsigned(K) * 2u;
         }
         if (kWM) {
+            // Through the last row's last column (rows b_ld apart).
             t.b = ws + t.n0;
-            t.b_bytes = unsigned((size_t(K) * n - t.n0) * 2);
+            t.b_bytes = HV ? unsigned((size_t(K - 1) * b_ld + n - t.n0) * 2)
+                           : unsigned((size_t(K) * n - t.n0) * 2);
         } else {
             t.b = ws + size_t(t.n0) * K;
             t.b_bytes = unsigned(min(BN, n - t.n0)) * unsigned(K) * 2u;
@@ -372,8 +385,6 @@ gemm_pipe(Operands op, TileArgs ta) {
     // [u KB, u KB + 1 KB) of its region; lane l writes bytes l * 16 .. + 16.
     // voff: the lane's byte offset in the global operand for k = 0 (the
     // k-step goes in the scalar offset).
-    const int a_ld = kXM ? m : K;
-    const int b_ld = kWM ? n : K;
     auto lane_voff = [&](int q, int rows, bool kmajor, int ld) {
         const int u = q * NLW + lw;
         if (kmajor) {
@@ -626,14 +637,15 @@ gemm_pipe(Operands op, TileArgs ta) {
         // chunk is whole once it starts).
         const int row_base = t.m0 + wm * WTM;
         const int col_base = t.n0 + wn * WTN;
-        const unsigned out_bytes = unsigned(size_t(m) * n * E::kOutElem);
+        const unsigned out_bytes = HV ? unsigned((size_t(m - 1) * y_ld + n) * E::kOutElem)
+                                      : unsigned(size_t(m) * n * E::kOutElem);
         auto chunk_at = [&](int j, int h, int q, int elem, int* r, int* cc) {
             const int c = q * 64 + lane;
             *r = c / E::kCpr;
             *cc = c % E::kCpr;
             const int gr = row_base + j * 32 + h * E::kRows + *r;
             const int gc = col_base + *cc * E::kPerChunk;
-            return gr < m && gc < n ? (unsigned(gr) * unsigned(n) + unsigned(gc)) * unsigned(elem)
+            return gr < m && gc < n ? (unsigned(gr) * unsigned(y_ld) + unsigned(gc)) * unsigned(elem)
                                     : 0xfffffff0u;
         };
         f32x4 res_all[kResEarly ? FM : 1][kResEarly ? E::kSubs : 1][kResEarly ? E::kPerLane : 1];
@@ -1111,6 +1123,8 @@ void plan_tn(size_t m, size_t n, size_t k, int max_splits, int cus, bool accumul
 template <Layout L, Store ST>
 hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, int split_len,
                        int cus, hipStream_t stream) {
+    constexpr bool kViews = L != Layout::kNT && (ST == Store::kNone || ST == Store::kTnHalf);
+    const bool hv = op.wv.heads != 0;
     TileArgs ta{};
     ta.tiles_m = (op.m + c.bm - 1) / c.bm;
     ta.tiles_n = (op.n + c.bn - 1) / c.bn;
@@ -1133,6 +1147,15 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
 #define FLINT_PIPE_CASE(BM_, BN_, S_, BK_, NW_, LD_)                                           \
     if constexpr (pipe_lds_bytes<BM_, BN_, S_, BK_, L, ST, NW_>() <= kPipeMaxLds) {            \
         if (c.same(PipeConfig{BM_, BN_, S_, BK_, NW_, LD_})) {                                 \
+            if constexpr (kViews) {                                                            \
+                if (hv) {                                                                      \
+                    hipLaunchKernelGGL((gemm_pipe<BM_, BN_, S_, BK_, L, ST, NW_, LD_ != 0,     \
+                                                  true>),                                      \
+                                       grid, dim3((NW_ + 4 * LD_) * 64), 0, stream, op, ta);   \
+                    return hipGetLastError();                                                  \
+                }                                                                              \
+            }                                                                                  \
+            if (hv) return hipErrorInvalidValue;                                               \
             hipLaunchKernelGGL((gemm_pipe<BM_, BN_, S_, BK_, L, ST, NW_, LD_ != 0>), grid,     \
                                dim3((NW_ + 4 * LD_) * 64), 0, stream, op, ta);                 \
             return hipGetLastError();                                                          \
@@ -1263,7 +1286,22 @@ bool gemm_pipe_eligible(GemmLayout gl, Epilogue e, size_t m, size_t n, size_t k)
 hipError_t launch_gemm_pipe(GemmLayout gl, Epilogue e, void* y, const void* x, const void* w,
                             const void* bias, void* aux, float scale, size_t slices, size_t m,
                             size_t n, size_t k, bool accumulate, void* partials, int split_len,
-                            hipStream_t stream, bool causal) {
+                            hipStream_t stream, bool causal, const HeadView* wv,
+                            const HeadView* yv) {
+    // Heads views: batched NN / TN with FP16 outputs only, every slice a
+    // whole (sequence, head) pair.
+    if (wv != nullptr || yv != nullptr) {
+        const bool ok_layout = gl != GemmLayout::kNT && e == Epilogue::kNone && slices > 1 &&
+                               split_len == 0 && partials == nullptr && !accumulate;
+        // A slice's rows, ld apart, must stay within the 32-bit buffer range.
+        auto ok_view = [&](const HeadView* v, size_t rows) {
+            return v == nullptr ||
+                   (v->heads > 0 && slices % size_t(v->heads) == 0 && v->ld >= 0 &&
+                    size_t(v->ld) >= n && v->seq >= 0 && v->head >= 0 &&
+                    ((rows - 1) * size_t(v->ld) + n) * 2 < (size_t{1} << 31));
+        };
+        if (!ok_layout || !ok_view(wv, k) || !ok_view(yv, m)) return hipErrorInvalidValue;
+    }
     int cus = 256;
     if (hipError_t err = device_cus(&cus); err != hipSuccess) return err;
     Operands op{};
@@ -1282,6 +1320,20 @@ hipError_t launch_gemm_pipe(GemmLayout gl, Epilogue e, void* y, const void* x, c
     // Causal needs the square operand, and no TN split (k-ranges of its own).
     op.causal = causal && split_len == 0 &&
                         (l == Layout::kNT ? m == n : m == k) ? 1 : 0;
+    // Both views set (heads != 0 selects the view kernels); a missing one is
+    // the plain [slices][rows][cols] layout as a view of one head.
+    if (wv != nullptr || yv != nullptr) {
+        auto plain = [](size_t rows, size_t cols) {
+            HeadView v;
+            v.heads = 1;
+            v.ld = int(cols);
+            v.seq = (long long)(rows * cols);
+            v.head = 0;
+            return v;
+        };
+        op.wv = wv != nullptr ? *wv : plain(k, n);
+        op.yv = yv != nullptr ? *yv : plain(m, n);
+    }
     const Store st = store_of(e, l);
     PipeConfig c;
     bool disabled = false;

@@ -41,10 +41,12 @@ hipError_t launch_gemm_pipe_tn(void* y, const void* x, const void* w, size_t m, 
 // causal: the per-slice m x m operand is zero above its diagonal (NT: only the
 // output's tiles at or below it are computed; NN / TN: each tile's k-range is
 // cut to where that operand can be nonzero). Requires m == n (NT) or m == k.
+struct HeadView;
 hipError_t launch_gemm_pipe(GemmLayout l, Epilogue e, void* y, const void* x, const void* w,
                             const void* bias, void* aux, float scale, size_t slices, size_t m,
                             size_t n, size_t k, bool accumulate, void* partials, int split_len,
-                            hipStream_t stream, bool causal = false);
+                            hipStream_t stream, bool causal = false,
+                            const HeadView* wv = nullptr, const HeadView* yv = nullptr);
 hipError_t launch_gemm_nn(void* y, const void* x, const void* w, const void* aux, Epilogue e,
                           size_t m, size_t n, size_t k, hipStream_t stream);
 // Number of k splits TN uses for m x n x k on this device (1 = none).
@@ -59,6 +61,20 @@ hipError_t launch_gemm_tn_split(void* y, const void* x, const void* w, size_t m,
                                 hipStream_t stream);
 hipError_t launch_tn_reduce(void* y, const void* partials, size_t m, size_t n, int splits,
                             bool accumulate, hipStream_t stream);
+// A batched operand laid out as the heads of token rows (the GPT-2 model's
+// attention): slice b is head b % heads of sequence b / heads, starting
+// (b / heads) * seq + (b % heads) * head elements in, its rows ld elements
+// apart. heads == 0: the plain [slices][rows][cols] layout.
+struct HeadView {
+    int heads = 0;
+    int ld = 0;
+    long long seq = 0, head = 0;
+};
+
+__host__ __device__ inline size_t head_view_offset(const HeadView& v, int slice) {
+    return size_t(slice / v.heads) * size_t(v.seq) + size_t(slice % v.heads) * size_t(v.head);
+}
+
 // The batched GEMMs. causal (attention inside the GPT-2 model only): x (NN,
 // TN) is zero above its diagonal per slice, or (NT) only y's entries at or
 // below the diagonal are wanted; the pipeline then skips the rest, which
@@ -73,6 +89,15 @@ hipError_t launch_gemm_nn_batched(void* y, const void* x, const void* w, size_t 
 hipError_t launch_gemm_tn_batched(void* y, const void* x, const void* w, size_t batches,
                                   size_t m, size_t n, size_t k, hipStream_t stream,
                                   bool causal = false);
+// The same on the pipeline with w (k-major) and y as heads views, for the
+// model's attention: only where gemm_batched_causal_taken says the pipeline
+// takes the shape (otherwise hipErrorInvalidValue).
+hipError_t launch_gemm_nn_batched_views(void* y, const void* x, const void* w, size_t batches,
+                                        size_t m, size_t n, size_t k, const HeadView& wv,
+                                        const HeadView& yv, hipStream_t stream, bool causal);
+hipError_t launch_gemm_tn_batched_views(void* y, const void* x, const void* w, size_t batches,
+                                        size_t m, size_t n, size_t k, const HeadView& wv,
+                                        const HeadView& yv, hipStream_t stream, bool causal);
 // Whether a causal batched GEMM of this layout and shape takes the causal path
 // (the pipeline, with the square operand); otherwise it computes everything.
 bool gemm_batched_causal_taken(GemmLayout l, size_t m, size_t n, size_t k);
@@ -197,13 +222,18 @@ hipError_t launch_causal_softmax_backward(void* ds, const void* p, const void* d
 // [batches][length][64], p and ds [batches][length][length] (ds not aliasing
 // p); zero_span as for the softmax passes.
 bool attn_scores_fusable(size_t length, size_t head_width);
+// qv / kv (dov / vv): the operands as heads views, or null for
+// [batches][length][64].
 hipError_t launch_attn_scores_softmax(void* p, const void* q, const void* k, size_t batches,
                                       size_t length, size_t head_width, float scale,
-                                      hipStream_t stream, int zero_span);
+                                      hipStream_t stream, int zero_span,
+                                      const HeadView* qv = nullptr, const HeadView* kv = nullptr);
 hipError_t launch_attn_scores_softmax_backward(void* ds, const void* p, const void* dout,
                                                const void* v, size_t batches, size_t length,
                                                size_t head_width, float scale,
-                                               hipStream_t stream, int zero_span);
+                                               hipStream_t stream, int zero_span,
+                                               const HeadView* dov = nullptr,
+                                               const HeadView* vv = nullptr);
 hipError_t launch_softmax_cross_entropy(void* dlogits, void* row_loss, const void* logits,
                                         const void* targets, float scale, size_t rows,
                                         size_t vocab, size_t cols, hipStream_t stream);

@@ -323,6 +323,34 @@ def test_fused_scores_and_softmax_change_no_bits(flint, cuda, tune, length, caus
     assert bool(torch.isfinite(one[1]).all())
 
 
+@pytest.mark.parametrize("length", [1024, 320, 96, 32])
+@pytest.mark.parametrize("causal", ["1", "0"], ids=["causal", "full"])
+def test_head_views_change_no_bits(flint, cuda, tune, length, causal):
+    """In one allocation the stored-probability model reads q, k, v and dO and
+    writes O, dQ, dK and dV as heads views of the token rows, with no split or
+    merge copies; separate buffers (q, k, v not back to back) run the copies
+    and the [batches][length][64] products. Every output and gradient must be
+    the same bits."""
+    cfg = dict(layers=2, heads=3, width=192, block_size=1024, vocab=1000, padded_vocab=1024)
+    sequences = 2
+    shapes = G.parameter_shapes(cfg["layers"], cfg["width"], cfg["block_size"],
+                                cfg["padded_vocab"])
+    params = G.init_params(shapes, cfg["layers"], cfg["vocab"], seed=17, trained=True)
+    params = {n: t.half().float() for n, t in params.items()}
+    idx, tgt = _tokens(cfg, sequences, length, 18)
+    if causal == "0":
+        tune("attn_causal", "0")
+    views = _run(flint, cfg, sequences, length, params, idx, tgt, 0.25)
+    copies = _run(flint, cfg, sequences, length, params, idx, tgt, 0.25, separate=True)
+    for x, y in zip(copies[:3], views[:3]):
+        assert torch.equal(x.view(torch.int32) if x.dtype == torch.float32 else x,
+                           y.view(torch.int32) if y.dtype == torch.float32 else y)
+    for n in copies[3]:
+        assert torch.equal(copies[3][n].view(torch.int32), views[3][n].view(torch.int32)), n
+    assert copies[4] == views[4]
+    assert bool(torch.isfinite(views[1]).all())
+
+
 WIDE = dict(layers=1, heads=4, width=256, block_size=1024, vocab=1000, padded_vocab=1024)
 
 
