@@ -47,6 +47,8 @@ constexpr int kMaxLength = 1024;
 constexpr int kPad = 8;            // halves after each staged row (bank spread)
 constexpr int kWaves = 8;           // waves per workgroup
 constexpr int kGroupsPerWave = kMaxLength / 32 / kWaves;
+constexpr int kRowsPerWave = kBlockRows / kWaves;   // row passes per wave
+static_assert(kBlockRows % kWaves == 0, "whole rows per wave");
 
 // The staged row stride (halves) for a sequence length, and the block's LDS
 // (sized for the longest rows: 66 KB, two workgroups per CU).
@@ -118,18 +120,26 @@ scores_softmax(h8* __restrict__ p, const _Float16* __restrict__ q, const _Float1
     stage_scores(staged, stride, q + head_view_offset(qv, b), qv.ld, k + head_view_offset(kv, b),
                  kv.ld, r0, scale, wave, lane);
     __syncthreads();
+    // The wave's rows wave, wave + kWaves, ... side by side.
     const int chunks = length >> 3;
-    for (int i = wave; i < kBlockRows; i += kWaves) {
+    h8 raw[kRowsPerWave][2];
+    int tt[kRowsPerWave];
+    h8* prs[kRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+        const int i = wave + r * kWaves;
         const int t = r0 + i;
+        tt[r] = t;
+        prs[r] = p + (head + t) * chunks;
         const int visible_chunks = (t >> 3) + 1;
-        h8 raw[2];
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
             const int c = lane + c2 * 64;
-            if (c < visible_chunks) raw[c2] = *reinterpret_cast<const h8*>(staged + i * stride + c * 8);
+            if (c < visible_chunks)
+                raw[r][c2] = *reinterpret_cast<const h8*>(staged + i * stride + c * 8);
         }
-        softmax_forward_row(p + (head + t) * chunks, raw, t, chunks, lane, zero_span);
     }
+    softmax_forward_rows<kRowsPerWave>(prs, raw, tt, chunks, lane, zero_span);
 }
 
 // dp staged as above (dO for q, V for k, scale 1); then per row the
@@ -149,22 +159,29 @@ scores_softmax_backward(h8* __restrict__ ds, const h8* __restrict__ p,
     stage_scores(staged, stride, dout + head_view_offset(dv_, b), dv_.ld,
                  v + head_view_offset(vv, b), vv.ld, r0, 1.0f, wave, lane);
     __syncthreads();
+    // The wave's rows side by side, their p loads in flight together.
     const int chunks = length >> 3;
-    for (int i = wave; i < kBlockRows; i += kWaves) {
+    h8 ph[kRowsPerWave][2], dh[kRowsPerWave][2];
+    int tt[kRowsPerWave];
+    h8* dsr[kRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+        const int i = wave + r * kWaves;
         const int t = r0 + i;
         const size_t row = head + t;
+        tt[r] = t;
+        dsr[r] = ds + row * chunks;
         const int visible_chunks = (t >> 3) + 1;
-        float pv[2][8], dv[2][8];
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
             const int c = lane + c2 * 64;
             if (c < visible_chunks) {
-                unpack8(load_stream(p + row * chunks + c), pv[c2]);
-                unpack8(*reinterpret_cast<const h8*>(staged + i * stride + c * 8), dv[c2]);
+                ph[r][c2] = load_stream(p + row * chunks + c);
+                dh[r][c2] = *reinterpret_cast<const h8*>(staged + i * stride + c * 8);
             }
         }
-        softmax_backward_row(ds + row * chunks, pv, dv, t, chunks, lane, scale, zero_span);
     }
+    softmax_backward_rows<kRowsPerWave>(dsr, ph, dh, tt, chunks, lane, scale, zero_span);
 }
 
 }  // namespace

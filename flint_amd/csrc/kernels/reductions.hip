@@ -656,16 +656,16 @@ causal_softmax_backward(h8* ds, const h8* __restrict__ p, const h8* dp, size_t r
     const int chunks = length >> 3;
     const int t = int(row % size_t(length));
     const int visible_chunks = (t >> 3) + 1;
-    float pv[2][8], dv[2][8];
+    h8 ph[2], dh[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int c = lane + i * 64;
         if (c < visible_chunks) {
-            unpack8(load_stream(p + row * chunks + c), pv[i]);
-            unpack8(load_stream(dp + row * chunks + c), dv[i]);
+            ph[i] = load_stream(p + row * chunks + c);
+            dh[i] = load_stream(dp + row * chunks + c);
         }
     }
-    softmax_backward_row(ds + row * chunks, pv, dv, t, chunks, lane, scale, zero_span);
+    softmax_backward_row(ds + row * chunks, ph, dh, t, chunks, lane, scale, zero_span);
     }
 }
 

@@ -1,7 +1,8 @@
 // The row arithmetic of the causal softmax passes, shared by the row kernels
 // (reductions.hip: flint_causal_softmax_forward / _backward) and the fused
 // attention passes of the GPT-2 model (attention_stored.hip), so that both
-// produce the same bits. One wave per row of length <= 1024; lane l holds the
+// produce the same bits. One wave per row of length <= 1024 (a wave may take
+// several rows side by side); lane l holds the
 // row's 16-byte chunks l and l + 64 (8 FP16 each). Row t sees columns 0..t;
 // chunks past the diagonal are written as zeros (up to written_chunks) and
 // never read. Reference formulas: ref src/kernels/softmax.cu (forward),
@@ -21,102 +22,176 @@ __device__ __forceinline__ int written_chunks(int t, int chunks, int zero_span) 
     return end < chunks ? end : chunks;
 }
 
-// p's row t from its scores: raw holds this lane's visible chunks (lane and
-// lane + 64, those below (t >> 3) + 1). max, then sum of exp(s - max) in the
-// lane's order (chunk lane, then lane + 64; columns 0..7) and the wave's
-// butterfly, then p = RN16(RN(e * RN(1 / sum))).
-__device__ __forceinline__ void softmax_forward_row(h8* pr, const h8 (&raw)[2], int t, int chunks,
-                                                    int lane, int zero_span) {
-    const int visible_chunks = (t >> 3) + 1;
-    float v[2][8];
-    float mx = -__builtin_huge_valf();
+// p's rows t[0..R) from their scores, one wave each, the R rows side by side
+// (their reductions' lane exchanges interleaved, so that one row's latency
+// hides the others'): raw[r] holds this lane's visible chunks of row r (lane
+// and lane + 64, those below (t >> 3) + 1). Per row: max, then the sum of
+// exp(s - max) in the lane's order (chunk lane, then lane + 64; columns
+// 0..7) and the wave's butterfly, then p = RN16(RN(e * RN(1 / sum))). Each
+// row's arithmetic is the same whatever R is.
+template <int R>
+__device__ __forceinline__ void softmax_forward_rows(h8* const (&pr)[R], const h8 (&raw)[R][2],
+                                                     const int (&t)[R], int chunks, int lane,
+                                                     int zero_span) {
+    float v[R][2][8];
+    float mx[R];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = lane + i * 64;
-        if (c < visible_chunks) {
-            unpack8(raw[i], v[i]);
-            const int vis = min(t + 1 - c * 8, 8);
+    for (int r = 0; r < R; ++r) {
+        const int visible_chunks = (t[r] >> 3) + 1;
+        mx[r] = -__builtin_huge_valf();
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (j < vis) mx = fmaxf(mx, v[i][j]);
-        }
-    }
-    mx = max_reduce<64>(mx);
-    float sum = 0.0f;
+        for (int i = 0; i < 2; ++i) {
+            const int c = lane + i * 64;
+            if (c < visible_chunks) {
+                unpack8(raw[r][i], v[r][i]);
+                const int vis = min(t[r] + 1 - c * 8, 8);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = lane + i * 64;
-        if (c < visible_chunks) {
-            const int vis = min(t + 1 - c * 8, 8);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                v[i][j] = j < vis ? exp_accurate(v[i][j] - mx) : 0.0f;
-                sum = add_rn(sum, v[i][j]);
+                for (int j = 0; j < 8; ++j)
+                    if (j < vis) mx[r] = fmaxf(mx[r], v[r][i][j]);
             }
         }
     }
-    sum = sum_reduce<64>(sum);
-    const float inv = __fdiv_rn(1.0f, sum);
-    const int written = written_chunks(t, chunks, zero_span);
+    // max_reduce<64> of each row.
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = lane + i * 64;
-        if (c < written) {
+    for (int off = 32; off > 0; off /= 2) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off, 64));
+    }
+    float sum[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int visible_chunks = (t[r] >> 3) + 1;
+        sum[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = lane + i * 64;
             if (c < visible_chunks) {
-                // Masked columns of the diagonal chunk are selected as +0, not
-                // formed as 0 / sum: a row whose sum is NaN keeps them +0.
-                const int vis = min(t + 1 - c * 8, 8);
-                float o[8];
+                const int vis = min(t[r] + 1 - c * 8, 8);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = j < vis ? mul_rn(v[i][j], inv) : 0.0f;
-                pr[c] = pack8(o);
-            } else {
-                pr[c] = h8{};
+                for (int j = 0; j < 8; ++j) {
+                    v[r][i][j] = j < vis ? exp_accurate(v[r][i][j] - mx[r]) : 0.0f;
+                    sum[r] = add_rn(sum[r], v[r][i][j]);
+                }
+            }
+        }
+    }
+    // sum_reduce<64> of each row.
+#pragma unroll
+    for (int off = 32; off > 0; off /= 2) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) sum[r] = add_rn(sum[r], __shfl_xor(sum[r], off, 64));
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int visible_chunks = (t[r] >> 3) + 1;
+        const float inv = __fdiv_rn(1.0f, sum[r]);
+        const int written = written_chunks(t[r], chunks, zero_span);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = lane + i * 64;
+            if (c < written) {
+                if (c < visible_chunks) {
+                    // Masked columns of the diagonal chunk are selected as +0,
+                    // not formed as 0 / sum: a row whose sum is NaN keeps them
+                    // +0.
+                    const int vis = min(t[r] + 1 - c * 8, 8);
+                    float o[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o[j] = j < vis ? mul_rn(v[r][i][j], inv) : 0.0f;
+                    pr[r][c] = pack8(o);
+                } else {
+                    pr[r][c] = h8{};
+                }
             }
         }
     }
 }
 
-// ds's row t: pv and dv hold this lane's visible chunks of p and dp. D is the
-// compensated sum (TwoSum) of the rounded products p * dp in the lane's order
-// and the wave's butterfly; ds = RN16(RN(RN(p * RN(RN(dp - D.sum) - D.error))
-// * scale)), with D.error dropped when D.sum is not finite.
-__device__ __forceinline__ void softmax_backward_row(h8* dsr, const float (&pv)[2][8],
-                                                     const float (&dv)[2][8], int t, int chunks,
-                                                     int lane, float scale, int zero_span) {
-    const int visible_chunks = (t >> 3) + 1;
-    Comp d;
+// One row: softmax_forward_rows<1>.
+__device__ __forceinline__ void softmax_forward_row(h8* pr, const h8 (&raw)[2], int t, int chunks,
+                                                    int lane, int zero_span) {
+    h8* const prs[1] = {pr};
+    const h8 (&raws)[1][2] = *reinterpret_cast<const h8 (*)[1][2]>(&raw);
+    const int ts[1] = {t};
+    softmax_forward_rows<1>(prs, raws, ts, chunks, lane, zero_span);
+}
+
+// ds's rows t[0..R), one wave each, the R rows side by side: ph[r] and dh[r]
+// hold this lane's visible chunks of p and dp. D is the compensated sum
+// (TwoSum) of the rounded products p * dp in the lane's order and the wave's
+// butterfly; ds = RN16(RN(RN(p * RN(RN(dp - D.sum) - D.error)) * scale)),
+// with D.error dropped when D.sum is not finite.
+template <int R>
+__device__ __forceinline__ void softmax_backward_rows(h8* const (&dsr)[R], const h8 (&ph)[R][2],
+                                                      const h8 (&dh)[R][2], const int (&t)[R],
+                                                      int chunks, int lane, float scale,
+                                                      int zero_span) {
+    Comp d[R];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = lane + i * 64;
-        if (c < visible_chunks) {
-            const int vis = min(t + 1 - c * 8, 8);
+    for (int r = 0; r < R; ++r) {
+        const int visible_chunks = (t[r] >> 3) + 1;
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (j < vis) comp_add(d, mul_rn(pv[i][j], dv[i][j]));
-        }
-    }
-    d = comp_reduce<64>(d);
-    if (!__builtin_isfinite(d.sum)) d.error = 0.0f;
-    const int written = written_chunks(t, chunks, zero_span);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = lane + i * 64;
-        if (c < written) {
+        for (int i = 0; i < 2; ++i) {
+            const int c = lane + i * 64;
             if (c < visible_chunks) {
-                const int vis = min(t + 1 - c * 8, 8);
-                float o[8];
+                float pv[8], dv[8];
+                unpack8(ph[r][i], pv);
+                unpack8(dh[r][i], dv);
+                const int vis = min(t[r] + 1 - c * 8, 8);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float diff = sub_rn(sub_rn(dv[i][j], d.sum), d.error);
-                    o[j] = j < vis ? mul_rn(mul_rn(pv[i][j], diff), scale) : 0.0f;
-                }
-                store_stream(dsr + c, pack8(o));
-            } else {
-                store_stream(dsr + c, h8{});
+                for (int j = 0; j < 8; ++j)
+                    if (j < vis) comp_add(d[r], mul_rn(pv[j], dv[j]));
             }
         }
     }
+    // comp_reduce<64> of each row.
+#pragma unroll
+    for (int off = 32; off > 0; off /= 2) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float s = __shfl_xor(d[r].sum, off, 64);
+            const float e = __shfl_xor(d[r].error, off, 64);
+            comp_merge(d[r], s, e);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (!__builtin_isfinite(d[r].sum)) d[r].error = 0.0f;
+        const int visible_chunks = (t[r] >> 3) + 1;
+        const int written = written_chunks(t[r], chunks, zero_span);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = lane + i * 64;
+            if (c < written) {
+                if (c < visible_chunks) {
+                    float pv[8], dv[8];
+                    unpack8(ph[r][i], pv);
+                    unpack8(dh[r][i], dv);
+                    const int vis = min(t[r] + 1 - c * 8, 8);
+                    float o[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float diff = sub_rn(sub_rn(dv[j], d[r].sum), d[r].error);
+                        o[j] = j < vis ? mul_rn(mul_rn(pv[j], diff), scale) : 0.0f;
+                    }
+                    store_stream(dsr[r] + c, pack8(o));
+                } else {
+                    store_stream(dsr[r] + c, h8{});
+                }
+            }
+        }
+    }
+}
+
+// One row: softmax_backward_rows<1>.
+__device__ __forceinline__ void softmax_backward_row(h8* dsr, const h8 (&ph)[2], const h8 (&dh)[2],
+                                                     int t, int chunks, int lane, float scale,
+                                                     int zero_span) {
+    h8* const dsrs[1] = {dsr};
+    const h8 (&phs)[1][2] = *reinterpret_cast<const h8 (*)[1][2]>(&ph);
+    const h8 (&dhs)[1][2] = *reinterpret_cast<const h8 (*)[1][2]>(&dh);
+    const int ts[1] = {t};
+    softmax_backward_rows<1>(dsrs, phs, dhs, ts, chunks, lane, scale, zero_span);
 }
 
 }  // namespace flint
