@@ -143,6 +143,21 @@ __device__ __forceinline__ float exp_accurate(float x) {
     return __builtin_isfinite(lo) ? __builtin_fmaf(e, lo * kLn2, e) : e;
 }
 
+// exp_accurate's bits for x <= 0 or NaN (a softmax's score minus its row
+// max), without the finiteness test: below -150 both give +0 (2^hi is below
+// the smallest denormal), so x is clamped there first by a NaN-propagating
+// maximum, which keeps lo finite (x = -inf included) and NaN a NaN.
+__device__ __forceinline__ float exp_accurate_nonpos(float x) {
+    constexpr float kLog2eHi = 1.44269502162933349609375f;
+    constexpr float kLog2eLo = 1.925963033500011079101604e-8f;
+    constexpr float kLn2 = 0.693147180559945309f;
+    x = __builtin_elementwise_maximum(x, -150.0f);
+    const float hi = x * kLog2eHi;
+    const float lo = __builtin_fmaf(x, kLog2eHi, -hi) + x * kLog2eLo;
+    const float e = __builtin_amdgcn_exp2f(hi);
+    return __builtin_fmaf(e, lo * kLn2, e);
+}
+
 __device__ __forceinline__ void unpack8(const h8& h, float (&v)[8]) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = float(h[i]);

@@ -33,6 +33,12 @@ template <int R>
 __device__ __forceinline__ void softmax_forward_rows(h8* const (&pr)[R], const h8 (&raw)[R][2],
                                                      const int (&t)[R], int chunks, int lane,
                                                      int zero_span) {
+    // The masked columns of the diagonal chunk (the one lane whose chunk
+    // holds column t) read as -inf: they leave the max alone and their exp is
+    // +0, the 0 the sum adds for them, so no other element needs a select.
+    // (The max is never NaN, fmaxf dropping NaN operands, so every masked
+    // difference is -inf or, in a row whose max is -inf, NaN; such a row's
+    // sum is NaN from its visible columns already. No difference is +inf.)
     float v[R][2][8];
     float mx[R];
 #pragma unroll
@@ -44,10 +50,14 @@ __device__ __forceinline__ void softmax_forward_rows(h8* const (&pr)[R], const h
             const int c = lane + i * 64;
             if (c < visible_chunks) {
                 unpack8(raw[r][i], v[r][i]);
-                const int vis = min(t[r] + 1 - c * 8, 8);
+                const int vis = t[r] + 1 - c * 8;
+                if (vis < 8) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (j < vis) mx[r] = fmaxf(mx[r], v[r][i][j]);
+                    for (int j = 1; j < 8; ++j)
+                        if (j >= vis) v[r][i][j] = -__builtin_huge_valf();
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) mx[r] = fmaxf(mx[r], v[r][i][j]);
             }
         }
     }
@@ -66,10 +76,9 @@ __device__ __forceinline__ void softmax_forward_rows(h8* const (&pr)[R], const h
         for (int i = 0; i < 2; ++i) {
             const int c = lane + i * 64;
             if (c < visible_chunks) {
-                const int vis = min(t[r] + 1 - c * 8, 8);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    v[r][i][j] = j < vis ? exp_accurate(v[r][i][j] - mx[r]) : 0.0f;
+                    v[r][i][j] = exp_accurate_nonpos(v[r][i][j] - mx[r]);
                     sum[r] = add_rn(sum[r], v[r][i][j]);
                 }
             }
@@ -91,13 +100,18 @@ __device__ __forceinline__ void softmax_forward_rows(h8* const (&pr)[R], const h
             const int c = lane + i * 64;
             if (c < written) {
                 if (c < visible_chunks) {
-                    // Masked columns of the diagonal chunk are selected as +0,
-                    // not formed as 0 / sum: a row whose sum is NaN keeps them
-                    // +0.
-                    const int vis = min(t[r] + 1 - c * 8, 8);
+                    // Masked columns of the diagonal chunk are set to +0, not
+                    // formed as 0 * (1 / sum): a row whose sum is NaN keeps
+                    // them +0.
+                    const int vis = t[r] + 1 - c * 8;
                     float o[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) o[j] = j < vis ? mul_rn(v[r][i][j], inv) : 0.0f;
+                    for (int j = 0; j < 8; ++j) o[j] = mul_rn(v[r][i][j], inv);
+                    if (vis < 8) {
+#pragma unroll
+                        for (int j = 1; j < 8; ++j)
+                            if (j >= vis) o[j] = 0.0f;
+                    }
                     pr[r][c] = pack8(o);
                 } else {
                     pr[r][c] = h8{};
@@ -126,6 +140,9 @@ __device__ __forceinline__ void softmax_backward_rows(h8* const (&dsr)[R], const
                                                       const h8 (&dh)[R][2], const int (&t)[R],
                                                       int chunks, int lane, float scale,
                                                       int zero_span) {
+    // The masked columns of the diagonal chunk add a product of -0, which
+    // leaves a finite D exactly as it was (its error is never -0), and a
+    // D.sum that is not finite drops D.error anyway.
     Comp d[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -137,10 +154,17 @@ __device__ __forceinline__ void softmax_backward_rows(h8* const (&dsr)[R], const
                 float pv[8], dv[8];
                 unpack8(ph[r][i], pv);
                 unpack8(dh[r][i], dv);
-                const int vis = min(t[r] + 1 - c * 8, 8);
+                float prod[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (j < vis) comp_add(d[r], mul_rn(pv[j], dv[j]));
+                for (int j = 0; j < 8; ++j) prod[j] = mul_rn(pv[j], dv[j]);
+                const int vis = t[r] + 1 - c * 8;
+                if (vis < 8) {
+#pragma unroll
+                    for (int j = 1; j < 8; ++j)
+                        if (j >= vis) prod[j] = -0.0f;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) comp_add(d[r], prod[j]);
             }
         }
     }
@@ -167,12 +191,17 @@ __device__ __forceinline__ void softmax_backward_rows(h8* const (&dsr)[R], const
                     float pv[8], dv[8];
                     unpack8(ph[r][i], pv);
                     unpack8(dh[r][i], dv);
-                    const int vis = min(t[r] + 1 - c * 8, 8);
+                    const int vis = t[r] + 1 - c * 8;
                     float o[8];
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const float diff = sub_rn(sub_rn(dv[j], d[r].sum), d[r].error);
-                        o[j] = j < vis ? mul_rn(mul_rn(pv[j], diff), scale) : 0.0f;
+                        o[j] = mul_rn(mul_rn(pv[j], diff), scale);
+                    }
+                    if (vis < 8) {
+#pragma unroll
+                        for (int j = 1; j < 8; ++j)
+                            if (j >= vis) o[j] = 0.0f;
                     }
                     store_stream(dsr[r] + c, pack8(o));
                 } else {
