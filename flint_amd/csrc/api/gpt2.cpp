@@ -99,6 +99,11 @@ size_t round_up(size_t b) { return (b + kAlign - 1) / kAlign * kAlign; }
 
 }  // namespace
 
+// How the default model's attention holds its per-head operands: split and
+// merged by copies (flint_heads_split / _merge, the reference's sequence), or
+// as heads views of the token rows. The same bits either way.
+enum class AttnPlan : int { kCopies, kViews };
+
 struct flint_gpt2 {
     flint_gpt2_config cfg{};
     size_t rows = 0, head_width = 0, head_batches = 0;
@@ -129,6 +134,9 @@ struct flint_gpt2 {
     // runs at once).
     size_t ln_offset = 0;
     mutable flint::ParamsMerge pending{};
+    // The attention plan of the last forward, which its backward follows
+    // (plan overrides may change in between).
+    AttnPlan attn_plan = AttnPlan::kCopies;
     std::vector<Request> requests;
     std::vector<void*> blocks;   // hipMalloc'd allocations
     std::vector<float> host_loss;
@@ -471,17 +479,23 @@ bool attn_scores_fused(size_t length, size_t head_width) {
 // heads views of their token rows, and dO is read as one. The split / merge
 // launches of the sequence (flint_heads_split / _merge) go away; the products
 // and their bits do not change. Taken where the fused scores take the shape,
-// the pipeline takes both batched products, and the buffers lie back to back
-// (one allocation whose 256-byte grid the head buffers' size is on).
-bool attn_views(const flint_gpt2& m, const Saved& s) {
+// the pipeline takes both batched products, and every layer's q, k, v lie
+// back to back (one allocation whose 256-byte grid the head buffers' size is
+// on).
+AttnPlan attn_plan_of(const flint_gpt2& m) {
     using flint::GemmLayout;
+    if (m.flash) return AttnPlan::kCopies;
     const size_t len = m.cfg.length, hw = m.head_width;
     const size_t heads_bytes = m.head_batches * len * hw * 2;
-    const char* q = static_cast<const char*>(s.q);
-    return s.k == q + heads_bytes && s.v == q + 2 * heads_bytes &&
-           attn_scores_fused(len, hw) &&
-           flint::gemm_batched_causal_taken(GemmLayout::kNN, len, hw, len) &&
-           flint::gemm_batched_causal_taken(GemmLayout::kTN, len, hw, len);
+    for (const Layer& L : m.layers) {
+        const char* q = static_cast<const char*>(L.s.q);
+        if (q == nullptr || L.s.k != q + heads_bytes || L.s.v != q + 2 * heads_bytes)
+            return AttnPlan::kCopies;
+    }
+    const bool views = attn_scores_fused(len, hw) &&
+                       flint::gemm_batched_causal_taken(GemmLayout::kNN, len, hw, len) &&
+                       flint::gemm_batched_causal_taken(GemmLayout::kTN, len, hw, len);
+    return views ? AttnPlan::kViews : AttnPlan::kCopies;
 }
 
 // Slices of [tokens][cols] rows as heads: slice b = sequence b / heads, head
@@ -544,7 +558,7 @@ flint_status forward_layer(const flint_gpt2& m, const Layer& L, flint_stream st)
         FLINT_HIP_CHECK(flint::launch_attention_forward(
             s.attn_out, s.lse, qkv, qkv + w, qkv + 2 * w, m.head_batches, c.length,
             score_scale(hw), flint::to_hip(st), attn_layout(m)));
-    } else if (attn_views(m, s)) {
+    } else if (m.attn_plan == AttnPlan::kViews) {
         auto* qkv = static_cast<_Float16*>(s.q);   // q, k, v back to back: [rows][3 width]
         FLINT_TRY(flint_gemm_nt_bias(qkv, s.h1, L.attn.half, L.attn.b->data, rows, 3 * w, w, st));
         const flint::HeadView qkv_v = heads_view(m, 3 * w), rows_v = heads_view(m, w);
@@ -691,9 +705,10 @@ flint_status backward_layer(const flint_gpt2& m, const Layer& L, int acc, flint_
         FLINT_HIP_CHECK(flint::launch_attention_backward(
             g, g + w, g + 2 * w, m.dh, qkv, qkv + w, qkv + 2 * w, s.attn_out, s.lse,
             m.attn_work, nb, len, score_scale(hw), flint::to_hip(st), attn_layout(m)));
-    } else if (attn_views(m, s)) {
-        // dO rows in dh, q, k, v in the layer's projection block; dQ, dK, dV
-        // straight into the qkv gradient's columns.
+    } else if (m.attn_plan == AttnPlan::kViews) {
+        // dO rows in dh, q, k, v in the layer's projection block (where the
+        // forward left them); dQ, dK, dV straight into the qkv gradient's
+        // columns.
         auto* g = static_cast<_Float16*>(m.qkv);
         auto* qkv = static_cast<_Float16*>(s.q);
         const flint::HeadView qkv_v = heads_view(m, 3 * w), rows_v = heads_view(m, w);
@@ -788,6 +803,7 @@ flint_status create_model(const char* name, const flint_gpt2_config* config, boo
         m->host_loss.resize(m->rows);
         FLINT_TRY(allocate(*m));
         link(*m);
+        m->attn_plan = attn_plan_of(*m);
         *model = m.release();
     } catch (const std::bad_alloc&) {
         return fail(FLINT_ERROR_CUDA, "%s: out of host memory", name);
@@ -868,6 +884,7 @@ FLINT_API flint_status flint_gpt2_forward(flint_gpt2* model, const void* tokens,
                   .status());
     FLINT_TRY(flint_embedding_forward(m.layers[0].s.x_in, tokens, m.wte->data, m.wpe->data,
                                       c.sequences, c.length, c.padded_vocab, c.width, stream));
+    model->attn_plan = attn_plan_of(m);
     for (const Layer& L : m.layers) FLINT_TRY(forward_layer(m, L, stream));
     FLINT_TRY(layer_norm(m, m.ln_f, m.x_final, m.h_f, m.mean_f, m.rstd_f, stream));
     FLINT_TRY(flint_gemm_nt(m.logits, m.h_f, m.wte_half, rows, c.padded_vocab, c.width, stream));

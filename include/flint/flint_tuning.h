@@ -16,7 +16,11 @@
  *   "ce_threads"    "256", "512" or "1024"
  *   "partials_cpl"  "1", "2" or "4"
  * A value the plan cannot use leaves its default in place. Set and clear
- * overrides only while no call of the library runs on another thread.
+ * overrides only while no call of the library runs on another thread, and
+ * not between a GPT-2 model's forward and its backward: the backward reads
+ * what the forward's plans left (the model keeps the forward's attention
+ * layout, but the causal zero span of the stored probabilities follows the
+ * overrides of each call).
  */
 #ifndef FLINT_FLINT_TUNING_H
 #define FLINT_FLINT_TUNING_H
