@@ -93,6 +93,24 @@ __device__ __forceinline__ float dpp_f(float v, int ctrl_sel) {
     return __builtin_bit_cast(float, r);
 }
 
+// The value of lane (this lane ^ OFF), OFF a power of two below 64: DPP for
+// 1, 2 (quad permutes) and 8 (row_ror:8 within 16 lanes), ds_swizzle for 4
+// and 16, ds_bpermute for 32. The same values as __shfl_xor(v, OFF, 64),
+// with only the cross-row exchanges through the LDS unit.
+template <int OFF>
+__device__ __forceinline__ float xor_lane(float v) {
+    static_assert(OFF > 0 && OFF < 64 && (OFF & (OFF - 1)) == 0, "a lane bit");
+    const int x = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (OFF == 1) r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+    else if constexpr (OFF == 2) r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+    else if constexpr (OFF == 8) r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);
+    else if constexpr (OFF == 4) r = __builtin_amdgcn_ds_swizzle(x, 0x101F);
+    else if constexpr (OFF == 16) r = __builtin_amdgcn_ds_swizzle(x, 0x401F);
+    else r = __shfl_xor(x, 32, 64);
+    return __builtin_bit_cast(float, r);
+}
+
 // Compensated all-reduce over the 64 lanes; every lane ends with the same
 // bits (comp_merge is symmetric). The order differs from comp_reduce<64>.
 __device__ __forceinline__ Comp comp_allreduce64(Comp a) {

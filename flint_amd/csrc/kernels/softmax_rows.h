@@ -9,6 +9,8 @@
 // ref src/kernels/softmax_backward.cu (backward).
 #pragma once
 
+#include <type_traits>
+
 #include "kernels/reduce_common.h"
 
 namespace flint {
@@ -61,12 +63,18 @@ __device__ __forceinline__ void softmax_forward_rows(h8* const (&pr)[R], const h
             }
         }
     }
-    // max_reduce<64> of each row.
+    // max_reduce<64> of each row (the lane exchanges of xor_lane: the max of
+    // the same values in the same order).
+    auto max_step = [&](auto off) {
 #pragma unroll
-    for (int off = 32; off > 0; off /= 2) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off, 64));
-    }
+        for (int r = 0; r < R; ++r) mx[r] = fmaxf(mx[r], xor_lane<decltype(off)::value>(mx[r]));
+    };
+    max_step(std::integral_constant<int, 32>{});
+    max_step(std::integral_constant<int, 16>{});
+    max_step(std::integral_constant<int, 8>{});
+    max_step(std::integral_constant<int, 4>{});
+    max_step(std::integral_constant<int, 2>{});
+    max_step(std::integral_constant<int, 1>{});
     float sum[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -84,12 +92,17 @@ __device__ __forceinline__ void softmax_forward_rows(h8* const (&pr)[R], const h
             }
         }
     }
-    // sum_reduce<64> of each row.
+    // sum_reduce<64> of each row: the butterfly's adds in its order.
+    auto sum_step = [&](auto off) {
 #pragma unroll
-    for (int off = 32; off > 0; off /= 2) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) sum[r] = add_rn(sum[r], __shfl_xor(sum[r], off, 64));
-    }
+        for (int r = 0; r < R; ++r) sum[r] = add_rn(sum[r], xor_lane<decltype(off)::value>(sum[r]));
+    };
+    sum_step(std::integral_constant<int, 32>{});
+    sum_step(std::integral_constant<int, 16>{});
+    sum_step(std::integral_constant<int, 8>{});
+    sum_step(std::integral_constant<int, 4>{});
+    sum_step(std::integral_constant<int, 2>{});
+    sum_step(std::integral_constant<int, 1>{});
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int visible_chunks = (t[r] >> 3) + 1;
@@ -168,16 +181,21 @@ __device__ __forceinline__ void softmax_backward_rows(h8* const (&dsr)[R], const
             }
         }
     }
-    // comp_reduce<64> of each row.
-#pragma unroll
-    for (int off = 32; off > 0; off /= 2) {
+    // comp_reduce<64> of each row: the butterfly's merges in its order.
+    auto comp_step = [&](auto off) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const float s = __shfl_xor(d[r].sum, off, 64);
-            const float e = __shfl_xor(d[r].error, off, 64);
+            const float s = xor_lane<decltype(off)::value>(d[r].sum);
+            const float e = xor_lane<decltype(off)::value>(d[r].error);
             comp_merge(d[r], s, e);
         }
-    }
+    };
+    comp_step(std::integral_constant<int, 32>{});
+    comp_step(std::integral_constant<int, 16>{});
+    comp_step(std::integral_constant<int, 8>{});
+    comp_step(std::integral_constant<int, 4>{});
+    comp_step(std::integral_constant<int, 2>{});
+    comp_step(std::integral_constant<int, 1>{});
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (!__builtin_isfinite(d[r].sum)) d[r].error = 0.0f;
