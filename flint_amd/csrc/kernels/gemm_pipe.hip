@@ -1022,10 +1022,18 @@ double pipe_eff(const PipeConfig& c, Store st) {
     // TN, whose fragments come from transposing LDS reads with a full LDS
     // wait per sub-step (3072 x 768 x 8192: 64.2 -> 55.2 us, 768 x 3072: 60.2
     // -> 55.1, 2304 x 768: 46.0 -> 43.6, same process; the logits dW 50304 x
-    // 768 x 8192: 744 -> 671 us at 256 x 128). NT and NN ran slower with them
-    // (MLP down 46.4 -> 54.8 us), so there they are taken only when forced.
-    if (c.loaders)
-        return st == Store::kTn || st == Store::kTnHalf ? 1.0 : 0.01;
+    // 768 x 8192: 744 -> 671 us at 256 x 128), and NT + bias at 128 x 192
+    // (the bias epilogue's stores retire on the MFMA waves' counter, apart
+    // from the loads: qkv 8192 x 2304 x 768 34.0 -> 31.6 us, 8192 x 768 x 768
+    // 13.8 -> 13.0, 8192 x 3072 x 768 43.1 -> 40.9, 8192 x 768 x 3072 37.9 ->
+    // 36.1, same process). Other NT and NN epilogues ran as fast or slower
+    // (MLP down + residual 43.8 -> 52.3 us: its residual no longer loads at
+    // tile start; MLP up + GELU 54.7 -> 54.2), so there they are taken only
+    // when forced.
+    if (c.loaders) {
+        if (st == Store::kTn || st == Store::kTnHalf) return 1.0;
+        return st == Store::kBias && c.bm == 128 ? 1.1 : 0.01;
+    }
     // The 8-wave tile: same bits as the 4-wave 256 x 192 x 2 x 64; faster only
     // for plain NT products of many tile rounds (logits 8192 x 50304 x 768:
     // 632.6 -> 608.0 us, same process, five rounds); slower at two rounds with
