@@ -1017,7 +1017,7 @@ bool usable(const PipeConfig& c, Store st, size_t k, Layout l) {
 // (256 x 64: 51 FLOP per loaded byte, worth it only where n <= 64.) TN's
 // operands are k-major, whole lines at either depth; there the 64-deep steps
 // gain from half the barriers, most in 128 x 192 tiles.
-double pipe_eff(const PipeConfig& c, Store st) {
+double pipe_eff(const PipeConfig& c, Store st, Layout l) {
     // Loader waves pay where the MFMA waves' own stream is the bottleneck:
     // TN, whose fragments come from transposing LDS reads with a full LDS
     // wait per sub-step (3072 x 768 x 8192: 64.2 -> 55.2 us, 768 x 3072: 60.2
@@ -1026,13 +1026,18 @@ double pipe_eff(const PipeConfig& c, Store st) {
     // (the bias epilogue's stores retire on the MFMA waves' counter, apart
     // from the loads: qkv 8192 x 2304 x 768 34.0 -> 31.6 us, 8192 x 768 x 768
     // 13.8 -> 13.0, 8192 x 3072 x 768 43.1 -> 40.9, 8192 x 768 x 3072 37.9 ->
-    // 36.1, same process). Other NT and NN epilogues ran as fast or slower
-    // (MLP down + residual 43.8 -> 52.3 us: its residual no longer loads at
-    // tile start; MLP up + GELU 54.7 -> 54.2), so there they are taken only
-    // when forced.
+    // 36.1, same process), and plain NT (8192 x 3072 x 768 43.7 -> 42.1 us,
+    // 8192 x 768 x 3072 38.3 -> 36.9; the logits 8192 x 50304 x 768 636.0 ->
+    // 617.6 at 256 x 128, which pick_pipe admits only for outputs that
+    // large). Other NT and NN epilogues ran as fast or slower (MLP down +
+    // residual 43.8 -> 52.3 us: its residual no longer loads at tile start;
+    // MLP up + GELU 54.7 -> 55.0; NN 8192 x 768 x 3072 38.2 -> 43.8), so
+    // there they are taken only when forced.
     if (c.loaders) {
         if (st == Store::kTn || st == Store::kTnHalf) return 1.0;
-        return st == Store::kBias && c.bm == 128 ? 1.1 : 0.01;
+        if (st == Store::kBias && c.bm == 128) return 1.1;
+        if (st == Store::kNone && l == Layout::kNT) return c.bm == 128 ? 1.1 : 1.15;
+        return 0.01;
     }
     // The 8-wave tile: same bits as the 4-wave 256 x 192 x 2 x 64; faster only
     // for plain NT products of many tile rounds (logits 8192 x 50304 x 768:
@@ -1078,7 +1083,11 @@ PipeConfig pick_pipe(size_t m, size_t n, size_t k, size_t slices, int cus, Store
                              double(slices);
         const double rounds = std::ceil(tiles / cus);
         if (c.waves == 8 && (st != Store::kNone || rounds < kPipe8MinRounds)) continue;
-        const double cost = rounds * double(c.bm) * double(c.bn) / pipe_eff(c, st);
+        // The 256 x 128 loader tile: plain NT only on the logits' size of
+        // output (8192 x 3072 x 768: 42.7 against 42.1 us for 128 x 192).
+        if (c.loaders && c.bm == 256 && l != Layout::kTN && double(m) * double(n) < 1e8)
+            continue;
+        const double cost = rounds * double(c.bm) * double(c.bn) / pipe_eff(c, st, l);
         if (cost < best_cost * 0.999) {
             best_cost = cost;
             best = c;
@@ -1105,7 +1114,7 @@ void plan_tn(size_t m, size_t n, size_t k, int max_splits, int cus, bool accumul
         if (only == nullptr && c.bn == 64 && (n > 64 || c.bm == 128)) continue;
         // The 256 x 128 loader tile won only on the logits' size of output.
         if (only == nullptr && c.loaders && c.bm == 256 && double(m) * double(n) < 8e6) continue;
-        const double eff = pipe_eff(c, st);
+        const double eff = pipe_eff(c, st, Layout::kTN);
         const double tiles = double((m + c.bm - 1) / c.bm) * double((n + c.bn - 1) / c.bn);
         for (int sp = 1; sp <= max_splits; ++sp) {
             const size_t len = (k + sp - 1) / sp;
