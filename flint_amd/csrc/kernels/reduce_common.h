@@ -146,34 +146,26 @@ __device__ __forceinline__ float max_reduce(float v) {
     return v;
 }
 
-// exp(x) to about 2 FP32 ulps: x log2(e) is formed as hi + lo with the
-// product's rounding error recovered by fma (log2(e) itself split in two
-// floats), then 2^hi comes from v_exp_f32 and the 2^lo factor from its first
-// order term 1 + lo ln 2 (|lo| < 2^-20 makes the second order negligible).
-__device__ __forceinline__ float exp_accurate(float x) {
-    constexpr float kLog2eHi = 1.44269502162933349609375f;       // float(log2 e)
-    constexpr float kLog2eLo = 1.925963033500011079101604e-8f;   // log2 e - kLog2eHi
-    constexpr float kLn2 = 0.693147180559945309f;
-    const float hi = x * kLog2eHi;
-    const float lo = __builtin_fmaf(x, kLog2eHi, -hi) + x * kLog2eLo;
-    const float e = __builtin_amdgcn_exp2f(hi);
-    // x = -inf leaves lo NaN with e = 0 (and x = +inf, e = inf): e is then exact.
-    return __builtin_isfinite(lo) ? __builtin_fmaf(e, lo * kLn2, e) : e;
-}
-
-// exp_accurate's bits for x <= 0 or NaN (a softmax's score minus its row
-// max), without the finiteness test: below -150 both give +0 (2^hi is below
-// the smallest denormal), so x is clamped there first by a NaN-propagating
-// maximum, which keeps lo finite (x = -inf included) and NaN a NaN.
+// exp(x) for x <= 0 or NaN (a softmax's score minus its row max), to about 2
+// FP32 ulps, by Cody and Waite's argument reduction: hi = RN(x log2e) with
+// log2(e) rounded to a float, e = 2^hi from v_exp_f32, and the rest of the
+// exponent r = x - hi ln 2 (in natural-log units, exactly what x log2(e) - hi
+// is worth once multiplied by ln 2) formed by two fmas with ln 2 split in two
+// floats, so r's error is far below 2^-24. exp(x) = e exp(r) = e + e r + ...,
+// and |r| < 2^-16 on the clamped range leaves the second order below 2^-33.
+// Below -150 the result is +0 (2^hi is below the smallest denormal), so x is
+// clamped there first by a NaN-propagating maximum, which keeps r finite
+// (x = -inf included) and NaN a NaN.
 __device__ __forceinline__ float exp_accurate_nonpos(float x) {
-    constexpr float kLog2eHi = 1.44269502162933349609375f;
-    constexpr float kLog2eLo = 1.925963033500011079101604e-8f;
-    constexpr float kLn2 = 0.693147180559945309f;
+    constexpr float kLog2e = 1.44269502162933349609375f;   // float(log2 e)
+    constexpr double kLn2 = 0.6931471805599453094172321;
+    constexpr float kLn2Hi = float(kLn2);
+    constexpr float kLn2Lo = float(kLn2 - double(kLn2Hi));
     x = __builtin_elementwise_maximum(x, -150.0f);
-    const float hi = x * kLog2eHi;
-    const float lo = __builtin_fmaf(x, kLog2eHi, -hi) + x * kLog2eLo;
+    const float hi = x * kLog2e;
+    const float r = __builtin_fmaf(-hi, kLn2Lo, __builtin_fmaf(-hi, kLn2Hi, x));
     const float e = __builtin_amdgcn_exp2f(hi);
-    return __builtin_fmaf(e, lo * kLn2, e);
+    return __builtin_fmaf(e, r, e);
 }
 
 __device__ __forceinline__ void unpack8(const h8& h, float (&v)[8]) {

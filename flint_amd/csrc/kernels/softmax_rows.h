@@ -79,7 +79,10 @@ __device__ __forceinline__ void softmax_forward_rows(h8* const (&pr)[R], const h
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int visible_chunks = (t[r] >> 3) + 1;
-        sum[r] = 0.0f;
+        // -0 + e is e for every e (+0 included), so the first add folds away;
+        // lane 0 always adds at least one e >= +0, so the row's sum is never
+        // -0 and equals the one started from +0.
+        sum[r] = -0.0f;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int c = lane + i * 64;
