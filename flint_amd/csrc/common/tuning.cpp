@@ -15,7 +15,7 @@ namespace {
 constexpr const char* kNames[] = {"gemm_pipe",  "gemm_config",  "gemm_group_m", "gemm_slots",
                                   "attn_causal", "fused_grads", "fused_sums",   "ln_defer",
                                   "ln_fused",    "ce_threads",  "emb_together", "attn_order",
-                                  "partials_cpl", "attn_scores"};
+                                  "partials_cpl", "attn_scores", "emb_scan"};
 static_assert(sizeof(kNames) / sizeof(kNames[0]) == size_t(Tune::kCount), "one name per knob");
 
 // Values are interned and never freed, so a pointer a reader loaded stays

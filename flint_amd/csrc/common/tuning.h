@@ -24,6 +24,7 @@ enum class Tune : int {
     kPartialsCpl,   // 1 | 2 | 4: bias-gradient partials' columns per lane
     kAttnScores,    // "0": the model's scores and dP through the batched product
                     // and the softmax passes (no fused scores + softmax)
+    kEmbScan,       // "0": the embedding backward's token rows through the sort
     kCount
 };
 

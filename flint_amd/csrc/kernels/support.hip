@@ -537,6 +537,151 @@ column_sums_one_chunk(float* __restrict__ out, const float* __restrict__ dy, int
     column_sums_quad(out, dy, rows, cols, accumulate, size_t(blockIdx.x) * 256 + threadIdx.x);
 }
 
+// ------------------------------------------------ token rows without a sort
+
+constexpr int kScanRows = 8192;   // tokens embedding_scan_runs holds in LDS
+constexpr int kScanWaves = 4;     // positions (one a wave) per workgroup
+constexpr int kScanThreads = kScanWaves * 64;
+constexpr int kScanBatch = 4;     // rows of a run whose loads go out together
+
+// The positions of one 512-position block of the scan that hold a token:
+// bit l of m[k] says whether lane l's position 8 l + k does. next() returns
+// them in ascending order (base + 8 l + k), then -1. Every member holds the
+// same value on all lanes.
+struct BlockMatches {
+    uint64_t m[8];
+    uint64_t lanes;   // lanes with a position not yet returned, but `at`
+    unsigned cur;     // positions k of lane `at` not yet returned
+    int at;
+    int base;
+    __device__ int next() {
+        if (cur == 0) {
+            if (lanes == 0) return -1;
+            at = __builtin_ctzll(lanes);
+            lanes &= lanes - 1;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) cur |= unsigned((m[k] >> at) & 1) << k;
+        }
+        const int k = __builtin_ctz(cur);
+        cur &= cur - 1;
+        return base + 8 * at + k;
+    }
+};
+
+// dwte += the token rows of dx without sorting them (up to kScanRows rows,
+// widths up to 256 G). The tokens sit in LDS, and wave w of workgroup b takes
+// position i = kScanWaves b + w. The wave scans the tokens in ascending
+// blocks of 512, lane l reading positions 8 l .. 8 l + 7 of a block as one
+// 16-byte word, so that lane order is position order. If the first block
+// holding the wave's token holds it before i, an earlier position's wave owns
+// the token and this one leaves. Otherwise i is the token's first position:
+// the wave adds the dx rows of i and of every later position with the same
+// token, in ascending order, kScanBatch rows' loads in flight at a time. That
+// is the run a stable sort puts together, summed as embedding_runs sums it
+// (compensated, in the same order), so the bits are the sorted path's. Lane l
+// holds columns 256 g + 4 l (g < G). Workgroups from run_blocks on take
+// column quads of the position gradient (column_sums_quad, as in
+// sort_tokens_and_positions).
+template <int G>
+__global__ void __launch_bounds__(kScanThreads)
+embedding_scan_runs(float* __restrict__ dwte, const float* __restrict__ dx,
+                    const uint16_t* __restrict__ tokens, int rows, size_t width,
+                    unsigned run_blocks, float* __restrict__ dwpe, int sequences, size_t cols,
+                    int accumulate_wpe) {
+    typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+    __shared__ __attribute__((aligned(16))) uint16_t tok[kScanRows];
+    if (blockIdx.x >= run_blocks) {
+        column_sums_quad(dwpe, dx, sequences, cols, accumulate_wpe,
+                         size_t(blockIdx.x - run_blocks) * kScanThreads + threadIdx.x);
+        return;
+    }
+    // The ABI's tokens are 16-byte aligned: whole words, then the last few.
+    const int words = rows / 8;
+    for (int q = int(threadIdx.x); q < words; q += kScanThreads)
+        reinterpret_cast<u4*>(tok)[q] = reinterpret_cast<const u4*>(tokens)[q];
+    for (int p = words * 8 + int(threadIdx.x); p < rows; p += kScanThreads) tok[p] = tokens[p];
+    __syncthreads();
+    const int lane = int(threadIdx.x & 63);
+    const size_t col0 = size_t(lane) * 4;
+    const int i = int(blockIdx.x) * kScanWaves + int(threadIdx.x >> 6);
+    if (i >= rows) return;
+    const uint16_t v = tok[i];
+    Comp s[G][4];
+    f4 old[G];
+    bool owner = false;
+    // Each block's word is read while the one before is tested. base + 8 lane
+    // + 7 < base + 512 <= kScanRows: the word stays inside tok; positions at
+    // or past rows are masked off.
+    u16x8 next = *reinterpret_cast<const u16x8*>(tok + 8 * lane);
+    for (int base = 0; base < rows; base += 512) {
+        const u16x8 t = next;
+        if (base + 512 < rows) next = *reinterpret_cast<const u16x8*>(tok + base + 512 + 8 * lane);
+        const int left = rows - base - 8 * lane;
+        BlockMatches bm;
+        bm.lanes = 0;
+        bm.cur = 0;
+        bm.at = 0;
+        bm.base = base;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) bm.m[k] = __builtin_amdgcn_ballot_w64(t[k] == v);
+        if (base + 512 > rows) {   // the last block: no match at or past rows
+#pragma unroll
+            for (int k = 0; k < 8; ++k) bm.m[k] &= __builtin_amdgcn_ballot_w64(k < left);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) bm.lanes |= bm.m[k];
+        if (bm.lanes == 0) continue;
+        if (!owner) {
+            BlockMatches first = bm;
+            if (first.next() < i) return;   // an earlier position holds the token
+            owner = true;
+            // The row the sums add into, loaded beside the first dx rows.
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const size_t col = col0 + size_t(g) * 256;
+                old[g] = col < width ? *reinterpret_cast<const f4*>(dwte + size_t(v) * width + col)
+                                     : f4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+        for (;;) {
+            int j[kScanBatch];
+#pragma unroll
+            for (int u = 0; u < kScanBatch; ++u) j[u] = bm.next();
+            f4 d[kScanBatch][G];
+#pragma unroll
+            for (int u = 0; u < kScanBatch; ++u)
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const size_t col = col0 + size_t(g) * 256;
+                    d[u][g] = j[u] >= 0 && col < width
+                                  ? *reinterpret_cast<const f4*>(dx + size_t(j[u]) * width + col)
+                                  : f4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+#pragma unroll
+            for (int u = 0; u < kScanBatch; ++u) {
+                if (j[u] < 0) break;
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) comp_add(s[g][c], d[u][g][c]);
+            }
+            if (j[kScanBatch - 1] < 0) break;
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const size_t col = col0 + size_t(g) * 256;
+        if (col >= width) continue;
+        f4 r;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            r[c] = add_rn(old[g][c], __builtin_isfinite(s[g][c].sum)
+                                         ? add_rn(s[g][c].sum, s[g][c].error)
+                                         : s[g][c].sum);
+        *reinterpret_cast<f4*>(dwte + size_t(v) * width + col) = r;
+    }
+}
+
 // The block sort and the position gradient in one launch: they are
 // independent, and the sort's one workgroup leaves the other CUs idle.
 // Workgroup 0 sorts; workgroup b > 0 takes column quads (b - 1) * 1024 + t of
@@ -636,6 +781,30 @@ size_t embedding_backward_workspace(size_t sequences, size_t length, size_t voca
     return emb_layout(sequences, length, vocab, width).bytes;
 }
 
+namespace {
+
+// dwpe: the column sums of dx viewed as sequences x cols (cols = length *
+// width), in the bias gradient's order; partials is the workspace's region for
+// more than one chunk of sequences.
+hipError_t launch_position_sums(void* dwpe, const void* dx, void* partials, size_t sequences,
+                                size_t cols, bool accumulate, hipStream_t stream) {
+    if (sequences <= 256) {
+        hipLaunchKernelGGL(column_sums_one_chunk, dim3(unsigned((cols / 4 + 255) / 256)),
+                           dim3(256), 0, stream, static_cast<float*>(dwpe),
+                           static_cast<const float*>(dx), int(sequences), cols,
+                           accumulate ? 1 : 0);
+        return hipGetLastError();
+    }
+    const dim3 pgrid(unsigned((cols / 8 + 7) / 8), unsigned((sequences + 255) / 256));
+    hipLaunchKernelGGL(column_partials_f32, pgrid, dim3(64), 0, stream,
+                       static_cast<float*>(partials), static_cast<const float*>(dx), sequences,
+                       cols);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    return launch_bias_gradient_finish(dwpe, partials, sequences, cols, accumulate, stream);
+}
+
+}  // namespace
+
 hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, const void* tokens,
                                      size_t sequences, size_t length, size_t vocab, size_t width,
                                      bool accumulate_wte, bool accumulate_wpe, void* workspace,
@@ -652,19 +821,46 @@ hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, con
     auto* offsets = reinterpret_cast<unsigned*>(ws + l.offsets);
     const auto* tok = static_cast<const uint16_t*>(tokens);
 
-    // Two stable passes of 8 bits: low byte into the pass buffers, high byte
-    // into the sorted buffers; in one workgroup's LDS when the rows fit.
     const size_t cols = length * width;   // dwpe: column sums of dx as sequences x cols
-    // With one chunk of sequences the position gradient rides in the sort's
-    // launch ("emb_together" = "0": its own launch after the token rows).
+    // With one chunk of sequences the position gradient rides in the token
+    // rows' launch ("emb_together" = "0": its own launch after them).
     const bool together = rows <= size_t(kBlockSortRows) && sequences <= 256 &&
                           (cols / 4 + 1023) / 1024 < (size_t{1} << 30) &&
                           !tuning_off(Tune::kEmbTogether);
+    const unsigned pos_blocks = together ? unsigned((cols / 4 + 1023) / 1024) : 0u;
+    const size_t scan_pos_blocks = together ? (cols / 4 + kScanThreads - 1) / kScanThreads : 0;
+    // Accumulating into dwte, with the tokens in one workgroup's LDS: the
+    // token rows without a sort ("emb_scan" = "0": the sorted path).
+    const size_t groups = (width + 255) / 256;
+    const size_t run_blocks = (rows + kScanWaves - 1) / kScanWaves;
+    if (accumulate_wte && rows <= size_t(kScanRows) && groups <= 4 &&
+        run_blocks + scan_pos_blocks < (size_t{1} << 31) && !tuning_off(Tune::kEmbScan)) {
+        const dim3 grid(unsigned(run_blocks + scan_pos_blocks));
+        auto scan = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, grid, dim3(kScanThreads), 0, stream, static_cast<float*>(dwte),
+                               static_cast<const float*>(dx), tok, int(rows), width,
+                               unsigned(run_blocks),
+                               static_cast<float*>(dwpe), int(sequences), cols,
+                               accumulate_wpe ? 1 : 0);
+        };
+        switch (groups) {
+        case 1: scan(embedding_scan_runs<1>); break;
+        case 2: scan(embedding_scan_runs<2>); break;
+        case 3: scan(embedding_scan_runs<3>); break;
+        default: scan(embedding_scan_runs<4>); break;
+        }
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+        if (together) return hipSuccess;
+        return launch_position_sums(dwpe, dx, ws + l.partials, sequences, cols, accumulate_wpe,
+                                    stream);
+    }
+    // Two stable passes of 8 bits: low byte into the pass buffers, high byte
+    // into the sorted buffers; in one workgroup's LDS when the rows fit.
     if (together) {
-        hipLaunchKernelGGL(sort_tokens_and_positions, dim3(unsigned(1 + (cols / 4 + 1023) / 1024)),
-                           dim3(1024), 0, stream, sorted_tokens, sorted_rows, tok, int(rows),
-                           static_cast<float*>(dwpe), static_cast<const float*>(dx),
-                           int(sequences), cols, accumulate_wpe ? 1 : 0);
+        hipLaunchKernelGGL(sort_tokens_and_positions, dim3(1 + pos_blocks), dim3(1024), 0, stream,
+                           sorted_tokens, sorted_rows, tok, int(rows), static_cast<float*>(dwpe),
+                           static_cast<const float*>(dx), int(sequences), cols,
+                           accumulate_wpe ? 1 : 0);
     } else if (rows <= size_t(kBlockSortRows)) {
         hipLaunchKernelGGL(sort_tokens_block, dim3(1), dim3(1024), 0, stream, sorted_tokens,
                            sorted_rows, tok, int(rows));
@@ -698,22 +894,9 @@ hipError_t launch_embedding_backward(void* dwte, void* dwpe, const void* dx, con
                            accumulate_wte ? 1 : 0);
     }
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    // dwpe: column sums of dx viewed as sequences x (length * width).
     if (together) return hipSuccess;
-    if (sequences <= 256) {
-        hipLaunchKernelGGL(column_sums_one_chunk, dim3(unsigned((cols / 4 + 255) / 256)),
-                           dim3(256), 0, stream, static_cast<float*>(dwpe),
-                           static_cast<const float*>(dx), int(sequences), cols,
-                           accumulate_wpe ? 1 : 0);
-        return hipGetLastError();
-    }
-    const dim3 pgrid(unsigned((cols / 8 + 7) / 8), unsigned((sequences + 255) / 256));
-    hipLaunchKernelGGL(column_partials_f32, pgrid, dim3(64), 0, stream,
-                       reinterpret_cast<float*>(ws + l.partials), static_cast<const float*>(dx),
-                       sequences, cols);
-    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    return launch_bias_gradient_finish(dwpe, ws + l.partials, sequences, cols, accumulate_wpe,
-                                       stream);
+    return launch_position_sums(dwpe, dx, ws + l.partials, sequences, cols, accumulate_wpe,
+                                stream);
 }
 
 }  // namespace flint

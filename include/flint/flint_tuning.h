@@ -12,7 +12,7 @@
  *   "gemm_config"   "bm,bn,bk,stages,waves_m[,waves]" (the non-pipeline kernel)
  *   "gemm_group_m", "gemm_slots"   positive integers (the non-pipeline kernel)
  *   "attn_causal", "fused_grads", "fused_sums", "ln_defer", "ln_fused",
- *   "emb_together", "attn_order", "attn_scores"   "0" selects the alternative plan
+ *   "emb_together", "attn_order", "attn_scores", "emb_scan"   "0" selects the alternative plan
  *   "ce_threads"    "256", "512" or "1024"
  *   "partials_cpl"  "1", "2" or "4"
  * A value the plan cannot use leaves its default in place. Set and clear

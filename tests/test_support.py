@@ -51,11 +51,13 @@ def test_embedding_forward_matches_pytorch_bitwise(flint, cuda, sequences, lengt
     (2, 1500, 5000, 16, "zipf"), (4, 256, 65536, 8, "uniform"), (9, 16, 300, 16, "zipf"),
     (300, 8, 100, 8, "uniform"), (3, 4000, 65536, 8, "uniform"), (5, 1700, 3000, 8, "zipf")])
 @pytest.mark.parametrize("accumulate", [False, True])
-@pytest.mark.parametrize("together", ["1", "0"])   # position sums in the sort's launch, or after
-def test_embedding_backward_matches_the_oracle_bitwise(flint, cuda, tune, together,
+@pytest.mark.parametrize("together", ["1", "0"])   # position sums in the token rows' launch, or after
+@pytest.mark.parametrize("scan", ["1", "0"])       # token rows by the scan (accumulating), or sorted
+def test_embedding_backward_matches_the_oracle_bitwise(flint, cuda, tune, together, scan,
                                                        sequences, length, vocab,
                                                        width, kind, accumulate):
     tune("emb_together", together)
+    tune("emb_scan", scan)
     rows = sequences * length
     g = torch.Generator().manual_seed(4)
     if kind == "uniform":
@@ -87,6 +89,28 @@ def test_embedding_backward_matches_the_oracle_bitwise(flint, cuda, tune, togeth
     if accumulate:
         ref += old_wte.double()
     assert torch.allclose(dwte.cpu().double(), ref, rtol=1e-6, atol=1e-3)
+
+
+@pytest.mark.parametrize("sequences,length", [(3, 700), (1, 13), (5, 1637)])
+def test_embedding_backward_rows_past_whole_words(flint, cuda, sequences, length):
+    """Row counts that are not a multiple of 8 (the sort-free path reads the
+    tokens in 16-byte words and the last few one by one, and masks the scan's
+    last block at the row count): the oracle's bits."""
+    vocab, width = 300, 24
+    rows = sequences * length
+    g = torch.Generator().manual_seed(12)
+    tok = torch.randint(0, vocab, (rows,), generator=g)
+    tok[-1] = tok[0]   # a run that ends at the last row
+    dx = normal((rows, width), 13)
+    old_wte, old_wpe = normal((vocab, width), 14), normal((length, width), 15)
+    dwte, dwpe = old_wte.clone().to(cuda), old_wpe.clone().to(cuda)
+    flint.embedding_backward(dwte, dwpe, dx.to(cuda), tok.to(torch.int16).to(cuda), sequences,
+                             length, vocab, width, accumulate_wte=True, accumulate_wpe=True)
+    torch.cuda.synchronize()
+    ewte, ewpe = oracle.embedding_backward(dx.numpy(), tok.numpy().astype(np.uint16), sequences,
+                                           length, vocab, width, old_wte.numpy(), old_wpe.numpy())
+    assert np.array_equal(dwte.cpu().numpy().view(np.int32), ewte.view(np.int32))
+    assert np.array_equal(dwpe.cpu().numpy().view(np.int32), ewpe.view(np.int32))
 
 
 def test_embedding_backward_at_gpt2_shape_against_fp64(flint, cuda):
