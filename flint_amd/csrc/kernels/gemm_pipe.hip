@@ -962,7 +962,8 @@ struct PipeConfig {
 constexpr PipeConfig kPipeConfigs[] = {
     {256, 256, 3, 32}, {256, 192, 4, 32}, {128, 192, 4, 32}, {256, 64, 4, 32},
     {128, 192, 3, 64}, {256, 128, 3, 64}, {256, 256, 2, 64}, {256, 192, 2, 64},
-    {256, 192, 2, 64, 8}, {128, 192, 3, 64, 4, 1}, {256, 128, 3, 64, 4, 1}, {128, 64, 4, 32}};
+    {256, 192, 2, 64, 8}, {128, 192, 3, 64, 4, 1}, {256, 128, 3, 64, 4, 1}, {128, 64, 4, 32},
+    {128, 64, 3, 64}};
 
 // The "gemm_pipe" override: "0" routes every call to gemm.hip's kernels;
 // "bm,bn,stages[,bk[,waves[,loaders]]]" forces one of kPipeConfigs (tests and
@@ -1045,7 +1046,10 @@ double pipe_eff(const PipeConfig& c, Store st, Layout l) {
     // an epilogue (MLP up + GELU 53.9 -> 58.1 us). pick_pipe admits it only
     // for plain NT products of at least kPipe8MinRounds rounds.
     if (c.waves == 8) return 1.04;
-    if (c.bn == 64) return 0.55;
+    // 64 wide: 64-deep steps for the causal attention products (their 128 x
+    // 64 tiles; the default model's training step 13.36 -> 13.07 ms against
+    // 32-deep steps, same process, the same bits).
+    if (c.bn == 64) return c.bk == 64 ? 0.56 : 0.55;
     // Two stages: worth it for 256 x 192 outside TN (MLP up 59 -> 56 us,
     // dGELU 77 -> 74 us); 256 x 256 measured no better than at 32-deep steps.
     if (c.stages == 2)
@@ -1183,6 +1187,7 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     FLINT_PIPE_CASE(128, 192, 4, 32, 4, 0)
     FLINT_PIPE_CASE(256, 64, 4, 32, 4, 0)
     FLINT_PIPE_CASE(128, 64, 4, 32, 4, 0)
+    FLINT_PIPE_CASE(128, 64, 3, 64, 4, 0)
     FLINT_PIPE_CASE(128, 192, 3, 64, 4, 0)
     FLINT_PIPE_CASE(256, 128, 3, 64, 4, 0)
     FLINT_PIPE_CASE(256, 256, 2, 64, 4, 0)

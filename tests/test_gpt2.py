@@ -265,7 +265,7 @@ def test_run_twice_and_separate_buffers_give_the_same_bits(flint, cuda):
 
 
 @pytest.mark.parametrize("length", [1024, 320])
-@pytest.mark.parametrize("force", [None, "128,192,3,64", "256,128,3,64", "256,256,3"])
+@pytest.mark.parametrize("force", [None, "128,64,4", "128,192,3,64", "256,128,3,64", "256,256,3"])
 def test_causal_attention_products_change_no_bits(flint, cuda, tune, length, force):
     """The attention GEMMs skip the tiles and k-ranges above the diagonal
     (FLINT_ATTN_CAUSAL unset); computing everything (=0) must give the same
