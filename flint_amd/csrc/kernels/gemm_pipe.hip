@@ -963,7 +963,7 @@ constexpr PipeConfig kPipeConfigs[] = {
     {256, 256, 3, 32}, {256, 192, 4, 32}, {128, 192, 4, 32}, {256, 64, 4, 32},
     {128, 192, 3, 64}, {256, 128, 3, 64}, {256, 256, 2, 64}, {256, 192, 2, 64},
     {256, 192, 2, 64, 8}, {128, 192, 3, 64, 4, 1}, {256, 128, 3, 64, 4, 1}, {128, 64, 4, 32},
-    {128, 64, 3, 64}};
+    {128, 64, 3, 64}, {256, 64, 3, 64}};
 
 // The "gemm_pipe" override: "0" routes every call to gemm.hip's kernels;
 // "bm,bn,stages[,bk[,waves[,loaders]]]" forces one of kPipeConfigs (tests and
@@ -1046,9 +1046,10 @@ double pipe_eff(const PipeConfig& c, Store st, Layout l) {
     // an epilogue (MLP up + GELU 53.9 -> 58.1 us). pick_pipe admits it only
     // for plain NT products of at least kPipe8MinRounds rounds.
     if (c.waves == 8) return 1.04;
-    // 64 wide: 64-deep steps for the causal attention products (their 128 x
-    // 64 tiles; the default model's training step 13.36 -> 13.07 ms against
-    // 32-deep steps, same process, the same bits).
+    // 64 wide: 64-deep steps, whole 128-byte lines a load (the causal
+    // attention products' 128 x 64 tiles: the default model's training step
+    // 13.36 -> 13.07 ms; the full batched NN 96 x 1024 x 64 x 1024 at 256 x
+    // 64: 53.1 -> 41.9 us, TN the same; same process, the same bits).
     if (c.bn == 64) return c.bk == 64 ? 0.56 : 0.55;
     // Two stages: worth it for 256 x 192 outside TN (MLP up 59 -> 56 us,
     // dGELU 77 -> 74 us); 256 x 256 measured no better than at 32-deep steps.
@@ -1188,6 +1189,7 @@ hipError_t launch_pipe(const PipeConfig& c, const Operands& op, size_t slices, i
     FLINT_PIPE_CASE(256, 64, 4, 32, 4, 0)
     FLINT_PIPE_CASE(128, 64, 4, 32, 4, 0)
     FLINT_PIPE_CASE(128, 64, 3, 64, 4, 0)
+    FLINT_PIPE_CASE(256, 64, 3, 64, 4, 0)
     FLINT_PIPE_CASE(128, 192, 3, 64, 4, 0)
     FLINT_PIPE_CASE(256, 128, 3, 64, 4, 0)
     FLINT_PIPE_CASE(256, 256, 2, 64, 4, 0)

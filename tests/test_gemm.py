@@ -268,7 +268,7 @@ def test_deterministic(flint, cuda):
 # then walks several, the next one's loads streaming under this one's stores).
 PIPE_CONFIGS = ["256,256,3", "256,192,4", "128,192,4", "256,64,4", "128,64,4", "128,192,3,64",
                 "256,128,3,64", "256,256,2,64", "256,192,2,64", "128,192,3,64,4,1",
-                "256,128,3,64,4,1", "128,64,3,64"]
+                "256,128,3,64,4,1", "128,64,3,64", "256,64,3,64"]
 PIPE_SHAPES = [(300, 200, 64), (4315, 4600, 96), (1100, 968, 448)]
 # The NT layout also has an 8-wave configuration (two waves per SIMD).
 NT_PIPE_CONFIGS = PIPE_CONFIGS + ["256,192,2,64,8"]
