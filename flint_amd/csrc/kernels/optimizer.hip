@@ -177,18 +177,27 @@ __global__ void __launch_bounds__(kThreads) adamw_update(AdamwGroup group, const
     const unsigned long long end = begin + kAdamwChunk < t.n ? begin + kAdamwChunk : t.n;
     if (end - begin == kAdamwChunk) {
         // A whole chunk in rounds of 4 float4s a thread, each round's loads
-        // issued before its arithmetic.
+        // issued before its arithmetic. param, m and v are read and written
+        // once a step, so they stream (non-temporal); the gradient, which the
+        // norm pass read just before, is read as usual.
+        typedef float f4v __attribute__((ext_vector_type(4)));
         constexpr int kPer = int(kAdamwChunk / (4 * kThreads)), kRound = 4;
+        auto load_nt = [](const float* q) {
+            return __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const f4v*>(q)));
+        };
+        auto store_nt = [](float* q, const float4& x) {
+            __builtin_nontemporal_store(__builtin_bit_cast(f4v, x), reinterpret_cast<f4v*>(q));
+        };
 #pragma unroll
         for (int r0 = 0; r0 < kPer; r0 += kRound) {
             float4 p[kRound], g[kRound], m[kRound], v[kRound];
 #pragma unroll
             for (int k = 0; k < kRound; ++k) {
                 const unsigned long long e = begin + 4ull * threadIdx.x + 4ull * kThreads * (r0 + k);
-                p[k] = *reinterpret_cast<const float4*>(t.p + e);
+                p[k] = load_nt(t.p + e);
                 g[k] = *reinterpret_cast<const float4*>(t.g + e);
-                m[k] = *reinterpret_cast<const float4*>(t.m + e);
-                v[k] = *reinterpret_cast<const float4*>(t.v + e);
+                m[k] = load_nt(t.m + e);
+                v[k] = load_nt(t.v + e);
             }
 #pragma unroll
             for (int k = 0; k < kRound; ++k) {
@@ -197,9 +206,9 @@ __global__ void __launch_bounds__(kThreads) adamw_update(AdamwGroup group, const
                 adamw_element(p[k].y, g[k].y, m[k].y, v[k].y, t.decay, d, mo);
                 adamw_element(p[k].z, g[k].z, m[k].z, v[k].z, t.decay, d, mo);
                 adamw_element(p[k].w, g[k].w, m[k].w, v[k].w, t.decay, d, mo);
-                *reinterpret_cast<float4*>(t.p + e) = p[k];
-                *reinterpret_cast<float4*>(t.m + e) = m[k];
-                *reinterpret_cast<float4*>(t.v + e) = v[k];
+                store_nt(t.p + e, p[k]);
+                store_nt(t.m + e, m[k]);
+                store_nt(t.v + e, v[k]);
                 if (t.h) {
                     __half2* h = reinterpret_cast<__half2*>(t.h + e);
                     h[0] = __floats2half2_rn(p[k].x, p[k].y);
