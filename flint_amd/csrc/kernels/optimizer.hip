@@ -177,10 +177,13 @@ __global__ void __launch_bounds__(kThreads) adamw_update(AdamwGroup group, const
     const unsigned long long end = begin + kAdamwChunk < t.n ? begin + kAdamwChunk : t.n;
     if (end - begin == kAdamwChunk) {
         // A whole chunk in rounds of 4 float4s a thread, each round's loads
-        // issued before its arithmetic. param, m and v are read and written
-        // once a step, so they stream (non-temporal); the gradient, which the
-        // norm pass read just before, is read as usual.
+        // issued before its arithmetic. Every access streams (non-temporal):
+        // param, m and v are touched once a step, this is the gradient's last
+        // read, and the FP16 copy waits for the next forward. The FP16 pairs
+        // go out as one 8-byte store (buffers are 16-byte aligned, e is a
+        // multiple of 4).
         typedef float f4v __attribute__((ext_vector_type(4)));
+        typedef unsigned u2v __attribute__((ext_vector_type(2)));
         constexpr int kPer = int(kAdamwChunk / (4 * kThreads)), kRound = 4;
         auto load_nt = [](const float* q) {
             return __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const f4v*>(q)));
@@ -195,7 +198,7 @@ __global__ void __launch_bounds__(kThreads) adamw_update(AdamwGroup group, const
             for (int k = 0; k < kRound; ++k) {
                 const unsigned long long e = begin + 4ull * threadIdx.x + 4ull * kThreads * (r0 + k);
                 p[k] = load_nt(t.p + e);
-                g[k] = *reinterpret_cast<const float4*>(t.g + e);
+                g[k] = load_nt(t.g + e);
                 m[k] = load_nt(t.m + e);
                 v[k] = load_nt(t.v + e);
             }
@@ -210,9 +213,9 @@ __global__ void __launch_bounds__(kThreads) adamw_update(AdamwGroup group, const
                 store_nt(t.m + e, m[k]);
                 store_nt(t.v + e, v[k]);
                 if (t.h) {
-                    __half2* h = reinterpret_cast<__half2*>(t.h + e);
-                    h[0] = __floats2half2_rn(p[k].x, p[k].y);
-                    h[1] = __floats2half2_rn(p[k].z, p[k].w);
+                    const u2v h = {__builtin_bit_cast(unsigned, __floats2half2_rn(p[k].x, p[k].y)),
+                                   __builtin_bit_cast(unsigned, __floats2half2_rn(p[k].z, p[k].w))};
+                    __builtin_nontemporal_store(h, reinterpret_cast<u2v*>(t.h + e));
                 }
             }
         }
